@@ -1,0 +1,223 @@
+"""Benchmark of the MI355X MoE layer (libmoe_hip) — one JSON line on stdout.
+
+Headline workload: the large imbalanced prefill layer — T=16384 tokens,
+d_model=2048, d_ff=8192, E=64 experts, top-4, Zipf-skewed router bias,
+inputs N(0,1), weights N(0,0.02), all fp32, synthetic and resident in HBM
+before the timed region.  A "step" is one full layer forward (route,
+dispatch, gate/up GEMM, down GEMM, combine).
+
+Also measured in the same run:
+  * decode: 64 sequences x 1 token through 8 MoE layers of d=512, d_ff=2048,
+    E=16, top-2 (8 layers' weights, 1.6 GB, so the 256 MB last-level cache
+    cannot hold them), reported as MoE decode tokens/s and HBM GB/s;
+  * cpu_baseline: the CPU oracle (a restatement of the reference's
+    moe_forward, bit-identical routing) on a bounded token sample of the same
+    prefill workload, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "llm.c_amd"))
+
+METRIC = "MoE layer tokens/s + % fp32 MFMA peak (prefill); decode tok/s + HBM GB/s"
+PEAK_FP32_MFMA_TFLOPS = 157.3      # MI355X dense fp32 matrix
+PEAK_HBM_GBS = 8000.0              # MI355X HBM3E
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def prefill(mh, steps, warmup, T=16384, d=2048, F=8192, E=64, k=4, seed=5):
+    layer = mh.Layer(d, F, E, k)
+    t0 = time.time()
+    layer.fill_synthetic(seed, 0.02, 0.02)
+    bias_path = os.path.join(ROOT, "tests", "golden", "zipf_bias_e64_k4.npy")
+    bias = None
+    if os.path.exists(bias_path):
+        bias = np.load(bias_path).astype(np.float32)
+        layer.set_bias(bias)
+    x = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(x.ptr, T * d, seed, 0, 0.0, 1.0)
+    out = mh.DeviceArray((T, d))
+    probs = mh.DeviceArray((T, E))
+    ids = mh.DeviceArray((T, k), np.int32)
+    mh.synchronize()
+    log(f"prefill setup {time.time() - t0:.1f}s (weights {3 * E * d * F * 4 / 1e9:.2f} GB)")
+
+    mh.set_timing(True)
+    for _ in range(warmup):
+        layer.forward_dev(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
+        mh.last_timings()
+    mh.synchronize()
+    phase = np.zeros(5)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        layer.forward_dev(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
+        phase += np.array(mh.last_timings())
+    mh.synchronize()
+    wall = time.perf_counter() - t0
+    mh.set_timing(False)
+    phase /= steps
+    ms = wall * 1e3 / steps
+    counts = np.bincount(ids.to_host().ravel(), minlength=E)
+    flops_gu = 4.0 * T * k * d * F
+    flops_dn = 2.0 * T * k * d * F
+    flops_layer = 6.0 * T * k * d * F + 2.0 * T * d * E
+    res = dict(T=T, d=d, F=F, E=E, k=k, ms=ms, phase_ms=phase.tolist(),
+               counts_max_over_mean=float(counts.max() / counts.mean()),
+               gateup_tflops=flops_gu / (phase[2] * 1e-3) / 1e12,
+               down_tflops=flops_dn / (phase[3] * 1e-3) / 1e12,
+               layer_tflops=flops_layer / (ms * 1e-3) / 1e12,
+               bias=bias is not None)
+    state = dict(layer=layer, x=x, bias=bias, ids=ids.to_host(), seed=seed)
+    return res, state
+
+
+def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
+    layers = []
+    for li in range(n_layers):
+        L = mh.Layer(d, F, E, k)
+        L.fill_synthetic(100 + li, 0.02, 0.02)
+        layers.append(L)
+    xn = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(xn.ptr, T * d, 99, 0, 0.0, 1.0)
+    x = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(x.ptr, T * d, 99, 2, 0.0, 1.0)
+    ids = [mh.DeviceArray((T, k), np.int32) for _ in range(n_layers)]
+    mh.synchronize()
+    mh.set_timing(True)
+    for _ in range(warmup):
+        for li, L in enumerate(layers):
+            L.forward_dev(xn.ptr, T, x.ptr, None, ids[li].ptr, accumulate=1)
+            mh.last_timings()
+    mh.synchronize()
+    phase = np.zeros(5)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for li, L in enumerate(layers):
+            L.forward_dev(xn.ptr, T, x.ptr, None, ids[li].ptr, accumulate=1)
+            phase += np.array(mh.last_timings())
+    mh.synchronize()
+    wall = time.perf_counter() - t0
+    mh.set_timing(False)
+    phase /= steps * n_layers
+    ms_step = wall * 1e3 / steps
+    used = [int((np.bincount(i.to_host().ravel(), minlength=E) > 0).sum()) for i in ids]
+    bytes_layer = [4.0 * (3 * d * F * u + d * E + 2 * T * d) for u in used]
+    bytes_gu = [4.0 * 2 * d * F * u for u in used]
+    dev_ms_layer = float(phase.sum())
+    res = dict(layers=n_layers, T=T, d=d, F=F, E=E, k=k, ms_per_step=ms_step,
+               tokens_per_s=T / (ms_step * 1e-3),
+               device_ms_per_layer=dev_ms_layer, phase_ms=phase.tolist(),
+               experts_used=used,
+               hbm_gbs_layer=float(np.mean(bytes_layer)) / (dev_ms_layer * 1e-3) / 1e9,
+               hbm_gbs_step=float(np.sum(bytes_layer)) / (ms_step * 1e-3) / 1e9,
+               gateup_gbs=float(np.mean(bytes_gu)) / (phase[2] * 1e-3) / 1e9)
+    for L in layers:
+        L.close()
+    return res
+
+
+def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, budget_s=15.0):
+    """Oracle moe_forward on the first tokens of the prefill workload, all
+    host cores, until ~budget_s of CPU work; tokens/s extrapolates linearly
+    (tokens are independent in the reference loop, src/transformer.c:312)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import orc
+    layer, ids = st["layer"], st["ids"]
+    wr = layer.get_router()
+    xh = st["x"].to_host()
+    threads = os.cpu_count() or 1
+    ex = {}
+    done, secs = 0, 0.0
+    chunk = max(threads, 16)
+    while secs < budget_s and done < T:
+        rows = slice(done, min(T, done + chunk))
+        for e in sorted(set(ids[rows].ravel().tolist()) - set(ex)):
+            ex[e] = layer.get_expert(e)
+        xs = np.ascontiguousarray(xh[rows])
+        t0 = time.perf_counter()
+        orc.moe_forward_experts(xs, wr, ex, d, F, E, k, st["bias"], nthreads=threads)
+        secs += time.perf_counter() - t0
+        done = rows.stop
+    return dict(value=done / secs, unit="tokens/s", cores=threads, kind="port",
+                sample=f"first {done} of {T} tokens of the same prefill layer "
+                       f"({secs:.1f} s of oracle time, {threads} threads)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part "
+                                   "of it (see the sharding design notes)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import moe_hip as mh
+    mh.check(mh.lib().moe_hip_init(0))
+
+    pre, st = prefill(mh, args.steps, args.warmup)
+    log("prefill", json.dumps(pre))
+    dec = None
+    if not args.no_decode:
+        dec = decode(mh, args.steps, args.warmup)
+        log("decode", json.dumps(dec))
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(mh, st)
+        log("cpu", json.dumps(cpu))
+
+    ms = pre["ms"]
+    gu_tflops = pre["gateup_tflops"]
+    line = {
+        "metric": METRIC,
+        "value": pre["T"] / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "moe prefill layer T=16384 d=2048 d_ff=8192 E=64 top-4 "
+                               "Zipf(1.1)-biased router", "T": pre["T"], "d_model": pre["d"],
+                   "d_ff": pre["F"], "n_experts": pre["E"], "top_k": pre["k"]},
+        "roofline": {"bound": "mfma", "kernel": "grouped gate/up GEMM",
+                     "achieved": gu_tflops, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": gu_tflops / PEAK_FP32_MFMA_TFLOPS, "traffic": None},
+        "layer_mfma_frac": pre["layer_tflops"] / PEAK_FP32_MFMA_TFLOPS,
+        "prefill_phase_ms": dict(zip(["route", "dispatch", "gate_up", "down", "combine"],
+                                     pre["phase_ms"])),
+        "expert_load_max_over_mean": pre["counts_max_over_mean"],
+        "cpu_baseline": cpu,
+    }
+    if dec:
+        line["decode"] = {
+            "workload": "64 seqs x 1 token, 8 MoE layers d=512 d_ff=2048 E=16 top-2",
+            "tokens_per_s": dec["tokens_per_s"], "ms_per_step": dec["ms_per_step"],
+            "device_ms_per_layer": dec["device_ms_per_layer"],
+            "hbm_gbs": dec["hbm_gbs_layer"], "hbm_frac": dec["hbm_gbs_layer"] / PEAK_HBM_GBS,
+            "gateup_gbs": dec["gateup_gbs"], "phase_ms_per_layer": dict(zip(
+                ["route", "dispatch", "gate_up", "down", "combine"], dec["phase_ms"])),
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,211 @@
+/*
+ * moe_hip.h — C ABI of libmoe_hip, the MI355X (gfx950) mixture-of-experts
+ * layer that drops into murderface-cpu/llm.c.
+ *
+ * Reference interfaces this library replaces or extends (paths relative to
+ * the reference repo root):
+ *   moe_forward        include/transformer.h:270-272, src/transformer.c:287-366
+ *                      (caller: block_forward, src/transformer.c:761-764)
+ *   moe_decode_step    the empty MoE branch of inference_step,
+ *                      src/inference.c:342-343 (x += MoE(x_norm), one row)
+ *   moe_decode_batch   the same for n rows at once (the reference decodes one
+ *                      sequence per inference_step call, src/inference.c:231)
+ * Struct layouts are byte-compatible with include/matrix.h:33-38,
+ * include/transformer.h:35-58,108-124 and include/config.h:23-48.  If the
+ * reference headers are included first, their definitions are used.
+ *
+ * Threading: one process-wide HIP stream; calls are serialised by the caller
+ * (the reference calls moe_forward from one thread, src/train.c:467-476).
+ */
+#ifndef MOE_HIP_H
+#define MOE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if !defined(LLM_MATRIX_H)
+/* include/matrix.h:33-38 */
+typedef struct {
+    float *data;
+    float *grad;
+    int    rows;
+    int    cols;
+} Matrix;
+#endif
+
+#if !defined(LLM_CONFIG_H)
+/* include/config.h:23-48 */
+typedef struct {
+    int vocab_size;
+    int max_seq_len;
+    int d_model;
+    int n_layers;
+    int n_heads;
+    int n_kv_heads;
+    int head_dim;
+    int window_size;
+    int ffn_hidden;
+    int n_experts;
+    int top_k_experts;
+    float rms_norm_eps;
+    float rope_theta;
+} ModelConfig;
+#endif
+
+#if !defined(LLM_TRANSFORMER_H)
+/* include/transformer.h:35-39 */
+typedef struct {
+    Matrix W_gate;   /* [d_model x ffn_hidden] */
+    Matrix W_up;     /* [d_model x ffn_hidden] */
+    Matrix W_down;   /* [ffn_hidden x d_model] */
+} FFNWeights;
+
+/* include/transformer.h:53-58 */
+typedef struct {
+    FFNWeights *experts;   /* [n_experts] */
+    Matrix      W_router;  /* [d_model x n_experts] */
+    int         n_experts;
+    int         top_k;
+} MoEWeights;
+
+/* include/transformer.h:108-124 */
+typedef struct {
+    Matrix x_norm_attn, x_norm_ffn, attn_out, ffn_out;
+    Matrix Q, K, V;
+    Matrix attn_scores, attn_weighted;
+    Matrix gate_buf, up_buf;
+    float *router_probs;   /* [seq_len x n_experts] */
+    int   *expert_ids;     /* [seq_len x top_k]     */
+} ForwardCache;
+#endif
+
+/* ---------------------------------------------------------------------------
+ * Status codes (moe_hip_last_error / status-returning entry points)
+ * ------------------------------------------------------------------------- */
+enum {
+    MOE_HIP_OK = 0,
+    MOE_HIP_ERR_ARG = 1,          /* bad shape / null pointer / top_k > n_experts */
+    MOE_HIP_ERR_UNSUPPORTED = 2,  /* shape outside the kernels' constraints       */
+    MOE_HIP_ERR_HIP = 3,          /* a HIP runtime call failed                    */
+    MOE_HIP_ERR_NOMEM = 4,        /* device allocation failed                     */
+    MOE_HIP_ERR_NODEV = 5         /* no usable GPU                                */
+};
+
+/* ---------------------------------------------------------------------------
+ * Drop-in entry points (host pointers, synchronous at return)
+ * ------------------------------------------------------------------------- */
+
+/* Replaces moe_forward (include/transformer.h:270-272).  Overwrites out
+ * [x->rows x d_model], writes cache->router_probs [T x E] and
+ * cache->expert_ids [T x top_k].  Weights are uploaded on first use and kept
+ * resident, keyed by the MoEWeights address and every matrix data pointer;
+ * call moe_hip_invalidate() after changing weight values in place.
+ * On error it prints the reason and aborts, as the reference does on OOM
+ * (src/matrix.c:148-158). */
+void moe_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg,
+                 ForwardCache *cache, Matrix *out);
+
+/* moe_forward with a status code instead of abort. */
+int moe_hip_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg,
+                    ForwardCache *cache, Matrix *out);
+
+/* Fills the MoE slot of inference_step (src/inference.c:342-343) for one row:
+ * x[0:d] += MoE(x_norm[0:d]).  Aborts on error. */
+void moe_decode_step(const MoEWeights *w, const ModelConfig *cfg,
+                     const float *x_norm, float *x);
+
+/* Batched decode extension: x[r] += MoE(x_norm[r]) for r < n_rows (one new
+ * token for each of n_rows sequences).  Returns a status code. */
+int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg,
+                     const float *x_norm, int n_rows, float *x);
+
+/* ---------------------------------------------------------------------------
+ * Library state and residency
+ * ------------------------------------------------------------------------- */
+int  moe_hip_init(int device);          /* optional; first call does it      */
+void moe_hip_shutdown(void);            /* frees every resident buffer       */
+int  moe_hip_invalidate(const MoEWeights *w);  /* drop w's device copy       */
+int  moe_hip_last_error(void);
+const char *moe_hip_error_string(int code);
+const char *moe_hip_last_error_message(void);
+
+/* ---------------------------------------------------------------------------
+ * Device-resident API: weights packed on the GPU, activations in device
+ * memory, work queued on `stream` (a hipStream_t; NULL = the library stream)
+ * and NOT synchronised.  Used by callers whose residual stream already lives
+ * on the GPU, by the benchmark and by the parity tests.
+ * ------------------------------------------------------------------------- */
+typedef struct MoeHipLayer MoeHipLayer;
+
+int moe_hip_layer_create(int d_model, int ffn_hidden, int n_experts, int top_k,
+                         MoeHipLayer **layer);
+int moe_hip_layer_destroy(MoeHipLayer *layer);
+
+/* Upload host weights (reference layout) and pack them. */
+int moe_hip_layer_load(MoeHipLayer *layer, const MoEWeights *w);
+
+/* Router bias b[E] added to the logits after the product, as mat_mul_add
+ * (src/matrix.c:418-439) does; NULL clears it.  The reference MoE has no
+ * router bias (src/transformer.c:299-300): zero bias = reference semantics. */
+int moe_hip_layer_set_router_bias(MoeHipLayer *layer, const float *bias);
+
+/* Deterministic synthetic weights generated on the device: W_router ~
+ * N(0, std_router), experts ~ N(0, std_expert), streams: router 1, expert e
+ * gate 16+3e, up 17+3e, down 18+3e (flat row-major index in each). */
+int moe_hip_layer_fill_synthetic(MoeHipLayer *layer, uint64_t seed,
+                                 float std_router, float std_expert);
+
+/* Copy expert e back to host in the reference layout (any pointer may be
+ * NULL): wg, wu [d x F], wd [F x d]; wr [d x E] via moe_hip_layer_get_router. */
+int moe_hip_layer_get_expert(MoeHipLayer *layer, int e, float *wg, float *wu,
+                             float *wd);
+int moe_hip_layer_get_router(MoeHipLayer *layer, float *wr);
+
+/* Full layer on device buffers: x [T x d] -> out [T x d] (overwritten);
+ * probs [T x E] and ids [T x top_k] are optional (NULL = not written).
+ * accumulate != 0 adds into out instead (x += MoE(x_norm) decode form). */
+int moe_hip_forward_dev(MoeHipLayer *layer, const float *x, int T, float *out,
+                        float *probs, int *ids, int accumulate, void *stream);
+
+/* Routing and dispatch only: probs [T x E], ids [T x k], gate weights
+ * gw [T x k] (renormalised), counts [E], offsets [E+1], perm [T x k]
+ * (perm[pos] = t*k + slot, stable by expert).  Any output may be NULL. */
+int moe_hip_route_dev(MoeHipLayer *layer, const float *x, int T, float *probs,
+                      int *ids, float *gw, int *counts, int *offsets, int *perm,
+                      void *stream);
+
+/* Device synthetic fill: dst[i] = N(mean, std) sample of (seed, stream, i). */
+int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed,
+                            uint64_t stream_id, float mean, float std,
+                            void *stream);
+
+/* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,
+ * src/matrix.c:82-116) or glibc-expf restatement (which = 1) of x[i], the two
+ * scalar exponentials the routing softmax uses. */
+int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream);
+
+/* Kernel timing of the last moe_hip_forward_dev call on the library's
+ * events: milliseconds for [route, dispatch, gate_up, down, combine]. */
+int moe_hip_last_timings(float *ms5);
+int moe_hip_set_timing(int on);
+
+/* ---------------------------------------------------------------------------
+ * Device memory helpers for callers with no HIP binding of their own (the
+ * Python tests and benchmark use these).  Copies and memsets run on the
+ * library stream and are complete at return.  kind: 1 host->device,
+ * 2 device->host, 3 device->device.
+ * ------------------------------------------------------------------------- */
+int moe_hip_dev_alloc(void **ptr, size_t bytes);
+int moe_hip_dev_free(void *ptr);
+int moe_hip_memcpy(void *dst, const void *src, size_t bytes, int kind);
+int moe_hip_memset(void *ptr, int value, size_t bytes);
+int moe_hip_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_HIP_H */

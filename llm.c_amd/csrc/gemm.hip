@@ -1,0 +1,342 @@
+// gemm.hip — grouped expert GEMMs on the fp32 matrix cores of gfx950, plus
+// the combine, weight packing and synthetic fill kernels.
+//
+// Layout (device, packed once at upload):
+//   gate/up  wgu [E][2F][d]: for feature block fb (32 features) rows
+//            64*fb + c hold gate feature 32*fb + c (c < 32) and up feature
+//            32*fb + c - 32 (c >= 32); every row is K (= d) contiguous.
+//   down     wdT [E][d][F]: row n holds W_down[:, n] (K = F contiguous).
+// The rows of one expert's m-tile are consecutive dispatch positions
+// offsets[e] + m; gate/up gathers them straight from x through perm.
+//
+// Work decomposition: the grid enumerates (m-tile, n-tile) pairs over the
+// flat per-expert m-tile list built by the dispatch kernel (tile_off), so a
+// hot expert simply owns more tiles; blocks past the live tile count exit.
+//
+// Each workgroup computes a 128 x (64*WN) tile with 2 x WN waves of 64 x 64.
+// A wave issues v_mfma_f32_32x32x2f32 on 2 x 2 sub-tiles.  K is staged
+// through double-buffered LDS in 32-wide slices; a lane of half h (lane/32)
+// feeds the MFMA's k-row h with the slice's elements 16h..16h+15 in turn, so
+// both operands come from LDS as 128-bit reads of K-contiguous rows.
+#include "moe_internal.h"
+#include "moe_math.h"
+#include "synth.h"
+
+namespace moe {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = kGemmBM;   // 128
+constexpr int KT = 32;
+constexpr int LDK = KT + 4;   // padded LDS row (144 B): conflict-free b128 reads
+
+// silu(g) * u in the vector form of swiglu (src/matrix.c:618-655).
+__device__ inline float swiglu1(float g, float u) {
+    float sig = 1.0f / (1.0f + exp_poly(-g));
+    return (g * sig) * u;
+}
+
+template <int MODE, int WN>
+__global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
+    constexpr int BN = 64 * WN;
+    constexpr int NT = 128 * WN;
+    constexpr int A_LD = (BM * KT / 4) / NT;   // float4 loads of A per thread
+    constexpr int B_LD = (BN * KT / 4) / NT;   // float4 loads of B per thread
+    extern __shared__ __align__(16) float smem[];
+    float *As = smem;                          // [2][BM][LDK]
+    float *Bs = smem + 2 * BM * LDK;           // [2][BN][LDK]
+
+    const int ntiles = a.N / BN;
+    const int nt = blockIdx.x % ntiles;
+    const int mtg = blockIdx.x / ntiles;
+    const int total = a.tile_off[a.E];
+    if (mtg >= total) return;
+    int lo = 0, hi = a.E - 1;
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (a.tile_off[mid] <= mtg) lo = mid; else hi = mid - 1;
+    }
+    const int e = lo;
+    const int row0 = a.offsets[e] + (mtg - a.tile_off[e]) * BM;
+    const int rows = min(BM, a.offsets[e + 1] - row0);
+    const int K = a.K;
+    const float *B = a.b + ((size_t)e * a.N + (size_t)nt * BN) * K;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int li = lane & 31, lh = lane >> 5;
+
+    // Per-thread global source rows for the A and B tiles.
+    const float *a_src[A_LD];
+    int a_dst[A_LD];
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+        int q = tid + NT * i;
+        int r = q >> 3, c4 = q & 7;
+        a_dst[i] = r * LDK + 4 * c4;
+        if (r < rows) {
+            size_t src_row;
+            if (MODE == 0) src_row = (size_t)(a.perm[row0 + r] / a.topk);
+            else           src_row = (size_t)(row0 + r);
+            a_src[i] = a.a + src_row * K + 4 * c4;
+        } else {
+            a_src[i] = nullptr;
+        }
+    }
+    const float *b_src[B_LD];
+    int b_dst[B_LD];
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+        int q = tid + NT * i;
+        int r = q >> 3, c4 = q & 7;
+        b_dst[i] = r * LDK + 4 * c4;
+        b_src[i] = B + (size_t)r * K + 4 * c4;
+    }
+
+    floatx4 ra[A_LD], rb[B_LD];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i)
+            ra[i] = a_src[i] ? *reinterpret_cast<const floatx4 *>(a_src[i] + k0)
+                             : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i)
+            rb[i] = *reinterpret_cast<const floatx4 *>(b_src[i] + k0);
+    };
+    auto sstore = [&](int buf) {
+        float *as = As + buf * BM * LDK;
+        float *bs = Bs + buf * BN * LDK;
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) *reinterpret_cast<floatx4 *>(as + a_dst[i]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) *reinterpret_cast<floatx4 *>(bs + b_dst[i]) = rb[i];
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.0f;
+
+    const int nk = K / KT;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * KT);
+        const float *as = As + buf * BM * LDK + (wm * 64 + li) * LDK + 16 * lh;
+        const float *bs = Bs + buf * BN * LDK + (wn * 64 + li) * LDK + 16 * lh;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
+            floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * LDK + 4 * q);
+            floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 4 * q);
+            floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 32 * LDK + 4 * q);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b1[s], acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b0[s], acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc[1][1], 0, 0, 0);
+            }
+        }
+        if (kt + 1 < nk) sstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Accumulator layout of a 32x32 block: lane l, register r holds
+    // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+    if (MODE == 0) {
+        const int f = ((nt * BN + wn * 64) >> 1) + li;   // feature index
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row < rows)
+                    a.c[(size_t)(row0 + row) * a.ldc + f] = swiglu1(acc[m][0][r], acc[m][1][r]);
+            }
+    } else {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row < rows) {
+                    size_t dst = (size_t)a.perm[row0 + row] * a.ldc;
+#pragma unroll
+                    for (int n = 0; n < 2; ++n)
+                        a.c[dst + nt * BN + wn * 64 + n * 32 + li] = acc[m][n][r];
+                }
+            }
+    }
+}
+
+template <int MODE, int WN>
+hipError_t launch_grouped(const GemmArgs &a, hipStream_t s) {
+    constexpr int BN = 64 * WN;
+    const size_t lds = (size_t)(2 * BM + 2 * BN) * LDK * sizeof(float);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t err = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&grouped_gemm_kernel<MODE, WN>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (err != hipSuccess) return err;
+        attr_set = true;
+    }
+    const int ntiles = a.N / BN;
+    dim3 grid((unsigned)(a.max_mtiles * ntiles));
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, WN>), grid, dim3(128 * WN), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_mode(const GemmArgs &a, hipStream_t s) {
+    switch (gemm_block_n(a.N)) {
+        case 256: return launch_grouped<MODE, 4>(a, s);
+        case 128: return launch_grouped<MODE, 2>(a, s);
+        case 64:  return launch_grouped<MODE, 1>(a, s);
+        default:  return hipErrorInvalidValue;
+    }
+}
+
+// out[t] = sum over slots of gw * y, one FMA per slot in slot order
+// (src/transformer.c:355-358 after contraction), optionally added into out.
+__global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
+    const int d4 = a.d >> 2;
+    const size_t total = (size_t)a.T * d4;
+    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+        const int t = (int)(i / d4), c = (int)(i % d4);
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int ki = 0; ki < a.k; ++ki) {
+            const float w = a.gw[(size_t)t * a.k + ki];
+            const floatx4 y = *reinterpret_cast<const floatx4 *>(
+                a.ys + ((size_t)t * a.k + ki) * a.d + 4 * c);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = fmaf(w, y[j], acc[j]);
+        }
+        floatx4 *o = reinterpret_cast<floatx4 *>(a.out + (size_t)t * a.d + 4 * c);
+        if (a.accumulate) {
+            floatx4 v = *o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = v[j] + acc[j];
+            *o = v;
+        } else {
+            *o = acc;
+        }
+    }
+}
+
+// Transposes through a 32 x 33 LDS tile.
+// pack gate/up: src [d x F] (gate, up) -> dst [2F x d] interleaved rows.
+__global__ __launch_bounds__(256) void pack_gateup_kernel(const float *wg, const float *wu,
+                                                           float *dst, int d, int F, int unpack) {
+    __shared__ float tile[32][33];
+    const int f0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
+    const float *src = blockIdx.z ? wu : wg;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8
+    if (!unpack) {
+        for (int r = ty; r < 32; r += 8)
+            tile[r][tx] = src[(size_t)(k0 + r) * F + f0 + tx];          // [k][f]
+        __syncthreads();
+        for (int r = ty; r < 32; r += 8) {
+            int f = f0 + r;
+            size_t row = (size_t)64 * (f >> 5) + (f & 31) + (blockIdx.z ? 32 : 0);
+            dst[row * d + k0 + tx] = tile[tx][r];
+        }
+    } else {
+        float *out = const_cast<float *>(src);
+        for (int r = ty; r < 32; r += 8) {
+            int f = f0 + r;
+            size_t row = (size_t)64 * (f >> 5) + (f & 31) + (blockIdx.z ? 32 : 0);
+            tile[r][tx] = dst[row * d + k0 + tx];                      // [f][k]
+        }
+        __syncthreads();
+        for (int r = ty; r < 32; r += 8)
+            out[(size_t)(k0 + r) * F + f0 + tx] = tile[tx][r];
+    }
+}
+
+// pack down: src [F x d] -> dst [d x F] (plain transpose); unpack inverts.
+__global__ __launch_bounds__(256) void transpose_kernel(const float *src, float *dst,
+                                                         int R, int Cc) {
+    __shared__ float tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int r = ty; r < 32; r += 8)
+        tile[r][tx] = src[(size_t)(r0 + r) * Cc + c0 + tx];
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8)
+        dst[(size_t)(c0 + r) * R + r0 + tx] = tile[tx][r];
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(float *dst, size_t n, uint64_t seed,
+                                                           uint64_t stream_id, float mean,
+                                                           float std) {
+    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = synth_normal(seed, stream_id, i, mean, std);
+}
+
+}  // namespace
+
+int gemm_block_n(int N) {
+    if (N % 256 == 0) return 256;
+    if (N % 128 == 0) return 128;
+    if (N % 64 == 0) return 64;
+    return 0;
+}
+
+hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) { return launch_mode<0>(a, s); }
+hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) { return launch_mode<1>(a, s); }
+
+hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
+    size_t total = (size_t)a.T * (a.d >> 2);
+    if (total == 0) return hipSuccess;
+    unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
+    hipLaunchKernelGGL(combine_kernel, dim3(blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_gateup(const float *wg, const float *wu, float *dst, int d, int F,
+                              hipStream_t s) {
+    dim3 grid(F / 32, d / 32, 2);
+    hipLaunchKernelGGL(pack_gateup_kernel, grid, dim3(256), 0, s, wg, wu, dst, d, F, 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack_gateup(const float *src, float *wg, float *wu, int d, int F,
+                                hipStream_t s) {
+    dim3 grid(F / 32, d / 32, 2);
+    hipLaunchKernelGGL(pack_gateup_kernel, grid, dim3(256), 0, s, wg, wu,
+                       const_cast<float *>(src), d, F, 1);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_down(const float *wd, float *dst, int F, int d, hipStream_t s) {
+    dim3 grid(d / 32, F / 32);
+    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, s, wd, dst, F, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack_down(const float *src, float *wd, int F, int d, hipStream_t s) {
+    dim3 grid(F / 32, d / 32);
+    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, s, src, wd, d, F);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream_id,
+                              float mean, float std, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(fill_normal_kernel, dim3(blocks), dim3(256), 0, s, dst, n, seed,
+                       stream_id, mean, std);
+    return hipGetLastError();
+}
+
+}  // namespace moe

@@ -1,0 +1,557 @@
+// moe_hip.cpp — the C ABI of libmoe_hip: drop-in moe_forward / decode entry
+// points over host pointers, the weight residency cache, and the
+// device-resident layer API.  All kernels are queued on one HIP stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <vector>
+
+#include "moe_internal.h"
+#include "../../include/moe_hip.h"
+
+struct MoeHipLayer {
+    int d = 0, F = 0, E = 0, k = 0;
+    float *wr = nullptr;     // [d x E]
+    float *bias = nullptr;   // [E] or null
+    float *wgu = nullptr;    // [E][2F][d]
+    float *wdT = nullptr;    // [E][d][F]
+};
+
+namespace {
+
+int g_err = MOE_HIP_OK;
+char g_msg[512] = "";
+bool g_init = false;
+int g_device = 0;
+hipStream_t g_stream = nullptr;
+bool g_timing = false;
+hipEvent_t g_ev[6] = {};
+bool g_have_times = false;
+
+int set_err(int code, const char *fmt, ...) {
+    g_err = code;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define HIP_TRY(expr)                                                              \
+    do {                                                                           \
+        hipError_t e_ = (expr);                                                    \
+        if (e_ != hipSuccess)                                                      \
+            return set_err(e_ == hipErrorOutOfMemory ? MOE_HIP_ERR_NOMEM : MOE_HIP_ERR_HIP, \
+                           "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_),  \
+                           __FILE__, __LINE__);                                    \
+    } while (0)
+
+#define TRY(expr)                        \
+    do {                                 \
+        int r_ = (expr);                 \
+        if (r_ != MOE_HIP_OK) return r_; \
+    } while (0)
+
+int ensure_init() {
+    if (g_init) return MOE_HIP_OK;
+    return moe_hip_init(-1);
+}
+
+hipStream_t pick_stream(void *s) { return s ? static_cast<hipStream_t>(s) : g_stream; }
+
+// Grow-only device buffer.
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    int reserve(size_t need) {
+        if (need <= bytes) return MOE_HIP_OK;
+        if (p) {
+            hipError_t e = hipFree(p);
+            p = nullptr;
+            bytes = 0;
+            if (e != hipSuccess) return set_err(MOE_HIP_ERR_HIP, "hipFree: %s", hipGetErrorString(e));
+        }
+        hipError_t e = hipMalloc(&p, need);
+        if (e != hipSuccess) {
+            p = nullptr;
+            return set_err(MOE_HIP_ERR_NOMEM, "hipMalloc(%zu) failed: %s", need, hipGetErrorString(e));
+        }
+        bytes = need;
+        return MOE_HIP_OK;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <class T> T *as() const { return static_cast<T *>(p); }
+};
+
+// Workspace shared by every call (calls are serialised by the caller).
+struct Workspace {
+    DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, perm, h, ys, stage;
+    void release_all() {
+        DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
+                         &perm, &h, &ys, &stage};
+        for (DevBuf *b : all) b->release();
+    }
+};
+Workspace g_ws;
+
+// Residency cache for the drop-in entry points.
+struct Resident {
+    MoeHipLayer *layer = nullptr;
+    std::vector<const void *> ptrs;
+};
+std::map<const MoEWeights *, Resident> g_resident;
+
+std::vector<const void *> weight_ptrs(const MoEWeights *w) {
+    std::vector<const void *> v;
+    v.push_back(w->W_router.data);
+    for (int e = 0; e < w->n_experts; ++e) {
+        v.push_back(w->experts[e].W_gate.data);
+        v.push_back(w->experts[e].W_up.data);
+        v.push_back(w->experts[e].W_down.data);
+    }
+    return v;
+}
+
+int check_shapes(int d, int F, int E, int k) {
+    if (d <= 0 || F <= 0 || E <= 0 || k <= 0)
+        return set_err(MOE_HIP_ERR_ARG, "bad MoE shape d=%d F=%d E=%d k=%d", d, F, E, k);
+    if (k > E)
+        return set_err(MOE_HIP_ERR_ARG, "top_k %d exceeds n_experts %d", k, E);
+    if (E > moe::kMaxExperts || k > moe::kMaxTopK)
+        return set_err(MOE_HIP_ERR_UNSUPPORTED, "n_experts %d / top_k %d above the supported %d / %d",
+                       E, k, moe::kMaxExperts, moe::kMaxTopK);
+    if (d % 64 != 0 || F % 32 != 0)
+        return set_err(MOE_HIP_ERR_UNSUPPORTED,
+                       "d_model %% 64 and ffn_hidden %% 32 must be 0 (got d=%d F=%d)", d, F);
+    return MOE_HIP_OK;
+}
+
+int validate_weights(const MoEWeights *w, int d, int F) {
+    if (!w || !w->experts || !w->W_router.data) return set_err(MOE_HIP_ERR_ARG, "null MoE weights");
+    if (w->W_router.rows != d || w->W_router.cols != w->n_experts)
+        return set_err(MOE_HIP_ERR_ARG, "W_router is %dx%d, expected %dx%d", w->W_router.rows,
+                       w->W_router.cols, d, w->n_experts);
+    for (int e = 0; e < w->n_experts; ++e) {
+        const FFNWeights &f = w->experts[e];
+        if (!f.W_gate.data || !f.W_up.data || !f.W_down.data)
+            return set_err(MOE_HIP_ERR_ARG, "expert %d has a null matrix", e);
+        if (f.W_gate.rows != d || f.W_gate.cols != F || f.W_up.rows != d || f.W_up.cols != F ||
+            f.W_down.rows != F || f.W_down.cols != d)
+            return set_err(MOE_HIP_ERR_ARG, "expert %d matrices do not match d=%d F=%d", e, d, F);
+    }
+    return MOE_HIP_OK;
+}
+
+int resident_layer(const MoEWeights *w, int d, int F, MoeHipLayer **out) {
+    TRY(validate_weights(w, d, F));
+    std::vector<const void *> ptrs = weight_ptrs(w);
+    auto it = g_resident.find(w);
+    if (it != g_resident.end()) {
+        MoeHipLayer *L = it->second.layer;
+        if (it->second.ptrs == ptrs && L->d == d && L->F == F && L->E == w->n_experts &&
+            L->k == w->top_k) {
+            *out = L;
+            return MOE_HIP_OK;
+        }
+        moe_hip_layer_destroy(L);
+        g_resident.erase(it);
+    }
+    MoeHipLayer *L = nullptr;
+    TRY(moe_hip_layer_create(d, F, w->n_experts, w->top_k, &L));
+    int rc = moe_hip_layer_load(L, w);
+    if (rc != MOE_HIP_OK) {
+        moe_hip_layer_destroy(L);
+        return rc;
+    }
+    g_resident[w] = Resident{L, ptrs};
+    *out = L;
+    return MOE_HIP_OK;
+}
+
+void die_on(int rc, const char *what) {
+    if (rc == MOE_HIP_OK) return;
+    fprintf(stderr, "[libmoe_hip] %s: %s\n", what, g_msg);
+    abort();
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_hip_init(int device) {
+    if (g_init) return MOE_HIP_OK;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0)
+        return set_err(MOE_HIP_ERR_NODEV, "no HIP device (%s)", hipGetErrorString(e));
+    if (device < 0) {
+        HIP_TRY(hipGetDevice(&device));
+    }
+    if (device >= n) return set_err(MOE_HIP_ERR_NODEV, "device %d of %d", device, n);
+    HIP_TRY(hipSetDevice(device));
+    HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    for (auto &ev : g_ev) HIP_TRY(hipEventCreate(&ev));
+    g_device = device;
+    g_init = true;
+    return MOE_HIP_OK;
+}
+
+void moe_hip_shutdown(void) {
+    if (!g_init) return;
+    (void)hipDeviceSynchronize();
+    for (auto &kv : g_resident) moe_hip_layer_destroy(kv.second.layer);
+    g_resident.clear();
+    g_ws.release_all();
+    for (auto &ev : g_ev) (void)hipEventDestroy(ev);
+    (void)hipStreamDestroy(g_stream);
+    g_stream = nullptr;
+    g_init = false;
+}
+
+int moe_hip_invalidate(const MoEWeights *w) {
+    auto it = g_resident.find(w);
+    if (it == g_resident.end()) return MOE_HIP_OK;
+    (void)hipStreamSynchronize(g_stream);
+    moe_hip_layer_destroy(it->second.layer);
+    g_resident.erase(it);
+    return MOE_HIP_OK;
+}
+
+int moe_hip_last_error(void) { return g_err; }
+const char *moe_hip_last_error_message(void) { return g_msg; }
+
+const char *moe_hip_error_string(int code) {
+    switch (code) {
+        case MOE_HIP_OK: return "ok";
+        case MOE_HIP_ERR_ARG: return "invalid argument";
+        case MOE_HIP_ERR_UNSUPPORTED: return "unsupported shape";
+        case MOE_HIP_ERR_HIP: return "HIP runtime error";
+        case MOE_HIP_ERR_NOMEM: return "device out of memory";
+        case MOE_HIP_ERR_NODEV: return "no GPU";
+        default: return "unknown";
+    }
+}
+
+int moe_hip_layer_create(int d_model, int ffn_hidden, int n_experts, int top_k,
+                         MoeHipLayer **layer) {
+    if (!layer) return set_err(MOE_HIP_ERR_ARG, "null layer out-pointer");
+    *layer = nullptr;
+    TRY(check_shapes(d_model, ffn_hidden, n_experts, top_k));
+    TRY(ensure_init());
+    MoeHipLayer *L = new MoeHipLayer();
+    L->d = d_model; L->F = ffn_hidden; L->E = n_experts; L->k = top_k;
+    const size_t ne = (size_t)n_experts * d_model * ffn_hidden;
+    hipError_t e1 = hipMalloc(&L->wr, sizeof(float) * (size_t)d_model * n_experts);
+    hipError_t e2 = e1 == hipSuccess ? hipMalloc(&L->wgu, sizeof(float) * 2 * ne) : e1;
+    hipError_t e3 = e2 == hipSuccess ? hipMalloc(&L->wdT, sizeof(float) * ne) : e2;
+    if (e3 != hipSuccess) {
+        moe_hip_layer_destroy(L);
+        return set_err(MOE_HIP_ERR_NOMEM, "layer weights (%zu bytes): %s",
+                       sizeof(float) * 3 * ne, hipGetErrorString(e3));
+    }
+    *layer = L;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_layer_destroy(MoeHipLayer *L) {
+    if (!L) return MOE_HIP_OK;
+    if (L->wr) (void)hipFree(L->wr);
+    if (L->bias) (void)hipFree(L->bias);
+    if (L->wgu) (void)hipFree(L->wgu);
+    if (L->wdT) (void)hipFree(L->wdT);
+    delete L;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_layer_load(MoeHipLayer *L, const MoEWeights *w) {
+    if (!L) return set_err(MOE_HIP_ERR_ARG, "null layer");
+    if (!w || w->n_experts != L->E || w->top_k != L->k)
+        return set_err(MOE_HIP_ERR_ARG, "weights do not match the layer (E=%d k=%d)", L->E, L->k);
+    TRY(validate_weights(w, L->d, L->F));
+    const size_t dF = (size_t)L->d * L->F;
+    TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
+    float *st = g_ws.stage.as<float>();
+    HIP_TRY(hipMemcpyAsync(L->wr, w->W_router.data, sizeof(float) * (size_t)L->d * L->E,
+                           hipMemcpyHostToDevice, g_stream));
+    for (int e = 0; e < L->E; ++e) {
+        const FFNWeights &f = w->experts[e];
+        HIP_TRY(hipMemcpyAsync(st, f.W_gate.data, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+        HIP_TRY(hipMemcpyAsync(st + dF, f.W_up.data, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+        HIP_TRY(hipMemcpyAsync(st + 2 * dF, f.W_down.data, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+        HIP_TRY(moe::launch_pack_gateup(st, st + dF, L->wgu + 2 * dF * e, L->d, L->F, g_stream));
+        HIP_TRY(moe::launch_pack_down(st + 2 * dF, L->wdT + dF * e, L->F, L->d, g_stream));
+    }
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_layer_set_router_bias(MoeHipLayer *L, const float *bias) {
+    if (!L) return set_err(MOE_HIP_ERR_ARG, "null layer");
+    if (!bias) {
+        if (L->bias) {
+            HIP_TRY(hipStreamSynchronize(g_stream));
+            HIP_TRY(hipFree(L->bias));
+        }
+        L->bias = nullptr;
+        return MOE_HIP_OK;
+    }
+    if (!L->bias) HIP_TRY(hipMalloc(&L->bias, sizeof(float) * L->E));
+    HIP_TRY(hipMemcpyAsync(L->bias, bias, sizeof(float) * L->E, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_layer_fill_synthetic(MoeHipLayer *L, uint64_t seed, float std_router,
+                                 float std_expert) {
+    if (!L) return set_err(MOE_HIP_ERR_ARG, "null layer");
+    const size_t dF = (size_t)L->d * L->F;
+    TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
+    float *st = g_ws.stage.as<float>();
+    HIP_TRY(moe::launch_fill_normal(L->wr, (size_t)L->d * L->E, seed, 1, 0.0f, std_router, g_stream));
+    for (int e = 0; e < L->E; ++e) {
+        HIP_TRY(moe::launch_fill_normal(st, dF, seed, 16 + 3 * (uint64_t)e, 0.0f, std_expert, g_stream));
+        HIP_TRY(moe::launch_fill_normal(st + dF, dF, seed, 17 + 3 * (uint64_t)e, 0.0f, std_expert, g_stream));
+        HIP_TRY(moe::launch_fill_normal(st + 2 * dF, dF, seed, 18 + 3 * (uint64_t)e, 0.0f, std_expert, g_stream));
+        HIP_TRY(moe::launch_pack_gateup(st, st + dF, L->wgu + 2 * dF * e, L->d, L->F, g_stream));
+        HIP_TRY(moe::launch_pack_down(st + 2 * dF, L->wdT + dF * e, L->F, L->d, g_stream));
+    }
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_layer_get_expert(MoeHipLayer *L, int e, float *wg, float *wu, float *wd) {
+    if (!L || e < 0 || e >= L->E) return set_err(MOE_HIP_ERR_ARG, "bad layer/expert");
+    const size_t dF = (size_t)L->d * L->F;
+    TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
+    float *st = g_ws.stage.as<float>();
+    HIP_TRY(moe::launch_unpack_gateup(L->wgu + 2 * dF * e, st, st + dF, L->d, L->F, g_stream));
+    HIP_TRY(moe::launch_unpack_down(L->wdT + dF * e, st + 2 * dF, L->F, L->d, g_stream));
+    if (wg) HIP_TRY(hipMemcpyAsync(wg, st, sizeof(float) * dF, hipMemcpyDeviceToHost, g_stream));
+    if (wu) HIP_TRY(hipMemcpyAsync(wu, st + dF, sizeof(float) * dF, hipMemcpyDeviceToHost, g_stream));
+    if (wd) HIP_TRY(hipMemcpyAsync(wd, st + 2 * dF, sizeof(float) * dF, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_layer_get_router(MoeHipLayer *L, float *wr) {
+    if (!L || !wr) return set_err(MOE_HIP_ERR_ARG, "bad layer/pointer");
+    HIP_TRY(hipMemcpyAsync(wr, L->wr, sizeof(float) * (size_t)L->d * L->E, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed, uint64_t stream_id, float mean,
+                            float std, void *stream) {
+    TRY(ensure_init());
+    if (!dst && n) return set_err(MOE_HIP_ERR_ARG, "null destination");
+    HIP_TRY(moe::launch_fill_normal(dst, n, seed, stream_id, mean, std, pick_stream(stream)));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream) {
+    TRY(ensure_init());
+    if (which != 0 && which != 1) return set_err(MOE_HIP_ERR_ARG, "which must be 0 or 1");
+    if (n && (!x || !y)) return set_err(MOE_HIP_ERR_ARG, "null pointer");
+    HIP_TRY(moe::launch_eval_exp(which, x, y, n, pick_stream(stream)));
+    return MOE_HIP_OK;
+}
+
+static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
+                      int *counts, int *offsets, int *tile_off, int *perm, hipStream_t s) {
+    moe::RouteArgs ra{x, L->wr, L->bias, T, L->d, L->E, L->k, probs, ids, gw};
+    if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
+    HIP_TRY(moe::launch_route(ra, s));
+    if (g_timing) HIP_TRY(hipEventRecord(g_ev[1], s));
+    moe::DispatchArgs da{ids, T * L->k, L->E, moe::kGemmBM, counts, offsets, tile_off, perm};
+    HIP_TRY(moe::launch_dispatch(da, s));
+    if (g_timing) HIP_TRY(hipEventRecord(g_ev[2], s));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_route_dev(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
+                      int *counts, int *offsets, int *perm, void *stream) {
+    if (!L || (!x && T > 0) || T < 0) return set_err(MOE_HIP_ERR_ARG, "bad route arguments");
+    if (T == 0) return MOE_HIP_OK;
+    const size_t n = (size_t)T * L->k;
+    TRY(g_ws.ids.reserve(sizeof(int) * n));
+    TRY(g_ws.gw.reserve(sizeof(float) * n));
+    TRY(g_ws.counts.reserve(sizeof(int) * L->E));
+    TRY(g_ws.offsets.reserve(sizeof(int) * (L->E + 1)));
+    TRY(g_ws.tile_off.reserve(sizeof(int) * (L->E + 1)));
+    TRY(g_ws.perm.reserve(sizeof(int) * n));
+    hipStream_t s = pick_stream(stream);
+    return route_impl(L, x, T, probs, ids ? ids : g_ws.ids.as<int>(), gw ? gw : g_ws.gw.as<float>(),
+                      counts ? counts : g_ws.counts.as<int>(),
+                      offsets ? offsets : g_ws.offsets.as<int>(), g_ws.tile_off.as<int>(),
+                      perm ? perm : g_ws.perm.as<int>(), s);
+}
+
+int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
+                        int accumulate, void *stream) {
+    if (!L || T < 0 || (T > 0 && (!x || !out))) return set_err(MOE_HIP_ERR_ARG, "bad forward arguments");
+    if (T == 0) return MOE_HIP_OK;
+    const int d = L->d, F = L->F, E = L->E, k = L->k;
+    const size_t n = (size_t)T * k;
+    if (n > (size_t)0x7fffffff / (size_t)(F > d ? F : d))
+        return set_err(MOE_HIP_ERR_UNSUPPORTED, "T*k*max(F,d) exceeds 32-bit indexing");
+    TRY(g_ws.ids.reserve(sizeof(int) * n));
+    TRY(g_ws.gw.reserve(sizeof(float) * n));
+    TRY(g_ws.counts.reserve(sizeof(int) * E));
+    TRY(g_ws.offsets.reserve(sizeof(int) * (E + 1)));
+    TRY(g_ws.tile_off.reserve(sizeof(int) * (E + 1)));
+    TRY(g_ws.perm.reserve(sizeof(int) * n));
+    TRY(g_ws.h.reserve(sizeof(float) * n * F));
+    TRY(g_ws.ys.reserve(sizeof(float) * n * d));
+    hipStream_t s = pick_stream(stream);
+    int *ids_d = ids ? ids : g_ws.ids.as<int>();
+    float *gw = g_ws.gw.as<float>();
+    int *offsets = g_ws.offsets.as<int>(), *tile_off = g_ws.tile_off.as<int>();
+    int *perm = g_ws.perm.as<int>();
+    TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm, s));
+
+    const int max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
+    moe::GemmArgs gu{x, perm, k, L->wgu, g_ws.h.as<float>(), offsets, tile_off, E, d, 2 * F, F,
+                     max_mtiles};
+    HIP_TRY(moe::launch_gemm_gateup(gu, s));
+    if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
+    moe::GemmArgs dn{g_ws.h.as<float>(), perm, k, L->wdT, g_ws.ys.as<float>(), offsets, tile_off, E,
+                     F, d, d, max_mtiles};
+    HIP_TRY(moe::launch_gemm_down(dn, s));
+    if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
+    moe::CombineArgs ca{g_ws.ys.as<float>(), gw, out, T, d, k, accumulate};
+    HIP_TRY(moe::launch_combine(ca, s));
+    if (g_timing) {
+        HIP_TRY(hipEventRecord(g_ev[5], s));
+        g_have_times = true;
+    }
+    return MOE_HIP_OK;
+}
+
+int moe_hip_set_timing(int on) {
+    TRY(ensure_init());
+    g_timing = on != 0;
+    g_have_times = false;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_last_timings(float *ms5) {
+    if (!ms5) return set_err(MOE_HIP_ERR_ARG, "null output");
+    if (!g_have_times) return set_err(MOE_HIP_ERR_ARG, "no timed forward since timing was enabled");
+    HIP_TRY(hipEventSynchronize(g_ev[5]));
+    for (int i = 0; i < 5; ++i) HIP_TRY(hipEventElapsedTime(&ms5[i], g_ev[i], g_ev[i + 1]));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg,
+                    ForwardCache *cache, Matrix *out) {
+    if (!x || !w || !cfg || !cache || !out) return set_err(MOE_HIP_ERR_ARG, "null argument");
+    const int T = x->rows, d = x->cols, F = cfg->ffn_hidden, E = w->n_experts, k = w->top_k;
+    if (out->rows != T || out->cols != d)
+        return set_err(MOE_HIP_ERR_ARG, "out is %dx%d, expected %dx%d", out->rows, out->cols, T, d);
+    TRY(check_shapes(d, F, E, k));
+    if (T == 0) return MOE_HIP_OK;
+    if (!x->data || !out->data || !cache->router_probs || !cache->expert_ids)
+        return set_err(MOE_HIP_ERR_ARG, "null data pointer");
+    TRY(ensure_init());
+    MoeHipLayer *L = nullptr;
+    TRY(resident_layer(w, d, F, &L));
+    const size_t xd = (size_t)T * d;
+    TRY(g_ws.x.reserve(sizeof(float) * xd));
+    TRY(g_ws.out.reserve(sizeof(float) * xd));
+    TRY(g_ws.probs.reserve(sizeof(float) * (size_t)T * E));
+    TRY(g_ws.ids.reserve(sizeof(int) * (size_t)T * k));
+    float *dx = g_ws.x.as<float>(), *dout = g_ws.out.as<float>(), *dprobs = g_ws.probs.as<float>();
+    int *dids = g_ws.ids.as<int>();
+    HIP_TRY(hipMemcpyAsync(dx, x->data, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
+    TRY(moe_hip_forward_dev(L, dx, T, dout, dprobs, dids, 0, g_stream));
+    HIP_TRY(hipMemcpyAsync(out->data, dout, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipMemcpyAsync(cache->router_probs, dprobs, sizeof(float) * (size_t)T * E,
+                           hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
+                           hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+void moe_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg, ForwardCache *cache,
+                 Matrix *out) {
+    die_on(moe_hip_forward(x, w, cfg, cache, out), "moe_forward");
+}
+
+int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x_norm, int n_rows,
+                     float *x) {
+    if (!w || !cfg || n_rows < 0 || (n_rows > 0 && (!x_norm || !x)))
+        return set_err(MOE_HIP_ERR_ARG, "bad decode arguments");
+    const int d = cfg->d_model, F = cfg->ffn_hidden;
+    TRY(check_shapes(d, F, w->n_experts, w->top_k));
+    if (n_rows == 0) return MOE_HIP_OK;
+    TRY(ensure_init());
+    MoeHipLayer *L = nullptr;
+    TRY(resident_layer(w, d, F, &L));
+    const size_t xd = (size_t)n_rows * d;
+    TRY(g_ws.x.reserve(sizeof(float) * xd));
+    TRY(g_ws.out.reserve(sizeof(float) * xd));
+    float *dxn = g_ws.x.as<float>(), *dx = g_ws.out.as<float>();
+    HIP_TRY(hipMemcpyAsync(dxn, x_norm, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipMemcpyAsync(dx, x, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
+    TRY(moe_hip_forward_dev(L, dxn, n_rows, dx, nullptr, nullptr, 1, g_stream));
+    HIP_TRY(hipMemcpyAsync(x, dx, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+void moe_decode_step(const MoEWeights *w, const ModelConfig *cfg, const float *x_norm, float *x) {
+    die_on(moe_decode_batch(w, cfg, x_norm, 1, x), "moe_decode_step");
+}
+
+int moe_hip_dev_alloc(void **ptr, size_t bytes) {
+    if (!ptr) return set_err(MOE_HIP_ERR_ARG, "null out-pointer");
+    *ptr = nullptr;
+    TRY(ensure_init());
+    HIP_TRY(hipMalloc(ptr, bytes ? bytes : 1));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_dev_free(void *ptr) {
+    if (!ptr) return MOE_HIP_OK;
+    HIP_TRY(hipFree(ptr));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_memcpy(void *dst, const void *src, size_t bytes, int kind) {
+    TRY(ensure_init());
+    if (bytes == 0) return MOE_HIP_OK;
+    if (!dst || !src) return set_err(MOE_HIP_ERR_ARG, "null pointer");
+    hipMemcpyKind k = kind == 1 ? hipMemcpyHostToDevice
+                    : kind == 2 ? hipMemcpyDeviceToHost
+                    : kind == 3 ? hipMemcpyDeviceToDevice : hipMemcpyDefault;
+    if (kind < 1 || kind > 3) return set_err(MOE_HIP_ERR_ARG, "bad copy kind %d", kind);
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, k, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_memset(void *ptr, int value, size_t bytes) {
+    TRY(ensure_init());
+    if (bytes == 0) return MOE_HIP_OK;
+    if (!ptr) return set_err(MOE_HIP_ERR_ARG, "null pointer");
+    HIP_TRY(hipMemsetAsync(ptr, value, bytes, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_synchronize(void) {
+    TRY(ensure_init());
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,87 @@
+// moe_internal.h — shared declarations between the HIP kernel files and the
+// C-ABI layer of libmoe_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+// Rows per m-tile of the grouped expert GEMMs; the dispatch kernel builds the
+// per-expert tile schedule with the same value.
+constexpr int kGemmBM = 128;
+// Largest expert count the routing kernels support (LDS sizing).
+constexpr int kMaxExperts = 128;
+// Largest top-k the routing kernels support.
+constexpr int kMaxTopK = 16;
+
+struct RouteArgs {
+    const float *x;      // [T x d]
+    const float *wr;     // [d x E], reference layout
+    const float *bias;   // [E] or nullptr
+    int T, d, E, k;
+    float *probs;        // [T x E]
+    int *ids;            // [T x k]
+    float *gw;           // [T x k]
+};
+
+struct DispatchArgs {
+    const int *ids;      // [T x k]
+    int n;               // T * k
+    int E;
+    int bm;              // rows per m-tile for the schedule
+    int *counts;         // [E]
+    int *offsets;        // [E + 1]
+    int *tile_off;       // [E + 1] m-tile prefix; tile_off[E] = total m-tiles
+    int *perm;           // [n]
+};
+
+struct GemmArgs {
+    // A rows: gate/up gathers x[perm[pos] / k]; down reads H[pos].
+    const float *a;      // x [T x K] (gate/up) or H [n x K] (down)
+    const int *perm;     // [n]
+    int topk;            // k, to turn perm entries into tokens
+    const float *b;      // packed weights, [E][N][K] (K contiguous)
+    float *c;            // H [n x F] (gate/up) or Ys [n x N] indexed by perm (down)
+    const int *offsets;  // [E + 1]
+    const int *tile_off; // [E + 1]
+    int E;
+    int K;               // reduction length
+    int N;               // packed output columns (2F for gate/up, d for down)
+    int ldc;             // row stride of c (F for gate/up, d for down)
+    int max_mtiles;      // grid bound on m-tiles
+};
+
+struct CombineArgs {
+    const float *ys;     // [T*k x d], slot-indexed expert outputs
+    const float *gw;     // [T x k]
+    float *out;          // [T x d]
+    int T, d, k;
+    int accumulate;      // out += combined instead of out = combined
+};
+
+hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
+hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);
+hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s);
+hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
+
+// Weight packing (reference layout -> device layout) and its inverse.
+hipError_t launch_pack_gateup(const float *wg, const float *wu, float *dst,
+                              int d, int F, hipStream_t s);
+hipError_t launch_pack_down(const float *wd, float *dst, int F, int d,
+                            hipStream_t s);
+hipError_t launch_unpack_gateup(const float *src, float *wg, float *wu, int d,
+                                int F, hipStream_t s);
+hipError_t launch_unpack_down(const float *src, float *wd, int F, int d,
+                              hipStream_t s);
+// Elementwise exp_poly (which = 0) or glibc-expf (which = 1) on the device,
+// exactly as the routing kernels evaluate them.
+hipError_t launch_eval_exp(int which, const float *x, float *y, size_t n, hipStream_t s);
+hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed,
+                              uint64_t stream_id, float mean, float std,
+                              hipStream_t s);
+
+// Number of n-tiles / block width the gate-up and down launches use.
+int gemm_block_n(int N);
+
+}  // namespace moe

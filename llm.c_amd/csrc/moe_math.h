@@ -1,0 +1,82 @@
+// moe_math.h — scalar device functions whose bits must match the reference's
+// CPU arithmetic.  Contraction is off for everything after this include:
+// every fused multiply-add is an explicit fmaf()/fma().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace moe {
+
+__device__ inline float ftz_f(float x) {
+    uint32_t u = __float_as_uint(x);
+    return ((u & 0x7f800000u) == 0u) ? __uint_as_float(u & 0x80000000u) : x;
+}
+
+// exp_avx2 lane (src/matrix.c:82-116) under DAZ/FTZ.
+__device__ inline float exp_poly(float v) {
+    v = fminf(fmaxf(ftz_f(v), -88.0f), 88.0f);
+    float z = ftz_f(v * 1.4426950408f);
+    float n = floorf(z);
+    float f = ftz_f(z - n);
+    float p = 0.0001540353f;
+    p = fmaf(p, f, 0.0013333558f);
+    p = fmaf(p, f, 0.0096181292f);
+    p = fmaf(p, f, 0.0555041086f);
+    p = fmaf(p, f, 0.2402265069f);
+    p = fmaf(p, f, 0.6931471806f);
+    p = fmaf(p, f, 1.0000000000f);
+    int ni = (int)n;
+    uint32_t sb = (uint32_t)(ni + 127) << 23;
+    if ((sb & 0x7f800000u) == 0u) return 0.0f;
+    return ftz_f(p * __uint_as_float(sb));
+}
+
+// 2^(i/32) as doubles with i<<47 subtracted from the bits (the table layout
+// of glibc's expf, glibc 2.35 sysdeps/ieee754/flt-32/e_expf.c).
+static __constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
+
+// glibc expf as the FMA build of x86-64 computes it: z = x*32/ln2 fused
+// into both of its additions, k by the 1.5*2^52 shift, cubic in r, scaled by
+// the table entry with k/32's exponent added; subnormal results flushed.
+__device__ inline float glibc_expf(float x) {
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    const double SHIFT = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    uint32_t ux = __float_as_uint(x);
+    uint32_t ax = ux & 0x7fffffffu;
+    if ((ax >> 20) >= (0x42b00000u >> 20)) {
+        if (ux == 0xff800000u) return 0.0f;
+        if (ax >= 0x7f800000u) return x + x;
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    double xd = (double)x;
+    double kd = fma(InvLn2N, xd, SHIFT);
+    uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= SHIFT;
+    double r = fma(InvLn2N, xd, -kd);
+    uint64_t t = kExp2Tab[ki % 32];
+    t += ki << (52 - 5);
+    double s = __longlong_as_double((long long)t);
+    double zz = fma(C0, r, C1);
+    double r2 = r * r;
+    double yy = fma(C2, r, 1.0);
+    yy = fma(zz, r2, yy);
+    double y = yy * s;
+    return ftz_f((float)y);
+}
+
+}  // namespace moe

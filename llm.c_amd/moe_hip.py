@@ -1,0 +1,235 @@
+"""Python binding of libmoe_hip (ctypes), mirroring the reference interface.
+
+`moe_forward(x, layer, cfg, cache, out)` keeps the argument meaning of the
+reference's moe_forward (include/transformer.h:270-272): x and out are
+[T x d_model] matrices, cache receives router_probs [T x E] and expert_ids
+[T x top_k].  The device-resident API works on raw device addresses
+(DeviceArray below allocates them through the library itself).
+
+The library is the native code in llm.c_amd/libmoe_hip.so; importing this
+module raises if it has not been built.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+from abi_types import (FFNWeights, ForwardCache, HostMoE, Matrix, MoEWeights,  # noqa: F401
+                       ModelConfig, fptr, iptr, make_cache, matrix)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmoe_hip.so")
+
+OK = 0
+ERRORS = {1: "invalid argument", 2: "unsupported shape", 3: "HIP runtime error",
+          4: "device out of memory", 5: "no GPU"}
+
+_P = C.c_void_p
+_F = C.POINTER(C.c_float)
+_I = C.POINTER(C.c_int)
+
+# name -> (restype, argtypes); one entry per function of include/moe_hip.h.
+SIGNATURES = {
+    "moe_forward": (None, [C.POINTER(Matrix), C.POINTER(MoEWeights), C.POINTER(ModelConfig),
+                           C.POINTER(ForwardCache), C.POINTER(Matrix)]),
+    "moe_hip_forward": (C.c_int, [C.POINTER(Matrix), C.POINTER(MoEWeights),
+                                  C.POINTER(ModelConfig), C.POINTER(ForwardCache),
+                                  C.POINTER(Matrix)]),
+    "moe_decode_step": (None, [C.POINTER(MoEWeights), C.POINTER(ModelConfig), _F, _F]),
+    "moe_decode_batch": (C.c_int, [C.POINTER(MoEWeights), C.POINTER(ModelConfig), _F,
+                                   C.c_int, _F]),
+    "moe_hip_init": (C.c_int, [C.c_int]),
+    "moe_hip_shutdown": (None, []),
+    "moe_hip_invalidate": (C.c_int, [C.POINTER(MoEWeights)]),
+    "moe_hip_last_error": (C.c_int, []),
+    "moe_hip_error_string": (C.c_char_p, [C.c_int]),
+    "moe_hip_last_error_message": (C.c_char_p, []),
+    "moe_hip_layer_create": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_P)]),
+    "moe_hip_layer_destroy": (C.c_int, [_P]),
+    "moe_hip_layer_load": (C.c_int, [_P, C.POINTER(MoEWeights)]),
+    "moe_hip_layer_set_router_bias": (C.c_int, [_P, _F]),
+    "moe_hip_layer_fill_synthetic": (C.c_int, [_P, C.c_uint64, C.c_float, C.c_float]),
+    "moe_hip_layer_get_expert": (C.c_int, [_P, C.c_int, _F, _F, _F]),
+    "moe_hip_layer_get_router": (C.c_int, [_P, _F]),
+    "moe_hip_forward_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
+    "moe_hip_route_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "moe_hip_fill_normal_dev": (C.c_int, [_P, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float,
+                                          C.c_float, _P]),
+    "moe_hip_eval_exp": (C.c_int, [C.c_int, _P, _P, C.c_size_t, _P]),
+    "moe_hip_last_timings": (C.c_int, [_F]),
+    "moe_hip_set_timing": (C.c_int, [C.c_int]),
+    "moe_hip_dev_alloc": (C.c_int, [C.POINTER(_P), C.c_size_t]),
+    "moe_hip_dev_free": (C.c_int, [_P]),
+    "moe_hip_memcpy": (C.c_int, [_P, _P, C.c_size_t, C.c_int]),
+    "moe_hip_memset": (C.c_int, [_P, C.c_int, C.c_size_t]),
+    "moe_hip_synchronize": (C.c_int, []),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libmoe_hip.so once; raises FileNotFoundError if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with `make -C llm.c_amd` "
+                "(or __graft_entry__.build()); there is no fallback path")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class MoeHipError(RuntimeError):
+    pass
+
+
+def check(rc):
+    if rc != OK:
+        msg = lib().moe_hip_last_error_message().decode(errors="replace")
+        raise MoeHipError(f"libmoe_hip error {rc} ({ERRORS.get(rc, '?')}): {msg}")
+
+
+def moe_forward(x, hw, cache_probs=None, cache_ids=None):
+    """Host-pointer drop-in: returns (out, probs, ids) for x [T x d] (numpy)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T = x.shape[0]
+    out = np.zeros((T, hw.d), np.float32)
+    fc, probs, ids = make_cache(T, hw.E, hw.k)
+    cfg = hw.config(T)
+    check(lib().moe_hip_forward(C.byref(matrix(x)), C.byref(hw.weights), C.byref(cfg),
+                                C.byref(fc), C.byref(matrix(out))))
+    return out, probs, ids
+
+
+def decode_batch(x_norm, x, hw):
+    """x[r] += MoE(x_norm[r]) through moe_decode_batch; returns the new x."""
+    xn = np.ascontiguousarray(x_norm, dtype=np.float32)
+    xo = np.array(x, dtype=np.float32, copy=True, order="C")
+    cfg = hw.config(xn.shape[0])
+    check(lib().moe_decode_batch(C.byref(hw.weights), C.byref(cfg), fptr(xn), xn.shape[0],
+                                 fptr(xo)))
+    return xo
+
+
+class Layer:
+    """Device-resident MoE layer (packed weights in HBM)."""
+
+    def __init__(self, d, F, E, k):
+        self.d, self.F, self.E, self.k = d, F, E, k
+        h = _P()
+        check(lib().moe_hip_layer_create(d, F, E, k, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().moe_hip_layer_destroy(self.h)
+            self.h = _P()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def load(self, hw):
+        check(lib().moe_hip_layer_load(self.h, C.byref(hw.weights)))
+
+    def set_bias(self, bias):
+        if bias is None:
+            check(lib().moe_hip_layer_set_router_bias(self.h, None))
+        else:
+            b = np.ascontiguousarray(bias, dtype=np.float32)
+            assert b.shape == (self.E,)
+            check(lib().moe_hip_layer_set_router_bias(self.h, fptr(b)))
+
+    def fill_synthetic(self, seed, std_router, std_expert):
+        check(lib().moe_hip_layer_fill_synthetic(self.h, seed, std_router, std_expert))
+
+    def get_expert(self, e):
+        wg = np.empty((self.d, self.F), np.float32)
+        wu = np.empty((self.d, self.F), np.float32)
+        wd = np.empty((self.F, self.d), np.float32)
+        check(lib().moe_hip_layer_get_expert(self.h, e, fptr(wg), fptr(wu), fptr(wd)))
+        return wg, wu, wd
+
+    def get_router(self):
+        wr = np.empty((self.d, self.E), np.float32)
+        check(lib().moe_hip_layer_get_router(self.h, fptr(wr)))
+        return wr
+
+    def forward_dev(self, x_ptr, T, out_ptr, probs_ptr=None, ids_ptr=None, accumulate=0,
+                    stream=None):
+        check(lib().moe_hip_forward_dev(self.h, x_ptr, T, out_ptr, probs_ptr, ids_ptr,
+                                        accumulate, stream))
+
+    def route_dev(self, x_ptr, T, probs=None, ids=None, gw=None, counts=None, offsets=None,
+                  perm=None, stream=None):
+        check(lib().moe_hip_route_dev(self.h, x_ptr, T, probs, ids, gw, counts, offsets, perm,
+                                      stream))
+
+
+def fill_normal_dev(ptr, n, seed, stream_id, mean, std, stream=None):
+    check(lib().moe_hip_fill_normal_dev(ptr, n, seed, stream_id, mean, std, stream))
+
+
+def eval_exp_dev(which, x_ptr, y_ptr, n, stream=None):
+    check(lib().moe_hip_eval_exp(which, x_ptr, y_ptr, n, stream))
+
+
+class DeviceArray:
+    """A device buffer owned through libmoe_hip (numpy dtype + shape)."""
+
+    def __init__(self, shape, dtype=np.float32):
+        self.shape = tuple(int(s) for s in np.atleast_1d(np.asarray(shape)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = _P()
+        check(lib().moe_hip_dev_alloc(C.byref(p), self.nbytes))
+        self.ptr = p
+
+    @classmethod
+    def from_host(cls, a):
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        check(lib().moe_hip_memcpy(d.ptr, a.ctypes.data_as(_P), d.nbytes, 1))
+        return d
+
+    def to_host(self):
+        a = np.empty(self.shape, self.dtype)
+        check(lib().moe_hip_memcpy(a.ctypes.data_as(_P), self.ptr, self.nbytes, 2))
+        return a
+
+    def zero(self):
+        check(lib().moe_hip_memset(self.ptr, 0, self.nbytes))
+
+    def free(self):
+        if self.ptr:
+            lib().moe_hip_dev_free(self.ptr)
+            self.ptr = _P()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize():
+    check(lib().moe_hip_synchronize())
+
+
+def set_timing(on):
+    check(lib().moe_hip_set_timing(1 if on else 0))
+
+
+def last_timings():
+    """[route, dispatch, gate_up, down, combine] in ms for the last forward_dev."""
+    a = (C.c_float * 5)()
+    check(lib().moe_hip_last_timings(a))
+    return list(a)

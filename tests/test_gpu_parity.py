@@ -1,0 +1,312 @@
+"""GPU parity: libmoe_hip (through its C ABI) against the CPU oracle.
+
+Bars (the layer's contract):
+  * router probabilities, expert ids, gate weights, expert counts, offsets
+    and the dispatch permutation: bit-exact;
+  * layer output: rel-L2 <= 1e-5 and max-abs <= 1e-4 against the oracle's
+    fp32 restatement of the reference on identical seeded inputs.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import moe_hip as mh
+import orc
+from abi_types import HostMoE
+from conftest import CONFIGS, GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-5
+ABS_TOL = 1e-4
+
+
+def say(*a):
+    print("[gpu-test]", *a, flush=True)
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def host_layer(d, F, E, k, seed, std_router, std_expert):
+    wr, ex = orc.synth_layer_host(d, F, E, k, seed, std_router, std_expert)
+    wg = np.stack([ex[e][0] for e in range(E)])
+    wu = np.stack([ex[e][1] for e in range(E)])
+    wd = np.stack([ex[e][2] for e in range(E)])
+    return HostMoE(wr, wg, wu, wd, k)
+
+
+def route_on_device(layer, x):
+    T = x.shape[0]
+    E, k = layer.E, layer.k
+    dx = mh.DeviceArray.from_host(x)
+    probs = mh.DeviceArray((T, E))
+    ids = mh.DeviceArray((T, k), np.int32)
+    gw = mh.DeviceArray((T, k))
+    counts = mh.DeviceArray((E,), np.int32)
+    offsets = mh.DeviceArray((E + 1,), np.int32)
+    perm = mh.DeviceArray((T * k,), np.int32)
+    layer.route_dev(dx.ptr, T, probs.ptr, ids.ptr, gw.ptr, counts.ptr, offsets.ptr, perm.ptr)
+    mh.synchronize()
+    return (probs.to_host(), ids.to_host(), gw.to_host(), counts.to_host(), offsets.to_host(),
+            perm.to_host())
+
+
+def assert_route_equal(dev, x, wr, k, E, bias=None):
+    probs, ids, gw, counts, offsets, perm = dev
+    p_ref, i_ref, w_ref = orc.route(x, wr, k, bias)
+    c_ref, o_ref, perm_ref = orc.dispatch(i_ref, E)
+    n_p = int((bits(probs) != bits(p_ref)).sum())
+    n_i = int((ids != i_ref).sum())
+    n_w = int((bits(gw) != bits(w_ref)).sum())
+    assert n_p == 0, f"{n_p} router probabilities differ in bits"
+    assert n_i == 0, f"{n_i} expert ids differ"
+    assert n_w == 0, f"{n_w} gate weights differ in bits"
+    assert np.array_equal(counts, c_ref)
+    assert np.array_equal(offsets, o_ref)
+    assert np.array_equal(perm, perm_ref), "dispatch permutation differs"
+
+
+def assert_close(out, ref, what):
+    rel = orc.rel_l2(out, ref)
+    mabs = float(np.abs(out.astype(np.float64) - ref.astype(np.float64)).max()) if out.size else 0.0
+    say(f"{what}: rel-L2 {rel:.3e} max-abs {mabs:.3e}")
+    assert rel <= REL_TOL, f"{what}: rel-L2 {rel:.3e} > {REL_TOL}"
+    assert mabs <= ABS_TOL, f"{what}: max-abs {mabs:.3e} > {ABS_TOL}"
+
+
+# --------------------------------------------------------------------- scalars
+def test_device_exp_functions_bitexact():
+    """The two scalar exponentials of the routing softmax: exp_avx2 lanes and
+    the glibc expf restatement, on every 61st float of [-104, 0] plus
+    special values, against the oracle (itself pinned to libm)."""
+    lo, hi = 0x80000000, 0xC2D00000
+    pats = np.arange(lo, hi, 61, dtype=np.uint64).astype(np.uint32)
+    extra = np.array([0x00000000, 0x80000000, 0xFF800000, 0x7F800000, 0x7FC00000,
+                      0x42B00000, 0xC2B00000, 0xC2AE0000, 0xC2CFFFFF, 0x00000001,
+                      0x80000001, 0x3F800000, 0xBF800000], dtype=np.uint32)
+    pats = np.concatenate([pats, extra])
+    x = pats.view(np.float32)
+    say(f"exp check over {x.size} inputs")
+    dx = mh.DeviceArray.from_host(x)
+    dy = mh.DeviceArray(x.shape)
+    for which, fn in ((0, orc.exp_poly_array), (1, orc.expf_array)):
+        mh.eval_exp_dev(which, dx.ptr, dy.ptr, x.size)
+        mh.synchronize()
+        y = dy.to_host()
+        yr = fn(x)
+        same = (bits(y) == bits(yr)) | (np.isnan(y) & np.isnan(yr))
+        assert same.all(), f"which={which}: {int((~same).sum())} mismatches, first at " \
+                           f"{hex(int(pats[np.argmin(same)]))}"
+
+
+def test_device_synth_matches_host():
+    for seed, stream, std in ((0, 0, 1.0), (7, 17, 0.02), (123, 1, 0.1)):
+        n = 1 << 20
+        d = mh.DeviceArray((n,))
+        mh.fill_normal_dev(d.ptr, n, seed, stream, 0.0, std)
+        mh.synchronize()
+        assert np.array_equal(bits(d.to_host()), bits(orc.synth((n,), seed, stream, std)))
+
+
+# --------------------------------------------------------------------- routing
+ROUTE_CASES = [
+    # name, T, d, E, k, std_router
+    ("c1", 256, 128, 4, 2, 0.02),
+    ("c2", 4096, 256, 8, 2, 0.1),
+    ("c3", 4096, 512, 8, 2, 0.02),
+    ("c4", 64, 512, 16, 2, 0.02),
+    ("e12k3_ragged", 1000, 192, 12, 3, 0.1),
+    ("e5k5_all", 33, 64, 5, 5, 0.5),
+    ("e64k4", 2048, 2048, 64, 4, 0.02),
+    ("e128k1", 777, 128, 128, 1, 0.2),
+    ("t1", 1, 256, 8, 2, 0.1),
+]
+
+
+@pytest.mark.parametrize("name,T,d,E,k,std_router", ROUTE_CASES, ids=[c[0] for c in ROUTE_CASES])
+def test_route_bitexact(name, T, d, E, k, std_router):
+    say(f"route {name}: T={T} d={d} E={E} k={k}")
+    x = orc.synth((T, d), 11, 0, 1.0)
+    layer = mh.Layer(d, 64, E, k)
+    layer.fill_synthetic(11, std_router, 0.02)
+    wr = layer.get_router()
+    assert np.array_equal(bits(wr), bits(orc.synth((d, E), 11, 1, std_router)))
+    assert_route_equal(route_on_device(layer, x), x, wr, k, E)
+    layer.close()
+
+
+def test_route_ties_and_bias():
+    """Exact ties go to the lowest expert; a router bias (mat_mul_add form)
+    can starve experts completely (empty groups in the dispatch)."""
+    T, d, E, k = 300, 64, 16, 2
+    x = orc.synth((T, d), 5, 0, 1.0)
+    col = orc.synth((d, 1), 5, 1, 0.1)
+    wr = np.ascontiguousarray(np.repeat(col, E, axis=1))     # all logits equal per row
+    hw = HostMoE(wr, np.zeros((E, d, 64), np.float32), np.zeros((E, d, 64), np.float32),
+                 np.zeros((E, 64, d), np.float32), k)
+    layer = mh.Layer(d, 64, E, k)
+    layer.load(hw)
+    dev = route_on_device(layer, x)
+    assert (dev[1] == np.arange(k)).all(), "ties must pick experts 0..k-1"
+    assert_route_equal(dev, x, wr, k, E)
+    bias = np.zeros(E, np.float32)
+    bias[[3, 9]] = 50.0
+    layer.set_bias(bias)
+    dev = route_on_device(layer, x)
+    assert_route_equal(dev, x, wr, k, E, bias)
+    assert dev[3][3] == T and dev[3][9] == T and dev[3].sum() == T * k
+    layer.close()
+
+
+# --------------------------------------------------------------------- full layer
+def test_dropin_moe_forward_c1():
+    """Config 1 through the host-pointer drop-in moe_forward."""
+    c = CONFIGS["c1"]
+    hw = host_layer(c["d"], c["F"], c["E"], c["k"], 0, c["std_router"], c["std_expert"])
+    x = orc.synth((c["T"], c["d"]), 0, 0, 1.0)
+    out, probs, ids = mh.moe_forward(x, hw)
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw)
+    assert np.array_equal(bits(probs), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    assert_close(out, o_ref, "c1 drop-in")
+    g = os.path.join(GOLDEN, "golden_c1.npz")
+    if os.path.exists(g):
+        gz = np.load(g)
+        assert np.array_equal(bits(probs), bits(gz["probs"]))
+        assert np.array_equal(ids, gz["ids"])
+        assert_close(out, gz["out"], "c1 vs compiled reference")
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c4"])
+def test_forward_dev_configs(name):
+    c = CONFIGS[name]
+    T, d, F, E, k = c["T"], c["d"], c["F"], c["E"], c["k"]
+    say(f"forward {name}: T={T} d={d} F={F} E={E} k={k}")
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(1, c["std_router"], c["std_expert"])
+    hw = host_layer(d, F, E, k, 1, c["std_router"], c["std_expert"])
+    x = orc.synth((T, d), 1, 0, 1.0)
+    dx = mh.DeviceArray.from_host(x)
+    dout = mh.DeviceArray((T, d))
+    dprobs = mh.DeviceArray((T, E))
+    dids = mh.DeviceArray((T, k), np.int32)
+    layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+    mh.synchronize()
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw, nthreads=16)
+    assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+    assert np.array_equal(dids.to_host(), i_ref)
+    assert_close(dout.to_host(), o_ref, name)
+    layer.close()
+
+
+def test_forward_c5_sampled():
+    """Config 5 at full size on the device (12.9 GB of experts, Zipf-skewed
+    router bias when its fixture exists); routing compared for all tokens,
+    the layer output for a sample of tokens."""
+    c = CONFIGS["c5"]
+    T, d, F, E, k = c["T"], c["d"], c["F"], c["E"], c["k"]
+    say("c5: filling 12.9 GB of synthetic experts on the device")
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(5, c["std_router"], c["std_expert"])
+    bias = None
+    bpath = os.path.join(GOLDEN, "zipf_bias_e64_k4.npy")
+    if os.path.exists(bpath):
+        bias = np.load(bpath).astype(np.float32)
+        layer.set_bias(bias)
+    x = orc.synth((T, d), 5, 0, 1.0)
+    dx = mh.DeviceArray.from_host(x)
+    dout = mh.DeviceArray((T, d))
+    dprobs = mh.DeviceArray((T, E))
+    dids = mh.DeviceArray((T, k), np.int32)
+    say("c5: forward")
+    layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+    mh.synchronize()
+    wr = layer.get_router()
+    p_ref, i_ref, _ = orc.route(x, wr, k, bias)
+    ids = dids.to_host()
+    assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    say(f"c5: expert load max/mean {counts.max() / counts.mean():.2f}")
+    rng = np.random.default_rng(0)
+    sample = np.sort(rng.choice(T, 6, replace=False))
+    hot = int(np.argmax(counts))
+    hot_tok = int(np.nonzero((ids == hot).any(1))[0][-1])
+    sample = np.unique(np.concatenate([sample, [0, T - 1, hot_tok]]))
+    need = sorted(set(ids[sample].ravel().tolist()))
+    say(f"c5: generating {len(need)} experts on the host for {sample.size} sampled tokens")
+    _, ex = orc.synth_layer_host(d, F, E, k, 5, c["std_router"], c["std_expert"], experts=need)
+    o_ref, _, _ = orc.moe_forward_experts(x[sample], wr, ex, d, F, E, k, bias, nthreads=16)
+    assert_close(dout.to_host()[sample], o_ref, "c5 sampled")
+    layer.close()
+
+
+def test_decode_batch_c4():
+    """moe_decode_batch: x += MoE(x_norm) for 64 rows (host pointers)."""
+    c = CONFIGS["c4"]
+    T, d, F, E, k = c["T"], c["d"], c["F"], c["E"], c["k"]
+    hw = host_layer(d, F, E, k, 4, c["std_router"], c["std_expert"])
+    xn = orc.synth((T, d), 4, 0, 1.0)
+    x0 = orc.synth((T, d), 4, 2, 1.0)
+    x1 = mh.decode_batch(xn, x0, hw)
+    o_ref, _, _ = orc.moe_forward(xn, hw, nthreads=16)
+    assert_close(x1 - x0, o_ref, "c4 decode increment")
+    # Single-row entry (the inference_step slot).
+    x_one = x0[:1].copy()
+    mh.lib().moe_decode_step(hw.weights, hw.config(1), mh.fptr(np.ascontiguousarray(xn[:1])),
+                             mh.fptr(x_one))
+    o1, _, _ = orc.moe_forward(xn[:1].copy(), hw)
+    assert_close(x_one - x0[:1], o1, "c4 decode step")
+
+
+EDGE_CASES = [
+    # name, T, d, F, E, k
+    ("t1", 1, 128, 256, 8, 2),
+    ("t31_k1", 31, 64, 96, 4, 1),
+    ("t129", 129, 192, 160, 6, 2),
+    ("k_eq_e", 70, 64, 64, 4, 4),
+    ("e3", 200, 128, 128, 3, 2),
+]
+
+
+@pytest.mark.parametrize("name,T,d,F,E,k", EDGE_CASES, ids=[c[0] for c in EDGE_CASES])
+def test_forward_edge_shapes(name, T, d, F, E, k):
+    hw = host_layer(d, F, E, k, 9, 0.3, 0.05)
+    x = orc.synth((T, d), 9, 0, 1.0)
+    out, probs, ids = mh.moe_forward(x, hw)
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw)
+    assert np.array_equal(bits(probs), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    assert_close(out, o_ref, name)
+
+
+def test_repeatable_and_residency():
+    """Two calls give identical bits; changing weights in place needs
+    moe_hip_invalidate, after which the new weights are used."""
+    c = CONFIGS["c1"]
+    hw = host_layer(c["d"], c["F"], c["E"], c["k"], 3, 0.1, 0.02)
+    x = orc.synth((c["T"], c["d"]), 3, 0, 1.0)
+    a = mh.moe_forward(x, hw)
+    b = mh.moe_forward(x, hw)
+    for u, v in zip(a, b):
+        assert np.array_equal(np.ascontiguousarray(u).view(np.uint8),
+                              np.ascontiguousarray(v).view(np.uint8))
+    hw.wd *= 2.0                        # in place: same pointers
+    mh.check(mh.lib().moe_hip_invalidate(hw.weights))
+    out2, _, _ = mh.moe_forward(x, hw)
+    o_ref, _, _ = orc.moe_forward(x, hw)
+    assert_close(out2, o_ref, "after invalidate")
+
+
+def test_error_paths():
+    hw = host_layer(128, 512, 4, 2, 0, 0.02, 0.02)
+    bad = HostMoE(hw.wr, hw.wg, hw.wu, hw.wd, 5)        # top_k > n_experts
+    x = orc.synth((4, 128), 0, 0, 1.0)
+    with pytest.raises(mh.MoeHipError):
+        mh.moe_forward(x, bad)
+    odd = host_layer(96, 512, 4, 2, 0, 0.02, 0.02)      # d_model % 64 != 0
+    with pytest.raises(mh.MoeHipError):
+        mh.moe_forward(orc.synth((4, 96), 0, 0, 1.0), odd)
