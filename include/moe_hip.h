@@ -183,6 +183,12 @@ int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed,
                             uint64_t stream_id, float mean, float std,
                             void *stream);
 
+/* Expert-product kernels: 0 = automatic (skinny decode GEMVs when the
+ * average expert holds at most 16 rows, grouped MFMA GEMMs otherwise),
+ * 1 = always grouped GEMMs, 2 = always decode GEMVs (needs ffn_hidden % 64
+ * == 0).  Process-wide; both paths compute the same layer. */
+int moe_hip_set_expert_path(int mode);
+
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,
  * src/matrix.c:82-116) or glibc-expf restatement (which = 1) of x[i], the two
  * scalar exponentials the routing softmax uses. */
@@ -192,6 +198,11 @@ int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream
  * events: milliseconds for [route, dispatch, gate_up, down, combine]. */
 int moe_hip_last_timings(float *ms5);
 int moe_hip_set_timing(int on);
+
+/* Elapsed device time on the library stream between timer_start and
+ * timer_stop (which waits for the stream), in milliseconds. */
+int moe_hip_timer_start(void);
+int moe_hip_timer_stop(float *ms);
 
 /* ---------------------------------------------------------------------------
  * Device memory helpers for callers with no HIP binding of their own (the

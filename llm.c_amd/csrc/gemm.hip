@@ -32,12 +32,6 @@ constexpr int BM = kGemmBM;   // 128
 constexpr int KT = 32;
 constexpr int LDK = KT + 4;   // padded LDS row (144 B): conflict-free b128 reads
 
-// silu(g) * u in the vector form of swiglu (src/matrix.c:618-655).
-__device__ inline float swiglu1(float g, float u) {
-    float sig = 1.0f / (1.0f + exp_poly(-g));
-    return (g * sig) * u;
-}
-
 template <int MODE, int WN>
 __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     constexpr int BN = 64 * WN;
@@ -208,6 +202,8 @@ hipError_t launch_mode(const GemmArgs &a, hipStream_t s) {
 
 // out[t] = sum over slots of gw * y, one FMA per slot in slot order
 // (src/transformer.c:355-358 after contraction), optionally added into out.
+// With ksplit > 1 each slot's y is the sum of its split partials, added in
+// split order.
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int d4 = a.d >> 2;
     const size_t total = (size_t)a.T * d4;
@@ -216,8 +212,13 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int ki = 0; ki < a.k; ++ki) {
             const float w = a.gw[(size_t)t * a.k + ki];
-            const floatx4 y = *reinterpret_cast<const floatx4 *>(
-                a.ys + ((size_t)t * a.k + ki) * a.d + 4 * c);
+            const float *yp = a.ys + ((size_t)t * a.k + ki) * a.d + 4 * c;
+            floatx4 y = *reinterpret_cast<const floatx4 *>(yp);
+            for (int sp = 1; sp < a.ksplit; ++sp) {
+                const floatx4 p = *reinterpret_cast<const floatx4 *>(yp + sp * a.split_stride);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) y[j] = y[j] + p[j];
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[j] = fmaf(w, y[j], acc[j]);
         }

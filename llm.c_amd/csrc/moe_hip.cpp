@@ -30,7 +30,9 @@ int g_device = 0;
 hipStream_t g_stream = nullptr;
 bool g_timing = false;
 hipEvent_t g_ev[6] = {};
+hipEvent_t g_tev[2] = {};
 bool g_have_times = false;
+int g_path = 0;   // 0 auto, 1 grouped GEMM, 2 skinny decode GEMV
 
 int set_err(int code, const char *fmt, ...) {
     g_err = code;
@@ -93,14 +95,26 @@ struct DevBuf {
 
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
-    DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, perm, h, ys, stage;
+    DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, perm, h, ys, stage, counters;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
-                         &perm, &h, &ys, &stage};
+                         &perm, &h, &ys, &stage, &counters};
         for (DevBuf *b : all) b->release();
     }
 };
 Workspace g_ws;
+
+// Completion counter of the fused route+dispatch launch ("last workgroup
+// does the tail work"); it is zero between launches because the last
+// workgroup resets it, so it is cleared only when allocated.
+constexpr int kMaxCounters = 64;
+int ensure_counters() {
+    if (g_ws.counters.bytes >= sizeof(int) * kMaxCounters) return MOE_HIP_OK;
+    TRY(g_ws.counters.reserve(sizeof(int) * kMaxCounters));
+    HIP_TRY(hipMemsetAsync(g_ws.counters.p, 0, sizeof(int) * kMaxCounters, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
 
 // Residency cache for the drop-in entry points.
 struct Resident {
@@ -199,6 +213,7 @@ int moe_hip_init(int device) {
     HIP_TRY(hipSetDevice(device));
     HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     for (auto &ev : g_ev) HIP_TRY(hipEventCreate(&ev));
+    for (auto &ev : g_tev) HIP_TRY(hipEventCreate(&ev));
     g_device = device;
     g_init = true;
     return MOE_HIP_OK;
@@ -211,6 +226,7 @@ void moe_hip_shutdown(void) {
     g_resident.clear();
     g_ws.release_all();
     for (auto &ev : g_ev) (void)hipEventDestroy(ev);
+    for (auto &ev : g_tev) (void)hipEventDestroy(ev);
     (void)hipStreamDestroy(g_stream);
     g_stream = nullptr;
     g_init = false;
@@ -366,13 +382,16 @@ int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream
 
 static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
                       int *counts, int *offsets, int *tile_off, int *perm, hipStream_t s) {
+    TRY(ensure_counters());
     moe::RouteArgs ra{x, L->wr, L->bias, T, L->d, L->E, L->k, probs, ids, gw};
+    moe::DispatchArgs da{ids, T * L->k, L->E, moe::kGemmBM, counts, offsets, tile_off, perm,
+                         g_ws.counters.as<int>()};
     if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
-    HIP_TRY(moe::launch_route(ra, s));
-    if (g_timing) HIP_TRY(hipEventRecord(g_ev[1], s));
-    moe::DispatchArgs da{ids, T * L->k, L->E, moe::kGemmBM, counts, offsets, tile_off, perm};
-    HIP_TRY(moe::launch_dispatch(da, s));
-    if (g_timing) HIP_TRY(hipEventRecord(g_ev[2], s));
+    HIP_TRY(moe::launch_route_dispatch(ra, da, s));
+    if (g_timing) {
+        HIP_TRY(hipEventRecord(g_ev[1], s));
+        HIP_TRY(hipEventRecord(g_ev[2], s));
+    }
     return MOE_HIP_OK;
 }
 
@@ -402,6 +421,7 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
     const size_t n = (size_t)T * k;
     if (n > (size_t)0x7fffffff / (size_t)(F > d ? F : d))
         return set_err(MOE_HIP_ERR_UNSUPPORTED, "T*k*max(F,d) exceeds 32-bit indexing");
+
     TRY(g_ws.ids.reserve(sizeof(int) * n));
     TRY(g_ws.gw.reserve(sizeof(float) * n));
     TRY(g_ws.counts.reserve(sizeof(int) * E));
@@ -417,21 +437,58 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
     int *perm = g_ws.perm.as<int>();
     TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm, s));
 
-    const int max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
-    moe::GemmArgs gu{x, perm, k, L->wgu, g_ws.h.as<float>(), offsets, tile_off, E, d, 2 * F, F,
-                     max_mtiles};
-    HIP_TRY(moe::launch_gemm_gateup(gu, s));
-    if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
-    moe::GemmArgs dn{g_ws.h.as<float>(), perm, k, L->wdT, g_ws.ys.as<float>(), offsets, tile_off, E,
-                     F, d, d, max_mtiles};
-    HIP_TRY(moe::launch_gemm_down(dn, s));
-    if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
-    moe::CombineArgs ca{g_ws.ys.as<float>(), gw, out, T, d, k, accumulate};
+    const bool decode_ok = F % 64 == 0;
+    if (g_path == 2 && !decode_ok)
+        return set_err(MOE_HIP_ERR_UNSUPPORTED, "decode kernels need ffn_hidden %% 64 == 0");
+    const bool use_decode = g_path == 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
+    int ksplit = 1;
+    if (use_decode) {
+        ksplit = moe::decode_ksplit(d, F, E);
+        TRY(g_ws.ys.reserve(sizeof(float) * n * d * ksplit));
+        moe::DecodeArgs gu{x, perm, offsets, k, L->wgu, g_ws.h.as<float>(), d, F, E, 1, (int)n};
+        HIP_TRY(moe::launch_decode_gateup(gu, s));
+        if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
+        moe::DecodeArgs dn{g_ws.h.as<float>(), perm, offsets, k, L->wdT, g_ws.ys.as<float>(), d, F,
+                           E, ksplit, (int)n};
+        HIP_TRY(moe::launch_decode_down(dn, s));
+        if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
+    } else {
+        const int max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
+        moe::GemmArgs gu{x, perm, k, L->wgu, g_ws.h.as<float>(), offsets, tile_off, E, d, 2 * F, F,
+                         max_mtiles};
+        HIP_TRY(moe::launch_gemm_gateup(gu, s));
+        if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
+        moe::GemmArgs dn{g_ws.h.as<float>(), perm, k, L->wdT, g_ws.ys.as<float>(), offsets, tile_off,
+                         E, F, d, d, max_mtiles};
+        HIP_TRY(moe::launch_gemm_down(dn, s));
+        if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
+    }
+    moe::CombineArgs ca{g_ws.ys.as<float>(), gw, out, T, d, k, accumulate, ksplit, n * (size_t)d};
     HIP_TRY(moe::launch_combine(ca, s));
     if (g_timing) {
         HIP_TRY(hipEventRecord(g_ev[5], s));
         g_have_times = true;
     }
+    return MOE_HIP_OK;
+}
+
+int moe_hip_set_expert_path(int mode) {
+    if (mode < 0 || mode > 2) return set_err(MOE_HIP_ERR_ARG, "expert path mode %d", mode);
+    g_path = mode;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_timer_start(void) {
+    TRY(ensure_init());
+    HIP_TRY(hipEventRecord(g_tev[0], g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_timer_stop(float *ms) {
+    if (!ms) return set_err(MOE_HIP_ERR_ARG, "null output");
+    HIP_TRY(hipEventRecord(g_tev[1], g_stream));
+    HIP_TRY(hipEventSynchronize(g_tev[1]));
+    HIP_TRY(hipEventElapsedTime(ms, g_tev[0], g_tev[1]));
     return MOE_HIP_OK;
 }
 

@@ -33,7 +33,13 @@ struct DispatchArgs {
     int *offsets;        // [E + 1]
     int *tile_off;       // [E + 1] m-tile prefix; tile_off[E] = total m-tiles
     int *perm;           // [n]
+    int *counter;        // zeroed device int for the fused path (reset after use)
 };
+
+// Up to this many (token, slot) assignments, and router workgroups, the
+// router's last workgroup performs the dispatch itself.
+constexpr int kFusedDispatchMax = 4096;
+constexpr int kFusedDispatchMaxBlocks = 16;
 
 struct GemmArgs {
     // A rows: gate/up gathers x[perm[pos] / k]; down reads H[pos].
@@ -52,18 +58,35 @@ struct GemmArgs {
 };
 
 struct CombineArgs {
-    const float *ys;     // [T*k x d], slot-indexed expert outputs
+    const float *ys;     // [ksplit][T*k x d], slot-indexed expert outputs
     const float *gw;     // [T x k]
     float *out;          // [T x d]
     int T, d, k;
     int accumulate;      // out += combined instead of out = combined
+    int ksplit;          // partial products per slot (1 for the GEMM path)
+    size_t split_stride; // floats between consecutive partials
 };
 
-hipError_t launch_route(const RouteArgs &a, hipStream_t s);
-hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s);
+struct DecodeArgs {
+    const float *x;      // gate/up: x [T x d]; down: H [n x F]
+    const int *perm;     // [n]
+    const int *offsets;  // [E + 1]
+    int topk;
+    const float *w;      // packed weights (wgu or wdT)
+    float *out;          // gate/up: H [n x F]; down: Yp [ksplit][n][d] by slot
+    int d, F, E;
+    int ksplit;          // down: splits of the F reduction
+    int nslots;          // n = T * k
+};
+
+hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
+hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s);
+hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s);
+// Number of reduction splits the decode down-projection uses.
+int decode_ksplit(int d, int F, int E);
 
 // Weight packing (reference layout -> device layout) and its inverse.
 hipError_t launch_pack_gateup(const float *wg, const float *wu, float *dst,

@@ -79,4 +79,11 @@ __device__ inline float glibc_expf(float x) {
     return ftz_f((float)y);
 }
 
+// silu(g) * u in the vector form of swiglu (src/matrix.c:618-655): sigmoid
+// through the exp_avx2 polynomial and an IEEE division.
+__device__ inline float swiglu1(float g, float u) {
+    float sig = 1.0f / (1.0f + exp_poly(-g));
+    return (g * sig) * u;
+}
+
 }  // namespace moe

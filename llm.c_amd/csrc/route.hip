@@ -57,109 +57,6 @@ __device__ inline void softmax_row(float *row, int E) {
     for (int j = 0; j < E; ++j) row[j] = ftz_f(row[j] * inv);
 }
 
-constexpr int kRouteTM = 32;   // tokens per workgroup
-constexpr int kRouteKT = 32;   // K slice staged per step
-
-// One workgroup: 32 tokens x all experts.  Thread (tx, ty) owns tokens
-// ty + 16 i (i < 2) and experts tx + 16 j (j < RE).
-template <int RE>
-__global__ __launch_bounds__(256) void router_kernel(RouteArgs a) {
-    constexpr int EP = 16 * RE;
-    __shared__ float xs[kRouteKT][kRouteTM + 1];
-    __shared__ float ws[kRouteKT][EP];
-    __shared__ float lg[kRouteTM][EP + 1];
-    const int tid = threadIdx.x;
-    const int tx = tid & 15, ty = tid >> 4;
-    const int t0 = blockIdx.x * kRouteTM;
-    const int T = a.T, d = a.d, E = a.E;
-
-    float acc[2][RE];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < RE; ++j) acc[i][j] = 0.0f;
-
-    for (int k0 = 0; k0 < d; k0 += kRouteKT) {
-        // x tile, transposed into xs[k][token]; out-of-range reads as 0,
-        // which the zero-skip turns into "no update" (exact padding).
-        for (int idx = tid; idx < kRouteTM * kRouteKT; idx += 256) {
-            int r = idx / kRouteKT, c = idx % kRouteKT;
-            float v = 0.0f;
-            int t = t0 + r, kk = k0 + c;
-            if (t < T && kk < d) v = a.x[(size_t)t * d + kk];
-            uint32_t u = __float_as_uint(v);
-            if ((u & 0x7f800000u) == 0u) v = 0.0f;     // DAZ
-            xs[c][r] = v;
-        }
-        for (int idx = tid; idx < kRouteKT * EP; idx += 256) {
-            int r = idx / EP, c = idx % EP;
-            float v = 0.0f;
-            int kk = k0 + r;
-            if (kk < d && c < E) v = a.wr[(size_t)kk * E + c];
-            ws[r][c] = ftz_f(v);
-        }
-        __syncthreads();
-#pragma unroll 4
-        for (int kk = 0; kk < kRouteKT; ++kk) {
-            float xv0 = xs[kk][ty];
-            float xv1 = xs[kk][ty + 16];
-#pragma unroll
-            for (int j = 0; j < RE; ++j) {
-                float wv = ws[kk][tx + 16 * j];
-                acc[0][j] = (xv0 != 0.0f) ? fmaf(xv0, wv, acc[0][j]) : acc[0][j];
-                acc[1][j] = (xv1 != 0.0f) ? fmaf(xv1, wv, acc[1][j]) : acc[1][j];
-            }
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < RE; ++j) {
-            int e = tx + 16 * j;
-            if (e < E) {
-                float v = acc[i][j];
-                if (a.bias) v = v + a.bias[e];
-                lg[ty + 16 * i][e] = v;
-            }
-        }
-    __syncthreads();
-
-    // One thread per token: softmax, top-k, gate weights.
-    if (tid < kRouteTM && t0 + tid < T) {
-        const int t = t0 + tid;
-        float *row = &lg[tid][0];
-        softmax_row(row, E);
-        int ids[kMaxTopK];
-        const int k = a.k;
-        for (int ki = 0; ki < k; ++ki) {
-            float best = -1.0f;
-            int best_e = 0;
-            for (int e = 0; e < E; ++e) {
-                bool already = false;
-                for (int kj = 0; kj < ki; ++kj)
-                    if (ids[kj] == e) { already = true; break; }
-                if (!already && row[e] > best) { best = row[e]; best_e = e; }
-            }
-            ids[ki] = best_e;
-        }
-        float s = 0.0f;
-        for (int ki = 0; ki < k; ++ki) s = s + row[ids[ki]];
-        float inv = (s > 1e-9f) ? 1.0f / s : 0.0f;
-        for (int ki = 0; ki < k; ++ki) {
-            if (a.ids) a.ids[(size_t)t * k + ki] = ids[ki];
-            if (a.gw) a.gw[(size_t)t * k + ki] = ftz_f(row[ids[ki]] * inv);
-        }
-    }
-    __syncthreads();
-    if (a.probs) {
-        for (int idx = tid; idx < kRouteTM * E; idx += 256) {
-            int r = idx / E, e = idx % E;
-            if (t0 + r < T) a.probs[(size_t)(t0 + r) * E + e] = lg[r][e];
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Dispatch: one workgroup of 16 waves.  Wave w owns the contiguous run
 // [w*chunk, (w+1)*chunk) of the flattened assignments a = t*k + slot.
@@ -171,18 +68,18 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a) {
 // The result is the stable counting sort: pos(a) = offsets[e] + #{a' < a
 // with the same expert}.
 // ---------------------------------------------------------------------------
-constexpr int kDispWaves = 16;
-
-__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
-    __shared__ int hist[kDispWaves][kMaxExperts];
-    __shared__ int offs[kMaxExperts + 1];
+// Counting sort body run by the NW waves (64*NW threads) of one workgroup.
+// hist: [NW][kMaxExperts] ints of LDS, offs: [kMaxExperts + 1].
+template <int NW>
+__device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], int *offs) {
+    constexpr int NT = 64 * NW;
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int E = a.E, n = a.n;
-    for (int i = tid; i < kDispWaves * kMaxExperts; i += 1024) (&hist[0][0])[i] = 0;
+    for (int i = tid; i < NW * kMaxExperts; i += NT) (&hist[0][0])[i] = 0;
     __syncthreads();
 
-    const int chunk = ((n + kDispWaves * 64 - 1) / (kDispWaves * 64)) * 64;
+    const int chunk = ((n + NW * 64 - 1) / (NW * 64)) * 64;
     const int beg = w * chunk;
     const int end = min(n, beg + chunk);
     for (int i = beg + lane; i < end; i += 64) atomicAdd(&hist[w][a.ids[i]], 1);
@@ -190,7 +87,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
 
     if (tid < E) {
         int c = 0;
-        for (int ww = 0; ww < kDispWaves; ++ww) c += hist[ww][tid];
+        for (int ww = 0; ww < NW; ++ww) c += hist[ww][tid];
         a.counts[tid] = c;
         offs[tid + 1] = c;
     }
@@ -210,7 +107,7 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
     __syncthreads();
     if (tid < E) {
         int base = offs[tid];
-        for (int ww = 0; ww < kDispWaves; ++ww) {
+        for (int ww = 0; ww < NW; ++ww) {
             int c = hist[ww][tid];
             hist[ww][tid] = base;
             base += c;
@@ -242,6 +139,224 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
     }
 }
 
+constexpr int kDispWaves = 16;
+
+__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
+    __shared__ int hist[kDispWaves][kMaxExperts];
+    __shared__ int offs[kMaxExperts + 1];
+    dispatch_body<kDispWaves>(a, hist, offs);
+}
+
+// kend steps of the per-thread FMA chains from one LDS chunk.  The LDS reads
+// of 8 steps are issued ahead of their FMAs; each accumulator still adds its
+// terms in ascending k.  SKIP applies the reference's zero-skip.
+template <int RT, int RE, int TM, int EP, int KC, bool SKIP>
+__device__ inline void chain_steps(const float *xs, const float *ws, int kend, int tx, int ty,
+                                   float (&acc)[RT][RE]) {
+    int kk = 0;
+    for (; kk + 8 <= kend; kk += 8) {
+        float xv[8][RT], wv[8][RE];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+#pragma unroll
+            for (int i = 0; i < RT; ++i) xv[u][i] = xs[(kk + u) * TM + ty * RT + i];
+#pragma unroll
+            for (int j = 0; j < RE; ++j) wv[u][j] = ws[(kk + u) * EP + tx * RE + j];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int i = 0; i < RT; ++i)
+#pragma unroll
+                for (int j = 0; j < RE; ++j) {
+                    if (SKIP) acc[i][j] = (xv[u][i] != 0.0f) ? fmaf(xv[u][i], wv[u][j], acc[i][j])
+                                                            : acc[i][j];
+                    else      acc[i][j] = fmaf(xv[u][i], wv[u][j], acc[i][j]);
+                }
+    }
+    for (; kk < kend; ++kk) {
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+            const float xv = xs[kk * TM + ty * RT + i];
+#pragma unroll
+            for (int j = 0; j < RE; ++j) {
+                const float wv = ws[kk * EP + tx * RE + j];
+                if (SKIP) acc[i][j] = (xv != 0.0f) ? fmaf(xv, wv, acc[i][j]) : acc[i][j];
+                else      acc[i][j] = fmaf(xv, wv, acc[i][j]);
+            }
+        }
+    }
+}
+
+// Router workgroup: 16*RT tokens x 16*RE expert slots, 256 threads.  Thread
+// (tx, ty) owns tokens ty*RT .. ty*RT+RT-1 and experts tx*RE .. tx*RE+RE-1,
+// each an independent ascending FMA chain.  K is staged through LDS in
+// KC-wide chunks with the next chunk prefetched into registers.  When a
+// chunk holds no exact zero among the live x values the zero-skip select is
+// a no-op and the chunk runs plain FMAs (a uniform branch).
+template <int RT, int RE, int KC, bool FUSE>
+__global__ __launch_bounds__(256) void router_kernel(RouteArgs a, DispatchArgs da) {
+    constexpr int TM = 16 * RT, EP = 16 * RE;
+    constexpr int XQ = TM * KC / 4;                 // float4s of x per chunk
+    constexpr int XL = (XQ + 255) / 256;
+    constexpr int WQ = KC * EP;                     // floats of w per chunk
+    constexpr int WL = (WQ + 255) / 256;
+    __shared__ __align__(16) float xs[2][KC][TM];
+    __shared__ __align__(16) float ws[2][KC][EP];
+    __shared__ float lg[TM][EP + 1];
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const int t0 = blockIdx.x * TM;
+    const int T = a.T, d = a.d, E = a.E;
+
+    float acc[RT][RE];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < RE; ++j) acc[i][j] = 0.0f;
+
+    float4 rx[XL];
+    float rw[WL];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XL; ++i) {
+            int q = tid + 256 * i;
+            int r = q / (KC / 4), c4 = q % (KC / 4);
+            int t = t0 + r, kk = k0 + 4 * c4;
+            rx[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (q < XQ && t < T && kk < d)
+                rx[i] = *reinterpret_cast<const float4 *>(a.x + (size_t)t * d + kk);
+        }
+#pragma unroll
+        for (int i = 0; i < WL; ++i) {
+            int q = tid + 256 * i;
+            int r = q / EP, c = q % EP;
+            int kk = k0 + r;
+            rw[i] = (q < WQ && kk < d && c < E) ? a.wr[(size_t)kk * E + c] : 0.0f;
+        }
+    };
+    // Stores the prefetched chunk; returns 1 if a live x value is exactly 0
+    // (after DAZ), which selects the zero-skip path for the chunk.
+    auto sstore = [&](int buf, int k0) -> int {
+        int z = 0;
+#pragma unroll
+        for (int i = 0; i < XL; ++i) {
+            int q = tid + 256 * i;
+            if (q < XQ) {
+                int r = q / (KC / 4), c4 = q % (KC / 4);
+                bool live = (t0 + r < T) && (k0 + 4 * c4 < d);
+                float v[4] = {rx[i].x, rx[i].y, rx[i].z, rx[i].w};
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    float u = ftz_f(v[m]);
+                    if (u == 0.0f) { u = 0.0f; z |= live ? 1 : 0; }
+                    xs[buf][4 * c4 + m][r] = u;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < WL; ++i) {
+            int q = tid + 256 * i;
+            if (q < WQ) ws[buf][q / EP][q % EP] = ftz_f(rw[i]);
+        }
+        return z;
+    };
+
+    const int nchunk = (d + KC - 1) / KC;
+    gload(0);
+    int zero = __syncthreads_or(sstore(0, 0));
+    for (int c = 0; c < nchunk; ++c) {
+        const int buf = c & 1;
+        const int k0 = c * KC;
+        if (c + 1 < nchunk) gload(k0 + KC);
+        const int kend = min(KC, d - k0);
+        if (!zero) chain_steps<RT, RE, TM, EP, KC, false>(&xs[buf][0][0], &ws[buf][0][0], kend,
+                                                          tx, ty, acc);
+        else       chain_steps<RT, RE, TM, EP, KC, true>(&xs[buf][0][0], &ws[buf][0][0], kend,
+                                                         tx, ty, acc);
+        int z = 0;
+        if (c + 1 < nchunk) z = sstore(buf ^ 1, k0 + KC);
+        zero = __syncthreads_or(z);
+    }
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < RE; ++j) {
+            int e = tx * RE + j;
+            if (e < E) {
+                float v = acc[i][j];
+                if (a.bias) v = v + a.bias[e];
+                lg[ty * RT + i][e] = v;
+            }
+        }
+    __syncthreads();
+
+    // One thread per token: softmax, top-k, gate weights.
+    if (tid < TM && t0 + tid < T) {
+        const int t = t0 + tid;
+        float *row = &lg[tid][0];
+        softmax_row(row, E);
+        // The reference's "already chosen" scan over ids[0..ki) is a set
+        // membership test; a bit set keeps it (and every index below) in
+        // registers.  The gate weight uses probs[ids[ki]], as the reference
+        // does even when no candidate beat -1.
+        uint64_t chosen[kMaxExperts / 64] = {};
+        float pk[kMaxTopK];
+        int idk[kMaxTopK];
+        const int k = a.k;
+#pragma unroll
+        for (int ki = 0; ki < kMaxTopK; ++ki) {
+            if (ki < k) {
+                float best = -1.0f;
+                int best_e = 0;
+                for (int e = 0; e < E; ++e) {
+                    const bool already = (chosen[e >> 6] >> (e & 63)) & 1ull;
+                    if (!already && row[e] > best) { best = row[e]; best_e = e; }
+                }
+                chosen[best_e >> 6] |= 1ull << (best_e & 63);
+                idk[ki] = best_e;
+                pk[ki] = row[best_e];
+            }
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int ki = 0; ki < kMaxTopK; ++ki)
+            if (ki < k) s = s + pk[ki];
+        float inv = (s > 1e-9f) ? 1.0f / s : 0.0f;
+#pragma unroll
+        for (int ki = 0; ki < kMaxTopK; ++ki) {
+            if (ki < k) {
+                if (a.ids) a.ids[(size_t)t * k + ki] = idk[ki];
+                if (a.gw) a.gw[(size_t)t * k + ki] = ftz_f(pk[ki] * inv);
+            }
+        }
+    }
+    __syncthreads();
+    if (a.probs) {
+        for (int idx = tid; idx < TM * E; idx += 256) {
+            int r = idx / E, e = idx % E;
+            if (t0 + r < T) a.probs[(size_t)(t0 + r) * E + e] = lg[r][e];
+        }
+    }
+    if (FUSE) {
+        // The last workgroup to finish runs the dispatch over every token's
+        // ids (release/acquire through the device-scope fences), then resets
+        // the counter for the next launch.
+        __shared__ int hist[4][kMaxExperts];
+        __shared__ int offs[kMaxExperts + 1];
+        __shared__ int is_last;
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) is_last = atomicAdd(da.counter, 1) == (int)gridDim.x - 1;
+        __syncthreads();
+        if (is_last) {
+            __threadfence();
+            dispatch_body<4>(da, hist, offs);
+            if (tid == 0) *da.counter = 0;
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void eval_exp_kernel(int which, const float *x, float *y,
                                                       size_t n) {
     for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
@@ -257,20 +372,47 @@ hipError_t launch_eval_exp(int which, const float *x, float *y, size_t n, hipStr
     return hipGetLastError();
 }
 
-hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
-    if (a.T <= 0) return hipSuccess;
-    dim3 grid((a.T + kRouteTM - 1) / kRouteTM);
-    if (a.E <= 16)       hipLaunchKernelGGL(router_kernel<1>, grid, dim3(256), 0, s, a);
-    else if (a.E <= 32)  hipLaunchKernelGGL(router_kernel<2>, grid, dim3(256), 0, s, a);
-    else if (a.E <= 64)  hipLaunchKernelGGL(router_kernel<4>, grid, dim3(256), 0, s, a);
-    else if (a.E <= 128) hipLaunchKernelGGL(router_kernel<8>, grid, dim3(256), 0, s, a);
-    else return hipErrorInvalidValue;
+namespace {
+
+template <bool FUSE>
+hipError_t launch_router(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
+    const bool big = a.T >= 2048;
+    const int TM = big ? 64 : 16;
+    dim3 grid((a.T + TM - 1) / TM), block(256);
+    if (big) {
+        if (a.E <= 16)       hipLaunchKernelGGL((router_kernel<4, 1, 64, FUSE>), grid, block, 0, s, a, da);
+        else if (a.E <= 32)  hipLaunchKernelGGL((router_kernel<4, 2, 64, FUSE>), grid, block, 0, s, a, da);
+        else if (a.E <= 64)  hipLaunchKernelGGL((router_kernel<4, 4, 32, FUSE>), grid, block, 0, s, a, da);
+        else if (a.E <= 128) hipLaunchKernelGGL((router_kernel<4, 8, 16, FUSE>), grid, block, 0, s, a, da);
+        else return hipErrorInvalidValue;
+    } else {
+        if (a.E <= 16)       hipLaunchKernelGGL((router_kernel<1, 1, 128, FUSE>), grid, block, 0, s, a, da);
+        else if (a.E <= 32)  hipLaunchKernelGGL((router_kernel<1, 2, 128, FUSE>), grid, block, 0, s, a, da);
+        else if (a.E <= 64)  hipLaunchKernelGGL((router_kernel<1, 4, 64, FUSE>), grid, block, 0, s, a, da);
+        else if (a.E <= 128) hipLaunchKernelGGL((router_kernel<1, 8, 32, FUSE>), grid, block, 0, s, a, da);
+        else return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_dispatch(const DispatchArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a);
+}  // namespace
+
+// Routing followed by dispatch.  For small launches (at most
+// kFusedDispatchMax assignments and kFusedDispatchMaxBlocks router
+// workgroups) the router's last workgroup sorts them in the same launch; its
+// device-scope fences write back and invalidate L2, which is cheap for a
+// handful of workgroups only.  Otherwise a separate 16-wave dispatch kernel
+// sorts them.
+hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
+    if (a.T <= 0) return hipSuccess;
+    const int grid = (a.T + (a.T >= 2048 ? 64 : 16) - 1) / (a.T >= 2048 ? 64 : 16);
+    if (da.n <= kFusedDispatchMax && grid <= kFusedDispatchMaxBlocks && da.counter)
+        return launch_router<true>(a, da, s);
+    hipError_t e = launch_router<false>(a, da, s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, da);
     return hipGetLastError();
 }
+
 
 }  // namespace moe

@@ -58,6 +58,9 @@ SIGNATURES = {
     "moe_hip_eval_exp": (C.c_int, [C.c_int, _P, _P, C.c_size_t, _P]),
     "moe_hip_last_timings": (C.c_int, [_F]),
     "moe_hip_set_timing": (C.c_int, [C.c_int]),
+    "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
+    "moe_hip_timer_start": (C.c_int, []),
+    "moe_hip_timer_stop": (C.c_int, [_F]),
     "moe_hip_dev_alloc": (C.c_int, [C.POINTER(_P), C.c_size_t]),
     "moe_hip_dev_free": (C.c_int, [_P]),
     "moe_hip_memcpy": (C.c_int, [_P, _P, C.c_size_t, C.c_int]),
@@ -224,8 +227,24 @@ def synchronize():
     check(lib().moe_hip_synchronize())
 
 
+def set_expert_path(mode):
+    """0 automatic, 1 grouped GEMMs, 2 skinny decode GEMVs."""
+    check(lib().moe_hip_set_expert_path(int(mode)))
+
+
 def set_timing(on):
     check(lib().moe_hip_set_timing(1 if on else 0))
+
+
+def timer_start():
+    check(lib().moe_hip_timer_start())
+
+
+def timer_stop():
+    """Milliseconds of device time since timer_start (waits for the stream)."""
+    ms = C.c_float()
+    check(lib().moe_hip_timer_stop(C.byref(ms)))
+    return ms.value
 
 
 def last_timings():

@@ -310,3 +310,32 @@ def test_error_paths():
     odd = host_layer(96, 512, 4, 2, 0, 0.02, 0.02)      # d_model % 64 != 0
     with pytest.raises(mh.MoeHipError):
         mh.moe_forward(orc.synth((4, 96), 0, 0, 1.0), odd)
+
+
+FORCED_PATH_CASES = [
+    # name, T, d, F, E, k, path (1 = grouped GEMMs, 2 = decode GEMVs)
+    ("c4_gemv", 64, 512, 2048, 16, 2, 2),
+    ("c4_gemm", 64, 512, 2048, 16, 2, 1),
+    ("multipass_gemv", 200, 128, 256, 4, 2, 2),     # ~100 rows per expert: 4 passes
+    ("kchunks_gemv", 48, 1024, 512, 16, 2, 2),      # d = 1024: two K chunks
+    ("tiny_gemv", 5, 64, 64, 8, 3, 2),
+    ("wide_gemm", 300, 256, 1024, 8, 2, 1),
+]
+
+
+@pytest.mark.parametrize("name,T,d,F,E,k,path", FORCED_PATH_CASES,
+                         ids=[c[0] for c in FORCED_PATH_CASES])
+def test_forced_expert_paths(name, T, d, F, E, k, path):
+    """Both expert-product paths (grouped MFMA GEMMs and the skinny decode
+    GEMVs) against the oracle, whatever the automatic choice would be."""
+    hw = host_layer(d, F, E, k, 21, 0.1, 0.02)
+    x = orc.synth((T, d), 21, 0, 1.0)
+    mh.set_expert_path(path)
+    try:
+        out, probs, ids = mh.moe_forward(x, hw)
+    finally:
+        mh.set_expert_path(0)
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw)
+    assert np.array_equal(bits(probs), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    assert_close(out, o_ref, name)
