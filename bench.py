@@ -168,7 +168,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
                     help="run one section only (for profiling); prints its JSON to stderr")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -178,6 +178,16 @@ def main():
     import moe_hip as mh
     mh.check(mh.lib().moe_hip_init(0))
 
+    if args.only == "copy":
+        # Calibration for the HBM traffic counters: one 1 GiB device-to-device
+        # copy (1 GiB read + 1 GiB written).
+        n = 1 << 28
+        a, b = mh.DeviceArray((n,)), mh.DeviceArray((n,))
+        mh.fill_normal_dev(a.ptr, n, 1, 0, 0.0, 1.0)
+        mh.synchronize()
+        mh.check(mh.lib().moe_hip_memcpy(b.ptr, a.ptr, 4 * n, 3))
+        log("copy", json.dumps({"bytes": 4 * n}))
+        return
     if args.only == "decode":
         log("decode", json.dumps(decode(mh, args.steps, args.warmup)))
         return
@@ -197,6 +207,13 @@ def main():
 
     ms = pre["ms"]
     gu_tflops = pre["gateup_tflops"]
+    # HBM bytes per gate/up launch come from the rocprofv3 FETCH_SIZE /
+    # WRITE_SIZE passes summarised in profiles/ (counters cannot be read from
+    # inside this process); null when that summary is absent.
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "moe_prefill_gateup_traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
     line = {
         "metric": METRIC,
         "value": pre["T"] / (ms * 1e-3),
@@ -215,7 +232,7 @@ def main():
                    "d_ff": pre["F"], "n_experts": pre["E"], "top_k": pre["k"]},
         "roofline": {"bound": "mfma", "kernel": "grouped gate/up GEMM",
                      "achieved": gu_tflops, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": gu_tflops / PEAK_FP32_MFMA_TFLOPS, "traffic": None},
+                     "frac": gu_tflops / PEAK_FP32_MFMA_TFLOPS, "traffic": traffic},
         "layer_mfma_frac": pre["layer_tflops"] / PEAK_FP32_MFMA_TFLOPS,
         "prefill_phase_ms": dict(zip(["route", "dispatch", "gate_up", "down", "combine"],
                                      pre["phase_ms"])),

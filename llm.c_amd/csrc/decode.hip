@@ -6,6 +6,8 @@
 // registers: a lane holds a 16-byte piece of one weight row (K contiguous),
 // the MFMA's k-row h (lane/16) takes the piece's 4 elements in turn, and the
 // activations come from LDS as 128-bit reads with the same k mapping.
+// Weights are in the unit layout (16 x 16 tiles in MFMA operand order, see
+// gemm.hip): a K step of 16 is one contiguous 1 KB unit per wave.
 //   gate/up: grid = E x (F/64); wave w of a workgroup owns features
 //            64*fb + 16w .. +15 and both their gate and up rows, so the SwiGLU
 //            epilogue is lane-local and writes H [n x F] (dispatch order).
@@ -23,6 +25,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kRows = 32;        // rows per pass (two 16-row MFMA blocks)
 constexpr int kChunk = 512;      // K elements staged per LDS fill
 constexpr int kLd = kChunk + 4;  // padded LDS row
+
+constexpr int kUnit = 256;      // floats per 16 x 16 unit = one K step of 16
 
 __device__ inline floatx4 mfma16(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -75,7 +79,7 @@ __device__ inline void gemv_first(const float *p0, const float *p1, int nq,
 #pragma unroll
     for (int u = 0; u < kU; ++u)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) cur[u][b] = *reinterpret_cast<const floatx4 *>(pb[b] + 16 * u);
+        for (int b = 0; b < NB; ++b) cur[u][b] = *reinterpret_cast<const floatx4 *>(pb[b] + kUnit * u);
 }
 
 // cur must hold the first kU steps (gemv_first) when nq >= kU.
@@ -93,7 +97,7 @@ __device__ inline void gemv_loop(const float *p0, const float *p1, const float *
             for (int u = 0; u < kU; ++u)
 #pragma unroll
                 for (int b = 0; b < NB; ++b)
-                    nxt[u][b] = *reinterpret_cast<const floatx4 *>(pb[b] + 16 * (q + kU + u));
+                    nxt[u][b] = *reinterpret_cast<const floatx4 *>(pb[b] + kUnit * (q + kU + u));
         }
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
@@ -118,7 +122,7 @@ __device__ inline void gemv_loop(const float *p0, const float *p1, const float *
     for (; q < nq; ++q) {
         floatx4 w[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) w[b] = *reinterpret_cast<const floatx4 *>(pb[b] + 16 * q);
+        for (int b = 0; b < NB; ++b) w[b] = *reinterpret_cast<const floatx4 *>(pb[b] + kUnit * q);
         floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 16 * q);
         floatx4 a1;
         if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as + 16 * kLd + 16 * q);
@@ -142,9 +146,11 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, h = lane >> 4;
     const int f = fb * 64 + wave * 16 + j;
-    const size_t grow = (size_t)64 * (f >> 5) + (f & 31);
-    const float *pg = a.w + ((size_t)e * 2 * a.F + grow) * a.d + 4 * h;
-    const float *pu = pg + (size_t)32 * a.d;
+    // Gate rows of this wave's 16 features form unit row nbg; up rows are
+    // 32 packed rows (2 unit rows) further.
+    const int nbg = 8 * fb + 4 * (wave >> 1) + (wave & 1);
+    const float *pg = a.w + (size_t)e * 2 * a.F * a.d + (size_t)nbg * (a.d / 16) * kUnit + 4 * lane;
+    const float *pu = pg + (size_t)2 * (a.d / 16) * kUnit;
 
     for (int r0 = 0; r0 < cnt; r0 += kRows) {
         const int rows = min(kRows, cnt - r0);
@@ -158,13 +164,13 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
             floatx4 stg[kStageMax];
             floatx4 cur[Unroll<2>::kU][2];
             stage_load<true>(stg, a.x, a.d, a.perm, a.topk, base + r0, rows, k0, kc);
-            gemv_first<2>(pg + k0, pu + k0, kc / 16, cur);
+            gemv_first<2>(pg + 16 * k0, pu + 16 * k0, kc / 16, cur);
             __syncthreads();
             stage_store(stg, xs, kc);
             __syncthreads();
             const float *as = xs + j * kLd + 4 * h;
-            if (rows > 16) gemv_loop<2, 2>(pg + k0, pu + k0, as, kc / 16, acc, cur);
-            else           gemv_loop<2, 1>(pg + k0, pu + k0, as, kc / 16, acc, cur);
+            if (rows > 16) gemv_loop<2, 2>(pg + 16 * k0, pu + 16 * k0, as, kc / 16, acc, cur);
+            else           gemv_loop<2, 1>(pg + 16 * k0, pu + 16 * k0, as, kc / 16, acc, cur);
         }
         // 16x16 accumulator: lane holds rows 4*(lane/16) + r, column lane%16.
 #pragma unroll
@@ -192,7 +198,8 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, h = lane >> 4;
     const int col = cb * 64 + wave * 16 + j;
-    const float *pw = a.w + ((size_t)e * a.d + col) * a.F + kbeg + 4 * h;
+    const float *pw = a.w + (size_t)e * a.d * a.F +
+                      ((size_t)(cb * 4 + wave) * (a.F / 16) + kbeg / 16) * kUnit + 4 * lane;
     const size_t nslots = (size_t)a.nslots;
 
     for (int r0 = 0; r0 < cnt; r0 += kRows) {
@@ -203,13 +210,13 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
             floatx4 stg[kStageMax];
             floatx4 cur[Unroll<1>::kU][1];
             stage_load<false>(stg, a.x, a.F, nullptr, 1, base + r0, rows, kbeg + k0, kc);
-            gemv_first<1>(pw + k0, nullptr, kc / 16, cur);
+            gemv_first<1>(pw + 16 * k0, nullptr, kc / 16, cur);
             __syncthreads();
             stage_store(stg, hs, kc);
             __syncthreads();
             const float *as = hs + j * kLd + 4 * h;
-            if (rows > 16) gemv_loop<1, 2>(pw + k0, nullptr, as, kc / 16, acc, cur);
-            else           gemv_loop<1, 1>(pw + k0, nullptr, as, kc / 16, acc, cur);
+            if (rows > 16) gemv_loop<1, 2>(pw + 16 * k0, nullptr, as, kc / 16, acc, cur);
+            else           gemv_loop<1, 1>(pw + 16 * k0, nullptr, as, kc / 16, acc, cur);
         }
 #pragma unroll
         for (int b = 0; b < 2; ++b)

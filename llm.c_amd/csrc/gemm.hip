@@ -1,11 +1,16 @@
 // gemm.hip — grouped expert GEMMs on the fp32 matrix cores of gfx950, plus
 // the combine, weight packing and synthetic fill kernels.
 //
-// Layout (device, packed once at upload):
-//   gate/up  wgu [E][2F][d]: for feature block fb (32 features) rows
-//            64*fb + c hold gate feature 32*fb + c (c < 32) and up feature
-//            32*fb + c - 32 (c >= 32); every row is K (= d) contiguous.
-//   down     wdT [E][d][F]: row n holds W_down[:, n] (K = F contiguous).
+// Layout (device, packed once at upload), per expert a matrix of N packed
+// rows by K, stored as 16 x 16 tiles ("units", 1 KB) in MFMA operand order:
+//   unit (nb, qb) at ((nb * K/16) + qb) * 256 floats holds rows
+//   16nb..16nb+15, k = 16qb..16qb+15; element (row 16nb + j, k = 16qb + 4h + s)
+//   sits at h*64 + j*4 + s, so lane 16h + j of a wave loads its 16-byte
+//   piece at lane*4 and one wave instruction reads one contiguous unit; the
+//   units of one row block follow each other along K.
+//   gate/up  wgu [E][2F rows][d]: packed rows 64*fb + c hold gate feature
+//            32*fb + c (c < 32) and up feature 32*fb + c - 32 (c >= 32).
+//   down     wdT [E][d rows][F]: row n holds W_down[:, n].
 // The rows of one expert's m-tile are consecutive dispatch positions
 // offsets[e] + m; gate/up gathers them straight from x through perm.
 //
@@ -56,7 +61,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     const int row0 = a.offsets[e] + (mtg - a.tile_off[e]) * BM;
     const int rows = min(BM, a.offsets[e + 1] - row0);
     const int K = a.K;
-    const float *B = a.b + ((size_t)e * a.N + (size_t)nt * BN) * K;
+    const float *B = a.b + (size_t)e * a.N * K;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -80,14 +85,16 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
             a_src[i] = nullptr;
         }
     }
+    // B tile = (BN/16) x 2 units; 64 consecutive threads load one unit.
     const float *b_src[B_LD];
     int b_dst[B_LD];
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
-        int q = tid + NT * i;
-        int r = q >> 3, c4 = q & 7;
-        b_dst[i] = r * LDK + 4 * c4;
-        b_src[i] = B + (size_t)r * K + 4 * c4;
+        int g = tid + NT * i;
+        int u = g >> 6, l = g & 63;
+        int nbl = u >> 1, qbl = u & 1;
+        b_dst[i] = (nbl * 16 + (l & 15)) * LDK + qbl * 16 + (l >> 4) * 4;
+        b_src[i] = B + ((size_t)(nt * (BN / 16) + nbl) * (K / 16) + qbl) * 256 + 4 * l;
     }
 
     floatx4 ra[A_LD], rb[B_LD];
@@ -98,7 +105,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                              : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < B_LD; ++i)
-            rb[i] = *reinterpret_cast<const floatx4 *>(b_src[i] + k0);
+            rb[i] = *reinterpret_cast<const floatx4 *>(b_src[i] + (size_t)16 * k0);
     };
     auto sstore = [&](int buf) {
         float *as = As + buf * BM * LDK;
@@ -234,47 +241,35 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     }
 }
 
-// Transposes through a 32 x 33 LDS tile.
-// pack gate/up: src [d x F] (gate, up) -> dst [2F x d] interleaved rows.
-__global__ __launch_bounds__(256) void pack_gateup_kernel(const float *wg, const float *wu,
-                                                           float *dst, int d, int F, int unpack) {
+// Packs source matrix src [K x N] (reference layout) into the unit layout
+// (unpack != 0: the inverse).  Source column c goes to packed row
+// c (mode 0, down), 64*(c/32) + c%32 (mode 1, gate) or that + 32 (mode 2,
+// up).  One workgroup moves a 32 x 32 block = 4 units through LDS.
+__global__ __launch_bounds__(256) void pack_kernel(float *src, float *dst, int K, int N,
+                                                    int mode, int unpack) {
     __shared__ float tile[32][33];
-    const int f0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
-    const float *src = blockIdx.z ? wu : wg;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8
+    const int c0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    const int row0 = mode == 0 ? c0 : 64 * (c0 >> 5) + (mode == 2 ? 32 : 0);
+    const int t = threadIdx.x;
+    const int h = t >> 6, j = (t >> 2) & 15, sx = t & 3;
     if (!unpack) {
-        for (int r = ty; r < 32; r += 8)
-            tile[r][tx] = src[(size_t)(k0 + r) * F + f0 + tx];          // [k][f]
+        for (int r = ty; r < 32; r += 8) tile[r][tx] = src[(size_t)(k0 + r) * N + c0 + tx];
         __syncthreads();
-        for (int r = ty; r < 32; r += 8) {
-            int f = f0 + r;
-            size_t row = (size_t)64 * (f >> 5) + (f & 31) + (blockIdx.z ? 32 : 0);
-            dst[row * d + k0 + tx] = tile[tx][r];
+        for (int u = 0; u < 4; ++u) {
+            const int nbl = u >> 1, qbl = u & 1;
+            const size_t unit = (size_t)((row0 >> 4) + nbl) * (K / 16) + (k0 >> 4) + qbl;
+            dst[unit * 256 + t] = tile[qbl * 16 + 4 * h + sx][nbl * 16 + j];
         }
     } else {
-        float *out = const_cast<float *>(src);
-        for (int r = ty; r < 32; r += 8) {
-            int f = f0 + r;
-            size_t row = (size_t)64 * (f >> 5) + (f & 31) + (blockIdx.z ? 32 : 0);
-            tile[r][tx] = dst[row * d + k0 + tx];                      // [f][k]
+        for (int u = 0; u < 4; ++u) {
+            const int nbl = u >> 1, qbl = u & 1;
+            const size_t unit = (size_t)((row0 >> 4) + nbl) * (K / 16) + (k0 >> 4) + qbl;
+            tile[qbl * 16 + 4 * h + sx][nbl * 16 + j] = dst[unit * 256 + t];
         }
         __syncthreads();
-        for (int r = ty; r < 32; r += 8)
-            out[(size_t)(k0 + r) * F + f0 + tx] = tile[tx][r];
+        for (int r = ty; r < 32; r += 8) src[(size_t)(k0 + r) * N + c0 + tx] = tile[r][tx];
     }
-}
-
-// pack down: src [F x d] -> dst [d x F] (plain transpose); unpack inverts.
-__global__ __launch_bounds__(256) void transpose_kernel(const float *src, float *dst,
-                                                         int R, int Cc) {
-    __shared__ float tile[32][33];
-    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-    for (int r = ty; r < 32; r += 8)
-        tile[r][tx] = src[(size_t)(r0 + r) * Cc + c0 + tx];
-    __syncthreads();
-    for (int r = ty; r < 32; r += 8)
-        dst[(size_t)(c0 + r) * R + r0 + tx] = tile[tx][r];
 }
 
 __global__ __launch_bounds__(256) void fill_normal_kernel(float *dst, size_t n, uint64_t seed,
@@ -306,28 +301,29 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
 
 hipError_t launch_pack_gateup(const float *wg, const float *wu, float *dst, int d, int F,
                               hipStream_t s) {
-    dim3 grid(F / 32, d / 32, 2);
-    hipLaunchKernelGGL(pack_gateup_kernel, grid, dim3(256), 0, s, wg, wu, dst, d, F, 0);
+    dim3 grid(F / 32, d / 32);
+    hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, const_cast<float *>(wg), dst, d, F, 1, 0);
+    hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, const_cast<float *>(wu), dst, d, F, 2, 0);
     return hipGetLastError();
 }
 
 hipError_t launch_unpack_gateup(const float *src, float *wg, float *wu, int d, int F,
                                 hipStream_t s) {
-    dim3 grid(F / 32, d / 32, 2);
-    hipLaunchKernelGGL(pack_gateup_kernel, grid, dim3(256), 0, s, wg, wu,
-                       const_cast<float *>(src), d, F, 1);
+    dim3 grid(F / 32, d / 32);
+    hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, wg, const_cast<float *>(src), d, F, 1, 1);
+    hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, wu, const_cast<float *>(src), d, F, 2, 1);
     return hipGetLastError();
 }
 
 hipError_t launch_pack_down(const float *wd, float *dst, int F, int d, hipStream_t s) {
     dim3 grid(d / 32, F / 32);
-    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, s, wd, dst, F, d);
+    hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, const_cast<float *>(wd), dst, F, d, 0, 0);
     return hipGetLastError();
 }
 
 hipError_t launch_unpack_down(const float *src, float *wd, int F, int d, hipStream_t s) {
-    dim3 grid(F / 32, d / 32);
-    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, s, src, wd, d, F);
+    dim3 grid(d / 32, F / 32);
+    hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, wd, const_cast<float *>(src), F, d, 0, 1);
     return hipGetLastError();
 }
 

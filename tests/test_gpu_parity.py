@@ -339,3 +339,22 @@ def test_forced_expert_paths(name, T, d, F, E, k, path):
     assert np.array_equal(bits(probs), bits(p_ref))
     assert np.array_equal(ids, i_ref)
     assert_close(out, o_ref, name)
+
+
+def test_weight_pack_roundtrip():
+    """Upload packs the reference-layout matrices into 16 x 16 units; reading
+    an expert back must return the same bits (device synth and host synth
+    agree as well)."""
+    d, F, E, k = 128, 96, 3, 2
+    hw = host_layer(d, F, E, k, 31, 0.1, 0.02)
+    layer = mh.Layer(d, F, E, k)
+    layer.load(hw)
+    for e in range(E):
+        wg, wu, wd = layer.get_expert(e)
+        assert np.array_equal(bits(wg), bits(hw.wg[e]))
+        assert np.array_equal(bits(wu), bits(hw.wu[e]))
+        assert np.array_equal(bits(wd), bits(hw.wd[e]))
+    layer.fill_synthetic(31, 0.1, 0.02)
+    wg, wu, wd = layer.get_expert(2)
+    assert np.array_equal(bits(wd), bits(hw.wd[2]))
+    layer.close()
