@@ -68,7 +68,9 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     const int wm = wave & 1, wn = wave >> 1;
     const int li = lane & 31, lh = lane >> 5;
 
-    // Per-thread global source rows for the A and B tiles.
+    // Per-thread global source rows for the A tile.  Rows past the expert's
+    // last row reuse its last row: their accumulator rows are never stored,
+    // and unconditional loads keep the K loop free of exec-masked branches.
     const float *a_src[A_LD];
     int a_dst[A_LD];
 #pragma unroll
@@ -76,14 +78,11 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         int q = tid + NT * i;
         int r = q >> 3, c4 = q & 7;
         a_dst[i] = r * LDK + 4 * c4;
-        if (r < rows) {
-            size_t src_row;
-            if (MODE == 0) src_row = (size_t)(a.perm[row0 + r] / a.topk);
-            else           src_row = (size_t)(row0 + r);
-            a_src[i] = a.a + src_row * K + 4 * c4;
-        } else {
-            a_src[i] = nullptr;
-        }
+        const int rr = min(r, rows - 1);
+        size_t src_row;
+        if (MODE == 0) src_row = (size_t)(a.perm[row0 + rr] / a.topk);
+        else           src_row = (size_t)(row0 + rr);
+        a_src[i] = a.a + src_row * K + 4 * c4;
     }
     // B tile = (BN/16) x 2 units; 64 consecutive threads load one unit.
     const float *b_src[B_LD];
@@ -101,8 +100,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     auto gload = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i)
-            ra[i] = a_src[i] ? *reinterpret_cast<const floatx4 *>(a_src[i] + k0)
-                             : floatx4{0.f, 0.f, 0.f, 0.f};
+            ra[i] = *reinterpret_cast<const floatx4 *>(a_src[i] + k0);
 #pragma unroll
         for (int i = 0; i < B_LD; ++i)
             rb[i] = *reinterpret_cast<const floatx4 *>(b_src[i] + (size_t)16 * k0);
