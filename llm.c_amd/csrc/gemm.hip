@@ -65,7 +65,13 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    // Waves are dealt to the 4 SIMDs in turn, so with 8 waves SIMD s runs
+    // waves s and s + 4; wm = wave / WN makes them an upper-half and a
+    // lower-half wave.  When an expert's last tile is short, the MFMAs the
+    // lower-half wave skips leave its SIMD to the upper-half wave.
+    const int wm = wave / WN, wn = wave % WN;
+    // Valid 32-row MFMA blocks of this wave (0, 1 or 2); uniform per wave.
+    const int nmb = max(0, min(2, (rows - wm * 64 + 31) / 32));
     const int li = lane & 31, lh = lane >> 5;
 
     // Per-thread global source rows for the A tile.  Rows past the expert's
@@ -131,21 +137,40 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         if (kt + 1 < nk) gload((kt + 1) * KT);
         const float *as = As + buf * BM * LDK + (wm * 64 + li) * LDK + 16 * lh;
         const float *bs = Bs + buf * BN * LDK + (wn * 64 + li) * LDK + 16 * lh;
+        if (nmb == 2) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
-            floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * LDK + 4 * q);
-            floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 4 * q);
-            floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 32 * LDK + 4 * q);
+            for (int q = 0; q < 4; ++q) {
+                floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
+                floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * LDK + 4 * q);
+                floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 4 * q);
+                floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 32 * LDK + 4 * q);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b1[s], acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b0[s], acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc[1][1], 0, 0, 0);
+                for (int s = 0; s < 4; ++s) {
+                    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
+                    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b1[s], acc[0][1], 0, 0, 0);
+                    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b0[s], acc[1][0], 0, 0, 0);
+                    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc[1][1], 0, 0, 0);
+                }
+                // The next tile's LDS fill goes in mid-block, while the other
+                // wave of this SIMD keeps the matrix unit busy.
+                if (q == 1 && kt + 1 < nk) sstore(buf ^ 1);
             }
+        } else {
+            if (nmb == 1) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
+                    floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 4 * q);
+                    floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 32 * LDK + 4 * q);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
+                        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b1[s], acc[0][1], 0, 0, 0);
+                    }
+                }
+            }
+            if (kt + 1 < nk) sstore(buf ^ 1);
         }
-        if (kt + 1 < nk) sstore(buf ^ 1);
         __syncthreads();
     }
 
