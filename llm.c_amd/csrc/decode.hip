@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
                 const int row = b * 16 + 4 * h + r;
                 if (row < rows)
                     a.out[(size_t)(base + r0 + row) * a.F + f] =
-                        swiglu1(acc[b][0][r], acc[b][1][r]);
+                        swiglu_fast(acc[b][0][r], acc[b][1][r]);
             }
     }
 }

@@ -52,12 +52,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     const int mtg = blockIdx.x / ntiles;
     const int total = a.tile_off[a.E];
     if (mtg >= total) return;
-    int lo = 0, hi = a.E - 1;
-    while (lo < hi) {
-        int mid = (lo + hi + 1) >> 1;
-        if (a.tile_off[mid] <= mtg) lo = mid; else hi = mid - 1;
-    }
-    const int e = lo;
+    const int e = a.tile_expert[mtg];
     const int row0 = a.offsets[e] + (mtg - a.tile_off[e]) * BM;
     const int rows = min(BM, a.offsets[e + 1] - row0);
     const int K = a.K;
@@ -184,7 +179,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
             for (int r = 0; r < 16; ++r) {
                 int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (row < rows)
-                    a.c[(size_t)(row0 + row) * a.ldc + f] = swiglu1(acc[m][0][r], acc[m][1][r]);
+                    a.c[(size_t)(row0 + row) * a.ldc + f] = swiglu_fast(acc[m][0][r], acc[m][1][r]);
             }
     } else {
 #pragma unroll

@@ -95,10 +95,11 @@ struct DevBuf {
 
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
-    DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, perm, h, ys, stage, counters;
+    DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, stage,
+        counters;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
-                         &perm, &h, &ys, &stage, &counters};
+                         &tile_expert, &perm, &h, &ys, &stage, &counters};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -384,8 +385,10 @@ static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *
                       int *counts, int *offsets, int *tile_off, int *perm, hipStream_t s) {
     TRY(ensure_counters());
     moe::RouteArgs ra{x, L->wr, L->bias, T, L->d, L->E, L->k, probs, ids, gw};
+    const size_t max_mtiles = ((size_t)T * L->k + moe::kGemmBM - 1) / moe::kGemmBM + L->E;
+    TRY(g_ws.tile_expert.reserve(sizeof(int) * max_mtiles));
     moe::DispatchArgs da{ids, T * L->k, L->E, moe::kGemmBM, counts, offsets, tile_off, perm,
-                         g_ws.counters.as<int>()};
+                         g_ws.counters.as<int>(), g_ws.tile_expert.as<int>()};
     if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
     HIP_TRY(moe::launch_route_dispatch(ra, da, s));
     if (g_timing) {
@@ -454,12 +457,13 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
     } else {
         const int max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
-        moe::GemmArgs gu{x, perm, k, L->wgu, g_ws.h.as<float>(), offsets, tile_off, E, d, 2 * F, F,
-                         max_mtiles};
+        const int *tile_e = g_ws.tile_expert.as<int>();
+        moe::GemmArgs gu{x, perm, k, L->wgu, g_ws.h.as<float>(), offsets, tile_off, tile_e, E, d,
+                         2 * F, F, max_mtiles};
         HIP_TRY(moe::launch_gemm_gateup(gu, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
         moe::GemmArgs dn{g_ws.h.as<float>(), perm, k, L->wdT, g_ws.ys.as<float>(), offsets, tile_off,
-                         E, F, d, d, max_mtiles};
+                         tile_e, E, F, d, d, max_mtiles};
         HIP_TRY(moe::launch_gemm_down(dn, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
     }

@@ -34,6 +34,7 @@ struct DispatchArgs {
     int *tile_off;       // [E + 1] m-tile prefix; tile_off[E] = total m-tiles
     int *perm;           // [n]
     int *counter;        // zeroed device int for the fused path (reset after use)
+    int *tile_expert;    // [n / bm + E] expert of each m-tile (optional)
 };
 
 // Up to this many (token, slot) assignments, and router workgroups, the
@@ -50,6 +51,7 @@ struct GemmArgs {
     float *c;            // H [n x F] (gate/up) or Ys [n x N] indexed by perm (down)
     const int *offsets;  // [E + 1]
     const int *tile_off; // [E + 1]
+    const int *tile_expert; // [max_mtiles] expert of each m-tile
     int E;
     int K;               // reduction length
     int N;               // packed output columns (2F for gate/up, d for down)

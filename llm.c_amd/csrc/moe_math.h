@@ -79,10 +79,13 @@ __device__ inline float glibc_expf(float x) {
     return ftz_f((float)y);
 }
 
-// silu(g) * u in the vector form of swiglu (src/matrix.c:618-655): sigmoid
-// through the exp_avx2 polynomial and an IEEE division.
-__device__ inline float swiglu1(float g, float u) {
-    float sig = 1.0f / (1.0f + exp_poly(-g));
+// silu(g) * u (swiglu, src/matrix.c:618-655) for the expert epilogues, with
+// the hardware exp2 and reciprocal (about 1 ulp each).  The expert outputs
+// are held to a tolerance, not bits (the compiled reference itself divides
+// with an rcpps estimate here), so the fast forms cost nothing in parity.
+__device__ inline float swiglu_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504f);
+    const float sig = __builtin_amdgcn_rcpf(1.0f + e);
     return (g * sig) * u;
 }
 

@@ -71,7 +71,8 @@ __device__ inline void softmax_row(float *row, int E) {
 // Counting sort body run by the NW waves (64*NW threads) of one workgroup.
 // hist: [NW][kMaxExperts] ints of LDS, offs: [kMaxExperts + 1].
 template <int NW>
-__device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], int *offs) {
+__device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], int *offs,
+                              int *toff) {
     constexpr int NT = 64 * NW;
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
@@ -95,16 +96,21 @@ __device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], i
     if (tid == 0) {
         offs[0] = 0;
         int tiles = 0;
-        a.tile_off[0] = 0;
+        toff[0] = 0;
         for (int e = 0; e < E; ++e) {
             int c = offs[e + 1];
             offs[e + 1] = offs[e] + c;
             tiles += (c + a.bm - 1) / a.bm;
-            a.tile_off[e + 1] = tiles;
+            toff[e + 1] = tiles;
         }
-        for (int e = 0; e <= E; ++e) a.offsets[e] = offs[e];
     }
     __syncthreads();
+    if (tid <= E) {
+        a.offsets[tid] = offs[tid];
+        a.tile_off[tid] = toff[tid];
+    }
+    if (a.tile_expert && tid < E)
+        for (int t = toff[tid]; t < toff[tid + 1]; ++t) a.tile_expert[t] = tid;
     if (tid < E) {
         int base = offs[tid];
         for (int ww = 0; ww < NW; ++ww) {
@@ -144,7 +150,8 @@ constexpr int kDispWaves = 16;
 __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
     __shared__ int hist[kDispWaves][kMaxExperts];
     __shared__ int offs[kMaxExperts + 1];
-    dispatch_body<kDispWaves>(a, hist, offs);
+    __shared__ int toff[kMaxExperts + 1];
+    dispatch_body<kDispWaves>(a, hist, offs, toff);
 }
 
 // kend steps of the per-thread FMA chains from one LDS chunk.  The LDS reads
@@ -344,6 +351,7 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a, DispatchArgs d
         // the counter for the next launch.
         __shared__ int hist[4][kMaxExperts];
         __shared__ int offs[kMaxExperts + 1];
+        __shared__ int toff[kMaxExperts + 1];
         __shared__ int is_last;
         __threadfence();
         __syncthreads();
@@ -351,7 +359,7 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a, DispatchArgs d
         __syncthreads();
         if (is_last) {
             __threadfence();
-            dispatch_body<4>(da, hist, offs);
+            dispatch_body<4>(da, hist, offs, toff);
             if (tid == 0) *da.counter = 0;
         }
     }
