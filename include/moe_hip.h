@@ -189,6 +189,11 @@ int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed,
  * == 0).  Process-wide; both paths compute the same layer. */
 int moe_hip_set_expert_path(int mode);
 
+/* Routing kernel selection: 0 = automatic, 1 = token x expert tiles,
+ * 2 = 16-token row blocks with every expert in one workgroup.  Process-wide;
+ * both give the same bits. */
+int moe_hip_set_router_path(int mode);
+
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,
  * src/matrix.c:82-116) or glibc-expf restatement (which = 1) of x[i], the two
  * scalar exponentials the routing softmax uses. */

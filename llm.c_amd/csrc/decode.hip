@@ -10,10 +10,14 @@
 // gemm.hip): a K step of 16 is one contiguous 1 KB unit per wave.
 //   gate/up: grid = E x (F/64); wave w of a workgroup owns features
 //            64*fb + 16w .. +15 and both their gate and up rows, so the SwiGLU
-//            epilogue is lane-local and writes H [n x F] (dispatch order).
+//            epilogue is lane-local and writes H [n x F] at the assignment
+//            index a = t*k + slot.
 //   down:    grid = E x (d/64) x S; split s covers F/S of the reduction and
-//            writes its partial product to Yp[s] at the slot index
-//            perm[pos]; the combine adds the S partials in fixed order.
+//            writes its partial product to Yp[s] at the assignment index;
+//            the combine adds the S partials in fixed order.
+// Each workgroup finds its expert's assignments itself (a ballot scan of the
+// router's expert ids into an ascending list in LDS), after it has issued its
+// first weight loads, which depend on nothing the router computes.
 #include "moe_internal.h"
 #include "moe_math.h"
 
@@ -32,15 +36,35 @@ __device__ inline floatx4 mfma16(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Staging of rows [pos0, pos0 + rows) of the expert's dispatch slice,
-// columns [k0, k0 + kc), into LDS, split so the caller can issue its first
-// weight loads between the global reads and the LDS writes.  GATHER: row =
-// x[perm[pos] / topk]; else src[pos].
+// Ascending list of the assignments a < n with ids[a] == e, built by the
+// workgroup's four waves with ballots; returns its length.  Every thread
+// calls this; wcnt is 4 ints of LDS.
+__device__ int expert_slots(const int *ids, int n, int e, int *list, int *wcnt) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int total = 0;
+    for (int base = 0; base < n; base += 256) {
+        const int i = base + threadIdx.x;
+        const bool hit = i < n && ids[i] == e;
+        const uint64_t m = __ballot(hit);
+        if (lane == 0) wcnt[wave] = __popcll(m);
+        __syncthreads();
+        int off = total;
+        for (int w = 0; w < wave; ++w) off += wcnt[w];
+        if (hit) list[off + __popcll(m & below)] = i;
+        total += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+        __syncthreads();
+    }
+    return total;
+}
+
+// Staging of rows list[pos0 .. pos0 + rows) / div of src, columns
+// [k0, k0 + kc), into LDS, split so the caller can issue weight loads
+// between the global reads and the LDS writes.
 constexpr int kStageMax = kRows * kChunk / 4 / 256;   // float4s per thread
 
-template <bool GATHER>
 __device__ inline void stage_load(floatx4 (&v)[kStageMax], const float *src, int ld,
-                                  const int *perm, int topk, int pos0, int rows, int k0, int kc) {
+                                  const int *list, int div, int pos0, int rows, int k0, int kc) {
     const int q4 = kc >> 2;
 #pragma unroll
     for (int i = 0; i < kStageMax; ++i) {
@@ -48,7 +72,7 @@ __device__ inline void stage_load(floatx4 (&v)[kStageMax], const float *src, int
         const int r = q / q4, c4 = q % q4;
         v[i] = floatx4{0.f, 0.f, 0.f, 0.f};
         if (r < rows) {
-            size_t row = GATHER ? (size_t)(perm[pos0 + r] / topk) : (size_t)(pos0 + r);
+            const size_t row = (size_t)(list[pos0 + r] / div);
             v[i] = *reinterpret_cast<const floatx4 *>(src + row * ld + k0 + 4 * c4);
         }
     }
@@ -137,12 +161,11 @@ __device__ inline void gemv_loop(const float *p0, const float *p1, const float *
 }
 
 __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
-    extern __shared__ __align__(16) float xs[];     // [kRows][kLd]
+    extern __shared__ __align__(16) float xs[];     // [kRows][kLd], then the slot list
+    __shared__ int wcnt[4];
+    int *list = reinterpret_cast<int *>(xs + kRows * kLd);
     const int nfb = a.F / 64;
     const int e = blockIdx.x / nfb, fb = blockIdx.x % nfb;
-    const int base = a.offsets[e];
-    const int cnt = a.offsets[e + 1] - base;
-    if (cnt == 0) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, h = lane >> 4;
     const int f = fb * 64 + wave * 16 + j;
@@ -152,6 +175,10 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
     const float *pg = a.w + (size_t)e * 2 * a.F * a.d + (size_t)nbg * (a.d / 16) * kUnit + 4 * lane;
     const float *pu = pg + (size_t)2 * (a.d / 16) * kUnit;
 
+    floatx4 cur[Unroll<2>::kU][2];
+    gemv_first<2>(pg, pu, min(kChunk, a.d) / 16, cur);
+    const int cnt = expert_slots(a.ids, a.nslots, e, list, wcnt);
+    if (cnt == 0) return;
     for (int r0 = 0; r0 < cnt; r0 += kRows) {
         const int rows = min(kRows, cnt - r0);
         floatx4 acc[2][2];
@@ -162,9 +189,8 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
         for (int k0 = 0; k0 < a.d; k0 += kChunk) {
             const int kc = min(kChunk, a.d - k0);
             floatx4 stg[kStageMax];
-            floatx4 cur[Unroll<2>::kU][2];
-            stage_load<true>(stg, a.x, a.d, a.perm, a.topk, base + r0, rows, k0, kc);
-            gemv_first<2>(pg + 16 * k0, pu + 16 * k0, kc / 16, cur);
+            stage_load(stg, a.x, a.d, list, a.topk, r0, rows, k0, kc);
+            if (r0 > 0 || k0 > 0) gemv_first<2>(pg + 16 * k0, pu + 16 * k0, kc / 16, cur);
             __syncthreads();
             stage_store(stg, xs, kc);
             __syncthreads();
@@ -179,21 +205,21 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(DecodeArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const int row = b * 16 + 4 * h + r;
                 if (row < rows)
-                    a.out[(size_t)(base + r0 + row) * a.F + f] =
+                    a.out[(size_t)list[r0 + row] * a.F + f] =
                         swiglu_fast(acc[b][0][r], acc[b][1][r]);
             }
     }
 }
 
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
-    extern __shared__ __align__(16) float hs[];     // [kRows][kLd]
+    extern __shared__ __align__(16) float hs[];     // [kRows][kLd], then the slot list
+    __shared__ int wcnt[4];
+    int *list = reinterpret_cast<int *>(hs + kRows * kLd);
     const int ncb = a.d / 64;
     const int S = a.ksplit;
     const int e = blockIdx.x / (ncb * S);
     const int rem = blockIdx.x % (ncb * S);
     const int cb = rem / S, sp = rem % S;
-    const int base = a.offsets[e];
-    const int cnt = a.offsets[e + 1] - base;
     const int kspan = a.F / S, kbeg = sp * kspan;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, h = lane >> 4;
@@ -202,15 +228,18 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
                       ((size_t)(cb * 4 + wave) * (a.F / 16) + kbeg / 16) * kUnit + 4 * lane;
     const size_t nslots = (size_t)a.nslots;
 
+    floatx4 cur[Unroll<1>::kU][1];
+    gemv_first<1>(pw, nullptr, min(kChunk, kspan) / 16, cur);
+    const int cnt = expert_slots(a.ids, a.nslots, e, list, wcnt);
+    if (cnt == 0) return;
     for (int r0 = 0; r0 < cnt; r0 += kRows) {
         const int rows = min(kRows, cnt - r0);
         floatx4 acc[2][1] = {{floatx4{0.f, 0.f, 0.f, 0.f}}, {floatx4{0.f, 0.f, 0.f, 0.f}}};
         for (int k0 = 0; k0 < kspan; k0 += kChunk) {
             const int kc = min(kChunk, kspan - k0);
             floatx4 stg[kStageMax];
-            floatx4 cur[Unroll<1>::kU][1];
-            stage_load<false>(stg, a.x, a.F, nullptr, 1, base + r0, rows, kbeg + k0, kc);
-            gemv_first<1>(pw + 16 * k0, nullptr, kc / 16, cur);
+            stage_load(stg, a.x, a.F, list, 1, r0, rows, kbeg + k0, kc);
+            if (r0 > 0 || k0 > 0) gemv_first<1>(pw + 16 * k0, nullptr, kc / 16, cur);
             __syncthreads();
             stage_store(stg, hs, kc);
             __syncthreads();
@@ -224,7 +253,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
             for (int r = 0; r < 4; ++r) {
                 const int row = b * 16 + 4 * h + r;
                 if (row < rows) {
-                    const size_t slot = (size_t)a.perm[base + r0 + row];
+                    const size_t slot = (size_t)list[r0 + row];
                     a.out[((size_t)sp * nslots + slot) * a.d + col] = acc[b][0][r];
                 }
             }
@@ -242,16 +271,23 @@ hipError_t set_lds(const void *kernel, size_t bytes, bool *done) {
 
 }  // namespace
 
+constexpr size_t kDecodeMaxLds = (size_t)kRows * kLd * sizeof(float) + sizeof(int) * kDecodeMaxSlots;
+
 int decode_ksplit(int d, int F, int E) {
     int S = 1;
     while ((long)E * (d / 64) * S < 512 && F % (S * 2 * 32) == 0 && F / (S * 2) >= 256) S *= 2;
     return S;
 }
 
+// Dynamic LDS: the staged rows and a slot list of up to n entries.
+size_t decode_lds(const DecodeArgs &a) {
+    return (size_t)kRows * kLd * sizeof(float) + sizeof(int) * (size_t)a.nslots;
+}
+
 hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s) {
-    const size_t lds = (size_t)kRows * kLd * sizeof(float);
+    const size_t lds = decode_lds(a);
     static bool attr = false;
-    hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_gateup_kernel), lds, &attr);
+    hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_gateup_kernel), kDecodeMaxLds, &attr);
     if (e != hipSuccess) return e;
     dim3 grid((unsigned)(a.E * (a.F / 64)));
     hipLaunchKernelGGL(decode_gateup_kernel, grid, dim3(256), lds, s, a);
@@ -259,9 +295,9 @@ hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s) {
-    const size_t lds = (size_t)kRows * kLd * sizeof(float);
+    const size_t lds = decode_lds(a);
     static bool attr = false;
-    hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_down_kernel), lds, &attr);
+    hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_down_kernel), kDecodeMaxLds, &attr);
     if (e != hipSuccess) return e;
     dim3 grid((unsigned)(a.E * (a.d / 64) * a.ksplit));
     hipLaunchKernelGGL(decode_down_kernel, grid, dim3(256), lds, s, a);

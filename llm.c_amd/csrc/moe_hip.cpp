@@ -3,6 +3,7 @@
 // device-resident layer API.  All kernels are queued on one HIP stream.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -16,6 +17,8 @@
 struct MoeHipLayer {
     int d = 0, F = 0, E = 0, k = 0;
     float *wr = nullptr;     // [d x E]
+    float *wrT = nullptr;    // [E x d]
+    int wr_nonfinite = 0;    // wr holds an inf or NaN
     float *bias = nullptr;   // [E] or null
     float *wgu = nullptr;    // [E][2F][d]
     float *wdT = nullptr;    // [E][d][F]
@@ -33,6 +36,7 @@ hipEvent_t g_ev[6] = {};
 hipEvent_t g_tev[2] = {};
 bool g_have_times = false;
 int g_path = 0;   // 0 auto, 1 grouped GEMM, 2 skinny decode GEMV
+int g_rpath = 0;  // 0 auto, 1 token x expert tiles, 2 one token per lane
 
 int set_err(int code, const char *fmt, ...) {
     g_err = code;
@@ -266,7 +270,8 @@ int moe_hip_layer_create(int d_model, int ffn_hidden, int n_experts, int top_k,
     MoeHipLayer *L = new MoeHipLayer();
     L->d = d_model; L->F = ffn_hidden; L->E = n_experts; L->k = top_k;
     const size_t ne = (size_t)n_experts * d_model * ffn_hidden;
-    hipError_t e1 = hipMalloc(&L->wr, sizeof(float) * (size_t)d_model * n_experts);
+    hipError_t e0 = hipMalloc(&L->wr, sizeof(float) * (size_t)d_model * n_experts);
+    hipError_t e1 = e0 == hipSuccess ? hipMalloc(&L->wrT, sizeof(float) * (size_t)d_model * n_experts) : e0;
     hipError_t e2 = e1 == hipSuccess ? hipMalloc(&L->wgu, sizeof(float) * 2 * ne) : e1;
     hipError_t e3 = e2 == hipSuccess ? hipMalloc(&L->wdT, sizeof(float) * ne) : e2;
     if (e3 != hipSuccess) {
@@ -281,6 +286,7 @@ int moe_hip_layer_create(int d_model, int ffn_hidden, int n_experts, int top_k,
 int moe_hip_layer_destroy(MoeHipLayer *L) {
     if (!L) return MOE_HIP_OK;
     if (L->wr) (void)hipFree(L->wr);
+    if (L->wrT) (void)hipFree(L->wrT);
     if (L->bias) (void)hipFree(L->bias);
     if (L->wgu) (void)hipFree(L->wgu);
     if (L->wdT) (void)hipFree(L->wdT);
@@ -298,6 +304,10 @@ int moe_hip_layer_load(MoeHipLayer *L, const MoEWeights *w) {
     float *st = g_ws.stage.as<float>();
     HIP_TRY(hipMemcpyAsync(L->wr, w->W_router.data, sizeof(float) * (size_t)L->d * L->E,
                            hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(moe::launch_transpose(L->wr, L->wrT, L->d, L->E, g_stream));
+    L->wr_nonfinite = 0;
+    for (size_t i = 0; i < (size_t)L->d * L->E; ++i)
+        if (!std::isfinite(w->W_router.data[i])) { L->wr_nonfinite = 1; break; }
     for (int e = 0; e < L->E; ++e) {
         const FFNWeights &f = w->experts[e];
         HIP_TRY(hipMemcpyAsync(st, f.W_gate.data, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
@@ -333,6 +343,8 @@ int moe_hip_layer_fill_synthetic(MoeHipLayer *L, uint64_t seed, float std_router
     TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
     float *st = g_ws.stage.as<float>();
     HIP_TRY(moe::launch_fill_normal(L->wr, (size_t)L->d * L->E, seed, 1, 0.0f, std_router, g_stream));
+    HIP_TRY(moe::launch_transpose(L->wr, L->wrT, L->d, L->E, g_stream));
+    L->wr_nonfinite = 0;
     for (int e = 0; e < L->E; ++e) {
         HIP_TRY(moe::launch_fill_normal(st, dF, seed, 16 + 3 * (uint64_t)e, 0.0f, std_expert, g_stream));
         HIP_TRY(moe::launch_fill_normal(st + dF, dF, seed, 17 + 3 * (uint64_t)e, 0.0f, std_expert, g_stream));
@@ -382,9 +394,15 @@ int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream
 }
 
 static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
-                      int *counts, int *offsets, int *tile_off, int *perm, hipStream_t s) {
+                      int *counts, int *offsets, int *tile_off, int *perm, hipStream_t s,
+                      bool dispatch = true) {
     TRY(ensure_counters());
     moe::RouteArgs ra{x, L->wr, L->bias, T, L->d, L->E, L->k, probs, ids, gw};
+    ra.no_dispatch = dispatch ? 0 : 1;
+    if (g_rpath != 1) {
+        ra.wrT = L->wrT;
+        ra.wr_nonfinite = L->wr_nonfinite;
+    }
     const size_t max_mtiles = ((size_t)T * L->k + moe::kGemmBM - 1) / moe::kGemmBM + L->E;
     TRY(g_ws.tile_expert.reserve(sizeof(int) * max_mtiles));
     moe::DispatchArgs da{ids, T * L->k, L->E, moe::kGemmBM, counts, offsets, tile_off, perm,
@@ -438,20 +456,24 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
     float *gw = g_ws.gw.as<float>();
     int *offsets = g_ws.offsets.as<int>(), *tile_off = g_ws.tile_off.as<int>();
     int *perm = g_ws.perm.as<int>();
-    TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm, s));
 
-    const bool decode_ok = F % 64 == 0;
+    // Expert products: skinny decode GEMVs (which find their own slots from
+    // the expert ids, so routing skips the dispatch) or grouped GEMMs.
+    const bool decode_ok = F % 64 == 0 && n <= (size_t)moe::kDecodeMaxSlots;
     if (g_path == 2 && !decode_ok)
-        return set_err(MOE_HIP_ERR_UNSUPPORTED, "decode kernels need ffn_hidden %% 64 == 0");
+        return set_err(MOE_HIP_ERR_UNSUPPORTED,
+                       "decode kernels need ffn_hidden %% 64 == 0 and T*k <= %d", moe::kDecodeMaxSlots);
     const bool use_decode = g_path == 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
+    TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm, s,
+                   !use_decode));
     int ksplit = 1;
     if (use_decode) {
         ksplit = moe::decode_ksplit(d, F, E);
         TRY(g_ws.ys.reserve(sizeof(float) * n * d * ksplit));
-        moe::DecodeArgs gu{x, perm, offsets, k, L->wgu, g_ws.h.as<float>(), d, F, E, 1, (int)n};
+        moe::DecodeArgs gu{x, ids_d, k, L->wgu, g_ws.h.as<float>(), d, F, E, 1, (int)n};
         HIP_TRY(moe::launch_decode_gateup(gu, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
-        moe::DecodeArgs dn{g_ws.h.as<float>(), perm, offsets, k, L->wdT, g_ws.ys.as<float>(), d, F,
+        moe::DecodeArgs dn{g_ws.h.as<float>(), ids_d, k, L->wdT, g_ws.ys.as<float>(), d, F,
                            E, ksplit, (int)n};
         HIP_TRY(moe::launch_decode_down(dn, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
@@ -473,6 +495,12 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
         HIP_TRY(hipEventRecord(g_ev[5], s));
         g_have_times = true;
     }
+    return MOE_HIP_OK;
+}
+
+int moe_hip_set_router_path(int mode) {
+    if (mode < 0 || mode > 2) return set_err(MOE_HIP_ERR_ARG, "router path mode %d", mode);
+    g_rpath = mode;
     return MOE_HIP_OK;
 }
 

@@ -22,7 +22,15 @@ struct RouteArgs {
     float *probs;        // [T x E]
     int *ids;            // [T x k]
     float *gw;           // [T x k]
+    // Row-block router; the tile router runs when wrT is null.
+    const float *wrT;    // [E x d], transpose of wr
+    int wr_nonfinite;    // wr holds an inf or NaN: apply the zero-skip per step
+    int no_dispatch;     // routing only (the decode kernels find their own slots)
 };
+
+// Up to this many 16-token row blocks the row-block router's last workgroup
+// performs the dispatch itself.
+constexpr int kRowsFusedMaxBlocks = 256;
 
 struct DispatchArgs {
     const int *ids;      // [T x k]
@@ -71,15 +79,17 @@ struct CombineArgs {
 
 struct DecodeArgs {
     const float *x;      // gate/up: x [T x d]; down: H [n x F]
-    const int *perm;     // [n]
-    const int *offsets;  // [E + 1]
+    const int *ids;      // [n] expert of each assignment a = t*k + slot
     int topk;
     const float *w;      // packed weights (wgu or wdT)
-    float *out;          // gate/up: H [n x F]; down: Yp [ksplit][n][d] by slot
+    float *out;          // gate/up: H [n x F]; down: Yp [ksplit][n][d], both by assignment
     int d, F, E;
     int ksplit;          // down: splits of the F reduction
     int nslots;          // n = T * k
 };
+
+// Most assignments (T * k) the decode kernels take (LDS slot list).
+constexpr int kDecodeMaxSlots = 4096;
 
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);
@@ -101,6 +111,8 @@ hipError_t launch_unpack_down(const float *src, float *wd, int F, int d,
                               hipStream_t s);
 // Elementwise exp_poly (which = 0) or glibc-expf (which = 1) on the device,
 // exactly as the routing kernels evaluate them.
+// dst[c][r] = src[r][c] for a rows x cols matrix.
+hipError_t launch_transpose(const float *src, float *dst, int rows, int cols, hipStream_t s);
 hipError_t launch_eval_exp(int which, const float *x, float *y, size_t n, hipStream_t s);
 hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed,
                               uint64_t stream_id, float mean, float std,

@@ -86,36 +86,42 @@ __device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], i
     for (int i = beg + lane; i < end; i += 64) atomicAdd(&hist[w][a.ids[i]], 1);
     __syncthreads();
 
-    if (tid < E) {
-        int c = 0;
-        for (int ww = 0; ww < NW; ++ww) c += hist[ww][tid];
-        a.counts[tid] = c;
-        offs[tid + 1] = c;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        offs[0] = 0;
-        int tiles = 0;
-        toff[0] = 0;
-        for (int e = 0; e < E; ++e) {
-            int c = offs[e + 1];
-            offs[e + 1] = offs[e] + c;
-            tiles += (c + a.bm - 1) / a.bm;
-            toff[e + 1] = tiles;
-        }
-    }
-    __syncthreads();
-    if (tid <= E) {
-        a.offsets[tid] = offs[tid];
-        a.tile_off[tid] = toff[tid];
-    }
-    if (a.tile_expert && tid < E)
-        for (int t = toff[tid]; t < toff[tid + 1]; ++t) a.tile_expert[t] = tid;
-    if (tid < E) {
-        int base = offs[tid];
+    // Wave 0 scans counts and m-tiles over the (at most 128) experts, two
+    // per lane.
+    if (w == 0) {
+        const int e0 = 2 * lane, e1 = e0 + 1;
+        int c0 = 0, c1 = 0;
         for (int ww = 0; ww < NW; ++ww) {
-            int c = hist[ww][tid];
-            hist[ww][tid] = base;
+            if (e0 < E) c0 += hist[ww][e0];
+            if (e1 < E) c1 += hist[ww][e1];
+        }
+        if (e0 < E) a.counts[e0] = c0;
+        if (e1 < E) a.counts[e1] = c1;
+        const int m0 = (c0 + a.bm - 1) / a.bm, m1 = (c1 + a.bm - 1) / a.bm;
+        int cs = c0 + c1, ms = m0 + m1;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(cs, o), v = __shfl_up(ms, o);
+            if (lane >= o) { cs += u; ms += v; }
+        }
+        const int cb = cs - c0 - c1, mb = ms - m0 - m1;
+        if (e0 < E) { offs[e0] = cb; toff[e0] = mb; }
+        if (e1 < E) { offs[e1] = cb + c0; toff[e1] = mb + m0; }
+        if (lane == 63) { offs[E] = cs; toff[E] = ms; }
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += NT) {
+        a.offsets[e] = offs[e];
+        a.tile_off[e] = toff[e];
+    }
+    if (a.tile_expert)
+        for (int e = tid; e < E; e += NT)
+            for (int t = toff[e]; t < toff[e + 1]; ++t) a.tile_expert[t] = e;
+    for (int e = tid; e < E; e += NT) {
+        int base = offs[e];
+        for (int ww = 0; ww < NW; ++ww) {
+            int c = hist[ww][e];
+            hist[ww][e] = base;
             base += c;
         }
     }
@@ -152,6 +158,45 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
     __shared__ int offs[kMaxExperts + 1];
     __shared__ int toff[kMaxExperts + 1];
     dispatch_body<kDispWaves>(a, hist, offs, toff);
+}
+
+// Softmax, top-k and gate weights of token t from its logits row (in LDS),
+// which is left holding the probabilities.  The reference's "already chosen"
+// scan over ids[0..ki) (src/transformer.c:321-325) is a set membership test;
+// a bit set keeps it (and every index below) in registers.  The gate weight
+// uses probs[ids[ki]], as the reference does even when no candidate beat -1.
+__device__ inline void finish_token(const RouteArgs &a, float *row, int t) {
+    const int E = a.E, k = a.k;
+    softmax_row(row, E);
+    uint64_t chosen[kMaxExperts / 64] = {};
+    float pk[kMaxTopK];
+    int idk[kMaxTopK];
+#pragma unroll
+    for (int ki = 0; ki < kMaxTopK; ++ki) {
+        if (ki < k) {
+            float best = -1.0f;
+            int best_e = 0;
+            for (int e = 0; e < E; ++e) {
+                const bool already = (chosen[e >> 6] >> (e & 63)) & 1ull;
+                if (!already && row[e] > best) { best = row[e]; best_e = e; }
+            }
+            chosen[best_e >> 6] |= 1ull << (best_e & 63);
+            idk[ki] = best_e;
+            pk[ki] = row[best_e];
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int ki = 0; ki < kMaxTopK; ++ki)
+        if (ki < k) s = s + pk[ki];
+    float inv = (s > 1e-9f) ? 1.0f / s : 0.0f;
+#pragma unroll
+    for (int ki = 0; ki < kMaxTopK; ++ki) {
+        if (ki < k) {
+            if (a.ids) a.ids[(size_t)t * k + ki] = idk[ki];
+            if (a.gw) a.gw[(size_t)t * k + ki] = ftz_f(pk[ki] * inv);
+        }
+    }
 }
 
 // kend steps of the per-thread FMA chains from one LDS chunk.  The LDS reads
@@ -299,45 +344,7 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a, DispatchArgs d
     __syncthreads();
 
     // One thread per token: softmax, top-k, gate weights.
-    if (tid < TM && t0 + tid < T) {
-        const int t = t0 + tid;
-        float *row = &lg[tid][0];
-        softmax_row(row, E);
-        // The reference's "already chosen" scan over ids[0..ki) is a set
-        // membership test; a bit set keeps it (and every index below) in
-        // registers.  The gate weight uses probs[ids[ki]], as the reference
-        // does even when no candidate beat -1.
-        uint64_t chosen[kMaxExperts / 64] = {};
-        float pk[kMaxTopK];
-        int idk[kMaxTopK];
-        const int k = a.k;
-#pragma unroll
-        for (int ki = 0; ki < kMaxTopK; ++ki) {
-            if (ki < k) {
-                float best = -1.0f;
-                int best_e = 0;
-                for (int e = 0; e < E; ++e) {
-                    const bool already = (chosen[e >> 6] >> (e & 63)) & 1ull;
-                    if (!already && row[e] > best) { best = row[e]; best_e = e; }
-                }
-                chosen[best_e >> 6] |= 1ull << (best_e & 63);
-                idk[ki] = best_e;
-                pk[ki] = row[best_e];
-            }
-        }
-        float s = 0.0f;
-#pragma unroll
-        for (int ki = 0; ki < kMaxTopK; ++ki)
-            if (ki < k) s = s + pk[ki];
-        float inv = (s > 1e-9f) ? 1.0f / s : 0.0f;
-#pragma unroll
-        for (int ki = 0; ki < kMaxTopK; ++ki) {
-            if (ki < k) {
-                if (a.ids) a.ids[(size_t)t * k + ki] = idk[ki];
-                if (a.gw) a.gw[(size_t)t * k + ki] = ftz_f(pk[ki] * inv);
-            }
-        }
-    }
+    if (tid < TM && t0 + tid < T) finish_token(a, &lg[tid][0], t0 + tid);
     __syncthreads();
     if (a.probs) {
         for (int idx = tid; idx < TM * E; idx += 256) {
@@ -365,6 +372,306 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a, DispatchArgs d
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-block router.  A workgroup owns 16 tokens and every expert, so routing
+// needs no cross-workgroup exchange.  Lane 16*r + c of wave w runs the
+// chains of token t0 + c with experts 4*(w*RE + j) + r, j < RE, over k
+// ascending.  x reaches the lanes through LDS (float4 reads; the four 16-lane
+// rows read the same token row); each expert's router row sits in VGPRs
+// sixteen k-values at a time (lane c of row r holds k0 + c of row r's
+// expert) and reaches all lanes of the row through DPP row_newbcast inside
+// the FMA, so the broadcast costs no instruction.
+//
+// Zero-skip: the reference skips x == 0 (src/matrix.c:394).  For finite
+// router weights fma(0, w, acc) returns acc up to the sign of a zero
+// accumulator, and a logit of +0 or -0 gives the same probabilities bit for
+// bit (every path of the softmax maps both to the same value), so SKIP = false
+// is exact for them.  Router weights holding an inf or NaN (0 * inf = NaN)
+// take the SKIP = true variant, which applies the skip per step.
+// ---------------------------------------------------------------------------
+
+// acc = fma(w from lane 16*row + J, x[J], acc) for J = 0..15 in order.  The
+// leading s_nop gives the wait states a DPP source read needs after a VALU
+// write of that register or of EXEC.
+__device__ inline void chain16_dpp(float &acc, float w, const float (&x)[16]) {
+    asm("s_nop 4\n\t"
+        "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        : "+v"(acc)
+        : "v"(w), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
+}
+
+template <int J>
+__device__ inline float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xF, 0xF, true));
+}
+
+// The same chain with the reference's per-step zero-skip.
+template <int J>
+struct SkipChain {
+    __device__ static inline void run(float &acc, float w, const float (&x)[16]) {
+        SkipChain<J - 1>::run(acc, w, x);
+        const float wj = row_bcast<J - 1>(w);
+        acc = (x[J - 1] != 0.0f) ? fmaf(x[J - 1], wj, acc) : acc;
+    }
+};
+template <>
+struct SkipChain<0> {
+    __device__ static inline void run(float &, float, const float (&)[16]) {}
+};
+
+// Lane l of each aligned group of 8 lanes reads lane l ^ M (DPP moves).
+template <int CTRL>
+__device__ inline int dpp_mov(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int M> __device__ inline int xor8(int v);
+template <> __device__ inline int xor8<1>(int v) { return dpp_mov<0xB1>(v); }   // quad_perm [1,0,3,2]
+template <> __device__ inline int xor8<2>(int v) { return dpp_mov<0x4E>(v); }   // quad_perm [2,3,0,1]
+template <> __device__ inline int xor8<4>(int v) {
+    const int up = dpp_mov<0x104>(v);   // row_shl:4, lane i reads lane i + 4
+    const int dn = dpp_mov<0x114>(v);   // row_shr:4, lane i reads lane i - 4
+    return (threadIdx.x & 4) ? dn : up;
+}
+template <int M> __device__ inline float xor8f(float v) {
+    return __int_as_float(xor8<M>(__float_as_int(v)));
+}
+
+// Eight consecutive lanes finish one token: lane l plays lane l of the
+// reference's 8-wide vectors, so softmax_rows (src/matrix.c:529-586) keeps
+// its per-lane maxima and sums and hsum256's fold order
+// (include/simd.h:110-121) becomes three butterfly steps; every lane then
+// runs the scalar tail in the reference's order.  Top-k
+// (src/transformer.c:317-331) is k rounds of an argmax over the experts not
+// yet chosen, ties to the lowest index, reduced across the eight lanes; lane
+// 0 records each round's expert and probability in id_out / p_out and the
+// returned value is the renormalisation factor (src/transformer.c:334-336).
+// Every lane of the wave calls this together.
+__device__ inline float finish_token8(const RouteArgs &a, float *row, int l, int *id_out,
+                                      float *p_out) {
+    const int E = a.E, k = a.k;
+    const int nb = E >> 3, tail = E - 8 * nb;
+    float m = -1e38f;
+    for (int b = 0; b < nb; ++b) m = fmaxf(m, row[8 * b + l]);
+    m = fmaxf(m, xor8f<4>(m));
+    m = fmaxf(m, xor8f<2>(m));
+    m = fmaxf(m, xor8f<1>(m));
+    for (int j = 8 * nb; j < E; ++j) {
+        const float v = row[j];
+        if (v > m) m = v;
+    }
+    float vs = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const float ex = exp_poly(row[8 * b + l] - m);
+        row[8 * b + l] = ex;
+        vs = vs + ex;
+    }
+    vs = vs + xor8f<4>(vs);   // v_l + v_(l+4)
+    vs = vs + xor8f<1>(vs);   // (v0+v4) + (v1+v5) and (v2+v6) + (v3+v7)
+    vs = vs + xor8f<2>(vs);   // the two halves
+    for (int j = 8 * nb; j < E; ++j) {
+        const float ex = glibc_expf(row[j] - m);
+        vs = vs + ex;
+        if (l == 0) row[j] = ex;
+    }
+    const float inv = 1.0f / vs;
+    for (int b = 0; b < nb; ++b) row[8 * b + l] = ftz_f(row[8 * b + l] * inv);
+    if (l < tail) row[8 * nb + l] = ftz_f(row[8 * nb + l] * inv);
+
+    uint64_t chosen0 = 0, chosen1 = 0;
+    float s = 0.0f;
+    for (int ki = 0; ki < k; ++ki) {
+        float best = -1.0f;
+        int be = 0x7fffffff;
+        auto consider = [&](int e) {
+            const uint64_t bit = e < 64 ? (chosen0 >> e) & 1ull : (chosen1 >> (e - 64)) & 1ull;
+            const float v = row[e];
+            if (!bit && v > best) { best = v; be = e; }
+        };
+        for (int b = 0; b < nb; ++b) consider(8 * b + l);
+        if (l < tail) consider(8 * nb + l);
+        auto merge = [&](float ob, int oe) {
+            if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; }
+        };
+        merge(xor8f<4>(best), xor8<4>(be));
+        merge(xor8f<2>(best), xor8<2>(be));
+        merge(xor8f<1>(best), xor8<1>(be));
+        if (be == 0x7fffffff) be = 0;   // nothing beat -1: the reference keeps best_e = 0
+        if (be < 64) chosen0 |= 1ull << be;
+        else         chosen1 |= 1ull << (be - 64);
+        const float p = row[be];
+        s = s + p;
+        if (l == 0) { id_out[ki] = be; p_out[ki] = p; }
+    }
+    return (s > 1e-9f) ? 1.0f / s : 0.0f;
+}
+
+template <int NWV, int RE, int KC, bool SKIP, bool FUSE>
+__global__ __launch_bounds__(64 * NWV) void router_rows_kernel(RouteArgs a, DispatchArgs da) {
+    static_assert(NWV >= 2, "two waves finish the block's 16 tokens");
+    constexpr int NT = 64 * NWV;
+    constexpr int LD = KC + 4;                     // padded LDS row of x (floats)
+    constexpr int XQ = 16 * KC / 4;                // float4s of x per chunk
+    constexpr int XL = (XQ + NT - 1) / NT;
+    constexpr int WV = KC / 16;                    // router VGPRs per expert per chunk
+    __shared__ __align__(16) float xs[2][16][LD];
+    __shared__ float lg[16][kMaxExperts + 1];
+    __shared__ float p_sel[16][kMaxTopK];
+    __shared__ int id_sel[16][kMaxTopK];
+    __shared__ float inv_sel[16];
+    __shared__ int is_last;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane >> 4, c = lane & 15;
+    const int T = a.T, d = a.d, E = a.E, k = a.k;
+    const int t0 = blockIdx.x * 16;
+
+    // Experts past E repeat expert E - 1 and store nothing; rows past T read
+    // row T - 1 (all lanes stay active for the DPP reads) and store nothing.
+    const float *wrow[RE];
+#pragma unroll
+    for (int j = 0; j < RE; ++j)
+        wrow[j] = a.wrT + (size_t)min(4 * (w * RE + j) + r, E - 1) * d + c;
+
+    float4 rx[XL];
+    float rw[RE][WV], wc[RE][WV];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XL; ++i) {
+            const int q = min(tid + NT * i, XQ - 1);
+            const int rr = q / (KC / 4), c4 = q % (KC / 4);
+            const int t = min(t0 + rr, T - 1);
+            rx[i] = *reinterpret_cast<const float4 *>(a.x + (size_t)t * d + k0 + 4 * c4);
+        }
+#pragma unroll
+        for (int j = 0; j < RE; ++j)
+#pragma unroll
+            for (int s4 = 0; s4 < WV; ++s4) rw[j][s4] = wrow[j][k0 + 16 * s4];
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XL; ++i) {
+            const int q = tid + NT * i;
+            if (XQ % NT == 0 || q < XQ) {
+                const int rr = q / (KC / 4), c4 = q % (KC / 4);
+                float4 v = rx[i];
+                if (SKIP) v = make_float4(ftz_f(v.x), ftz_f(v.y), ftz_f(v.z), ftz_f(v.w));
+                *reinterpret_cast<float4 *>(&xs[buf][rr][4 * c4]) = v;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < RE; ++j)
+#pragma unroll
+            for (int s4 = 0; s4 < WV; ++s4) wc[j][s4] = rw[j][s4];
+    };
+
+    float acc[RE];
+#pragma unroll
+    for (int j = 0; j < RE; ++j) acc[j] = 0.0f;
+    const int nchunk = d / KC;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int ch = 0; ch < nchunk; ++ch) {
+        const int buf = ch & 1;
+        if (ch + 1 < nchunk) gload((ch + 1) * KC);
+        // x of the next 16 steps is read while the FMAs of these run.
+        auto xread = [&](float (&xv)[16], int s4) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = *reinterpret_cast<const float4 *>(&xs[buf][c][16 * s4 + 4 * q]);
+                xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
+            }
+        };
+        auto chains = [&](const float (&xv)[16], int s4) {
+#pragma unroll
+            for (int j = 0; j < RE; ++j) {
+                if (SKIP) SkipChain<16>::run(acc[j], wc[j][s4], xv);
+                else      chain16_dpp(acc[j], wc[j][s4], xv);
+            }
+        };
+        float xa[16], xb[16];
+        xread(xa, 0);
+#pragma unroll
+        for (int s4 = 0; s4 < WV; s4 += 2) {
+            xread(xb, s4 + 1);
+            chains(xa, s4);
+            if (s4 + 2 < WV) xread(xa, s4 + 2);
+            chains(xb, s4 + 1);
+        }
+        if (ch + 1 < nchunk) sstore(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < RE; ++j) {
+        const int e = 4 * (w * RE + j) + r;
+        if (e < E) lg[c][e] = a.bias ? acc[j] + a.bias[e] : acc[j];
+    }
+    __syncthreads();
+    if (tid < 128) {
+        const int ct = tid >> 3, l = tid & 7;
+        const float inv = finish_token8(a, &lg[ct][0], l, &id_sel[ct][0], &p_sel[ct][0]);
+        if (l == 0) inv_sel[ct] = inv;
+    }
+    __syncthreads();
+    const int tn = min(16, T - t0);
+    if (a.ids || a.gw)
+        for (int i = tid; i < tn * k; i += NT) {
+            const int ct = i / k, ki = i - ct * k;
+            const size_t o = (size_t)(t0 + ct) * k + ki;
+            if (a.ids) a.ids[o] = id_sel[ct][ki];
+            if (a.gw) a.gw[o] = ftz_f(p_sel[ct][ki] * inv_sel[ct]);
+        }
+    if (a.probs)
+        for (int i = tid; i < tn * E; i += NT) {
+            const int ct = i / E, e = i - ct * E;
+            a.probs[(size_t)(t0 + ct) * E + e] = lg[ct][e];
+        }
+    if (FUSE) {
+        // The last workgroup to finish runs the dispatch over every token's
+        // ids (release/acquire through the device-scope fences), then resets
+        // the counter for the next launch.
+        __shared__ int hist[NWV][kMaxExperts];
+        __shared__ int offs[kMaxExperts + 1];
+        __shared__ int toff[kMaxExperts + 1];
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) is_last = atomicAdd(da.counter, 1) == (int)gridDim.x - 1;
+        __syncthreads();
+        if (is_last) {
+            __threadfence();
+            dispatch_body<NWV>(da, hist, offs, toff);
+            if (tid == 0) *da.counter = 0;
+        }
+    }
+}
+
+// dst[c][r] = src[r][c] for a rows x cols matrix.
+__global__ __launch_bounds__(256) void transpose_kernel(const float *src, float *dst, int rows,
+                                                        int cols) {
+    __shared__ float tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int i = ty; i < 32; i += 8)
+        if (r0 + i < rows && c0 + tx < cols) tile[i][tx] = src[(size_t)(r0 + i) * cols + c0 + tx];
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8)
+        if (c0 + i < cols && r0 + tx < rows) dst[(size_t)(c0 + i) * rows + r0 + tx] = tile[tx][i];
+}
+
 __global__ __launch_bounds__(256) void eval_exp_kernel(int which, const float *x, float *y,
                                                       size_t n) {
     for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
@@ -372,6 +679,13 @@ __global__ __launch_bounds__(256) void eval_exp_kernel(int which, const float *x
 }
 
 }  // namespace
+
+hipError_t launch_transpose(const float *src, float *dst, int rows, int cols, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    dim3 grid((cols + 31) / 32, (rows + 31) / 32);
+    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, s, src, dst, rows, cols);
+    return hipGetLastError();
+}
 
 hipError_t launch_eval_exp(int which, const float *x, float *y, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
@@ -403,6 +717,44 @@ hipError_t launch_router(const RouteArgs &a, const DispatchArgs &da, hipStream_t
     return hipGetLastError();
 }
 
+template <int NWV, int RE, int KC, bool FUSE>
+void launch_rows(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
+    dim3 grid((a.T + 15) / 16), block(64 * NWV);
+    if (a.wr_nonfinite)
+        hipLaunchKernelGGL((router_rows_kernel<NWV, RE, KC, true, FUSE>), grid, block, 0, s, a, da);
+    else
+        hipLaunchKernelGGL((router_rows_kernel<NWV, RE, KC, false, FUSE>), grid, block, 0, s, a, da);
+}
+
+// Waves and experts per lane: 4 * NWV * RE >= E.  Chunks of 128 k when d
+// allows (d % 64 == 0 always holds).
+template <int KC, bool FUSE>
+hipError_t launch_rows_kc(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
+    if (a.E <= 8)        launch_rows<2, 1, KC, FUSE>(a, da, s);
+    else if (a.E <= 16)  launch_rows<4, 1, KC, FUSE>(a, da, s);
+    else if (a.E <= 32)  launch_rows<4, 2, KC, FUSE>(a, da, s);
+    else {
+        if constexpr (KC == 512) {
+            return hipErrorInvalidValue;
+        } else {
+            if (a.E <= 64)       launch_rows<4, 4, KC, FUSE>(a, da, s);
+            else if (a.E <= 128) launch_rows<4, 8, KC, FUSE>(a, da, s);
+            else return hipErrorInvalidValue;
+        }
+    }
+    return hipGetLastError();
+}
+
+// k chunk: 512 when d allows and the router rows fit in registers (up to 32
+// experts), so a d = 512 layer stages x once; else 128 or 64 (d % 64 == 0
+// always holds).
+template <bool FUSE>
+hipError_t launch_rows_router(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
+    if (a.d % 512 == 0 && a.E <= 32) return launch_rows_kc<512, FUSE>(a, da, s);
+    if (a.d % 128 == 0) return launch_rows_kc<128, FUSE>(a, da, s);
+    return launch_rows_kc<64, FUSE>(a, da, s);
+}
+
 }  // namespace
 
 // Routing followed by dispatch.  For small launches (at most
@@ -413,6 +765,16 @@ hipError_t launch_router(const RouteArgs &a, const DispatchArgs &da, hipStream_t
 // sorts them.
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
+    if (a.no_dispatch)
+        return a.wrT ? launch_rows_router<false>(a, da, s) : launch_router<false>(a, da, s);
+    if (a.wrT) {
+        const int blocks = (a.T + 15) / 16;
+        const bool fuse = da.counter && da.n <= kFusedDispatchMax && blocks <= kRowsFusedMaxBlocks;
+        hipError_t e = fuse ? launch_rows_router<true>(a, da, s) : launch_rows_router<false>(a, da, s);
+        if (e != hipSuccess || fuse) return e;
+        hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, da);
+        return hipGetLastError();
+    }
     const int grid = (a.T + (a.T >= 2048 ? 64 : 16) - 1) / (a.T >= 2048 ? 64 : 16);
     if (da.n <= kFusedDispatchMax && grid <= kFusedDispatchMaxBlocks && da.counter)
         return launch_router<true>(a, da, s);

@@ -59,6 +59,7 @@ SIGNATURES = {
     "moe_hip_last_timings": (C.c_int, [_F]),
     "moe_hip_set_timing": (C.c_int, [C.c_int]),
     "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
+    "moe_hip_set_router_path": (C.c_int, [C.c_int]),
     "moe_hip_timer_start": (C.c_int, []),
     "moe_hip_timer_stop": (C.c_int, [_F]),
     "moe_hip_dev_alloc": (C.c_int, [C.POINTER(_P), C.c_size_t]),
@@ -230,6 +231,11 @@ def synchronize():
 def set_expert_path(mode):
     """0 automatic, 1 grouped GEMMs, 2 skinny decode GEMVs."""
     check(lib().moe_hip_set_expert_path(int(mode)))
+
+
+def set_router_path(mode):
+    """0 automatic, 1 token x expert tiles, 2 16-token row blocks."""
+    check(lib().moe_hip_set_router_path(int(mode)))
 
 
 def set_timing(on):

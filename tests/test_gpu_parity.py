@@ -123,18 +123,56 @@ ROUTE_CASES = [
     ("e64k4", 2048, 2048, 64, 4, 0.02),
     ("e128k1", 777, 128, 128, 1, 0.2),
     ("t1", 1, 256, 8, 2, 0.1),
+    ("t65_d64", 65, 64, 16, 2, 0.1),
+    ("t5000", 5000, 128, 16, 2, 0.1),
 ]
 
+ROUTER_PATHS = [0, 1, 2]   # automatic, token x expert tiles, 16-token row blocks
 
+
+@pytest.fixture
+def router_path():
+    yield mh.set_router_path
+    mh.set_router_path(0)
+
+
+@pytest.mark.parametrize("path", ROUTER_PATHS, ids=["auto", "tiles", "rows"])
 @pytest.mark.parametrize("name,T,d,E,k,std_router", ROUTE_CASES, ids=[c[0] for c in ROUTE_CASES])
-def test_route_bitexact(name, T, d, E, k, std_router):
-    say(f"route {name}: T={T} d={d} E={E} k={k}")
+def test_route_bitexact(name, T, d, E, k, std_router, path, router_path):
+    say(f"route {name}: T={T} d={d} E={E} k={k} path={path}")
+    router_path(path)
     x = orc.synth((T, d), 11, 0, 1.0)
     layer = mh.Layer(d, 64, E, k)
     layer.fill_synthetic(11, std_router, 0.02)
     wr = layer.get_router()
     assert np.array_equal(bits(wr), bits(orc.synth((d, E), 11, 1, std_router)))
     assert_route_equal(route_on_device(layer, x), x, wr, k, E)
+    layer.close()
+
+
+@pytest.mark.parametrize("path", ROUTER_PATHS, ids=["auto", "tiles", "rows"])
+def test_route_zero_skip_nonfinite_weights(path, router_path):
+    """The reference skips x == 0 (DAZ: also denormal x), so an inf router
+    weight facing a zero (or denormal) x leaves the logit finite."""
+    T, d, E, k = 100, 128, 16, 2
+    router_path(path)
+    x = orc.synth((T, d), 7, 0, 1.0)
+    x[:, 5] = 0.0
+    x[:, 9] = -0.0
+    x[:, 40] = np.float32(1e-40)            # denormal: zero under DAZ
+    x[::3, 77] = 0.0                         # zero for some tokens only
+    wr = orc.synth((d, E), 7, 1, 0.1)
+    wr[5, :] = np.inf
+    wr[9, ::2] = -np.inf
+    wr[40, 3] = np.nan
+    wr[77, 1] = 0.0
+    hw = HostMoE(wr, np.zeros((E, d, 64), np.float32), np.zeros((E, d, 64), np.float32),
+                 np.zeros((E, 64, d), np.float32), k)
+    layer = mh.Layer(d, 64, E, k)
+    layer.load(hw)
+    dev = route_on_device(layer, x)
+    assert np.isfinite(dev[0]).all()
+    assert_route_equal(dev, x, wr, k, E)
     layer.close()
 
 
