@@ -94,19 +94,32 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
     mh.fill_normal_dev(x.ptr, T * d, 99, 2, 0.0, 1.0)
     ids = [mh.DeviceArray((T, k), np.int32) for _ in range(n_layers)]
     mh.synchronize()
-    for _ in range(warmup):
+
+    def step():
         for li, L in enumerate(layers):
             L.forward_dev(xn.ptr, T, x.ptr, None, ids[li].ptr, accumulate=1)
+
+    for _ in range(max(warmup, 1)):
+        step()
     mh.synchronize()
-    # Headline: K decode steps back to back, device time between two events
-    # on the library stream (no per-kernel events in the way).
+    # Headline: K decode steps issued back to back on the library stream,
+    # device time between two events on that stream.
     mh.timer_start()
     t0 = time.perf_counter()
     for _ in range(steps):
-        for li, L in enumerate(layers):
-            L.forward_dev(xn.ptr, T, x.ptr, None, ids[li].ptr, accumulate=1)
+        step()
     dev_ms = mh.timer_stop()
     wall = time.perf_counter() - t0
+    # The same step replayed from a captured HIP graph (informational).
+    with mh.Graph() as graph:
+        step()
+    graph.launch()
+    mh.synchronize()
+    mh.timer_start()
+    for _ in range(steps):
+        graph.launch()
+    graph_ms = mh.timer_stop() / steps
+    graph.close()
     # Breakdown (informational): one more pass with per-phase events, which
     # themselves add a few microseconds each.
     mh.set_timing(True)
@@ -122,7 +135,7 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
     bytes_gu = [4.0 * 2 * d * F * u for u in used]
     dev_ms_layer = ms_step / n_layers
     res = dict(layers=n_layers, T=T, d=d, F=F, E=E, k=k, ms_per_step=ms_step,
-               wall_ms_per_step=wall * 1e3 / steps,
+               wall_ms_per_step=wall * 1e3 / steps, graph_ms_per_step=graph_ms,
                tokens_per_s=T / (ms_step * 1e-3),
                device_ms_per_layer=dev_ms_layer, phase_ms=phase.tolist(),
                experts_used=used,
@@ -243,6 +256,7 @@ def main():
         line["decode"] = {
             "workload": "64 seqs x 1 token, 8 MoE layers d=512 d_ff=2048 E=16 top-2",
             "tokens_per_s": dec["tokens_per_s"], "ms_per_step": dec["ms_per_step"],
+            "graph_ms_per_step": dec["graph_ms_per_step"],
             "device_ms_per_layer": dec["device_ms_per_layer"],
             "hbm_gbs": dec["hbm_gbs_layer"], "hbm_frac": dec["hbm_gbs_layer"] / PEAK_HBM_GBS,
             "gateup_gbs": dec["gateup_gbs"], "phase_ms_per_layer": dict(zip(

@@ -221,6 +221,17 @@ int moe_hip_memcpy(void *dst, const void *src, size_t bytes, int kind);
 int moe_hip_memset(void *ptr, int value, size_t bytes);
 int moe_hip_synchronize(void);
 
+/* HIP graphs for such callers (the benchmark replays a captured decode
+ * step).  graph_begin starts capturing `stream` (NULL: the library stream):
+ * work queued on it until graph_end is recorded, not run.  graph_end
+ * instantiates the recording into *graph.  Recorded calls must not allocate:
+ * run each once beforehand so the library workspace is already sized (a
+ * call that would grow it fails the capture). */
+int moe_hip_graph_begin(void *stream);
+int moe_hip_graph_end(void *stream, void **graph);
+int moe_hip_graph_launch(void *graph, void *stream);
+int moe_hip_graph_destroy(void *graph);
+
 #ifdef __cplusplus
 }
 #endif

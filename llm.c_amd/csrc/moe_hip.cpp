@@ -644,3 +644,44 @@ int moe_hip_synchronize(void) {
 }
 
 }  // extern "C"
+
+struct MoeHipGraph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int moe_hip_graph_begin(void *stream) {
+    TRY(ensure_init());
+    HIP_TRY(hipStreamBeginCapture(pick_stream(stream), hipStreamCaptureModeThreadLocal));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_graph_end(void *stream, void **graph) {
+    if (!graph) return set_err(MOE_HIP_ERR_ARG, "null graph out-pointer");
+    *graph = nullptr;
+    MoeHipGraph *G = new MoeHipGraph();
+    hipError_t e = hipStreamEndCapture(pick_stream(stream), &G->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&G->exec, G->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        if (G->graph) (void)hipGraphDestroy(G->graph);
+        delete G;
+        return set_err(MOE_HIP_ERR_HIP, "graph capture: %s", hipGetErrorString(e));
+    }
+    *graph = G;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_graph_launch(void *graph, void *stream) {
+    if (!graph) return set_err(MOE_HIP_ERR_ARG, "null graph");
+    HIP_TRY(hipGraphLaunch(static_cast<MoeHipGraph *>(graph)->exec, pick_stream(stream)));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_graph_destroy(void *graph) {
+    if (!graph) return MOE_HIP_OK;
+    MoeHipGraph *G = static_cast<MoeHipGraph *>(graph);
+    if (G->exec) (void)hipGraphExecDestroy(G->exec);
+    if (G->graph) (void)hipGraphDestroy(G->graph);
+    delete G;
+    return MOE_HIP_OK;
+}

@@ -67,6 +67,10 @@ SIGNATURES = {
     "moe_hip_memcpy": (C.c_int, [_P, _P, C.c_size_t, C.c_int]),
     "moe_hip_memset": (C.c_int, [_P, C.c_int, C.c_size_t]),
     "moe_hip_synchronize": (C.c_int, []),
+    "moe_hip_graph_begin": (C.c_int, [_P]),
+    "moe_hip_graph_end": (C.c_int, [_P, C.POINTER(_P)]),
+    "moe_hip_graph_launch": (C.c_int, [_P, _P]),
+    "moe_hip_graph_destroy": (C.c_int, [_P]),
 }
 
 _lib = None
@@ -204,6 +208,11 @@ class DeviceArray:
         check(lib().moe_hip_memcpy(d.ptr, a.ctypes.data_as(_P), d.nbytes, 1))
         return d
 
+    def upload(self, a):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes
+        check(lib().moe_hip_memcpy(self.ptr, a.ctypes.data_as(_P), self.nbytes, 1))
+
     def to_host(self):
         a = np.empty(self.shape, self.dtype)
         check(lib().moe_hip_memcpy(a.ctypes.data_as(_P), self.ptr, self.nbytes, 2))
@@ -226,6 +235,34 @@ class DeviceArray:
 
 def synchronize():
     check(lib().moe_hip_synchronize())
+
+
+class Graph:
+    """Records the library calls made inside ``with Graph() as g:`` (on the
+    library stream) into a HIP graph; ``g.launch()`` replays them."""
+
+    def __init__(self):
+        self.h = None
+
+    def __enter__(self):
+        check(lib().moe_hip_graph_begin(None))
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = C.c_void_p()
+        rc = lib().moe_hip_graph_end(None, C.byref(h))
+        if exc_type is None:
+            check(rc)
+            self.h = h
+        return False
+
+    def launch(self):
+        check(lib().moe_hip_graph_launch(self.h, None))
+
+    def close(self):
+        if self.h is not None:
+            lib().moe_hip_graph_destroy(self.h)
+            self.h = None
 
 
 def set_expert_path(mode):

@@ -300,6 +300,53 @@ def test_decode_batch_c4():
     assert_close(x_one - x0[:1], o1, "c4 decode step")
 
 
+@pytest.mark.parametrize("path", [2, 1], ids=["gemv", "gemm"])
+def test_graph_replay(path):
+    """A captured forward (two layers, accumulating) replays to the same bits
+    as the eager calls, replay after replay, with eager work and
+    synchronisations in between."""
+    T, d, F, E, k = 64, 512, 2048, 16, 2
+    mh.set_expert_path(path)
+    layers = [mh.Layer(d, F, E, k) for _ in range(2)]
+    try:
+        for i, L in enumerate(layers):
+            L.fill_synthetic(40 + i, 0.02, 0.02)
+        xn = mh.DeviceArray((T, d))
+        mh.fill_normal_dev(xn.ptr, T * d, 41, 0, 0.0, 1.0)
+        x0 = orc.synth((T, d), 41, 2, 1.0)
+        out = mh.DeviceArray.from_host(x0)
+        ids = [mh.DeviceArray((T, k), np.int32) for _ in layers]
+
+        def step():
+            for L, i in zip(layers, ids):
+                L.forward_dev(xn.ptr, T, out.ptr, None, i.ptr, accumulate=1)
+
+        step()                       # eager; also sizes the workspace
+        mh.synchronize()
+        ref = out.to_host()
+        ref_ids = [i.to_host() for i in ids]
+        with mh.Graph() as g:
+            step()
+        other = mh.DeviceArray((T, d))
+        for rep in range(3):
+            out.upload(x0)
+            for i in ids:
+                i.zero()
+            g.launch()
+            mh.synchronize()
+            assert np.array_equal(bits(out.to_host()), bits(ref)), f"replay {rep}: output differs"
+            for i, r in zip(ids, ref_ids):
+                assert np.array_equal(i.to_host(), r), f"replay {rep}: expert ids differ"
+            # Eager work on other data between replays.
+            layers[0].forward_dev(out.ptr, T, other.ptr)
+            mh.synchronize()
+        g.close()
+    finally:
+        mh.set_expert_path(0)
+        for L in layers:
+            L.close()
+
+
 EDGE_CASES = [
     # name, T, d, F, E, k
     ("t1", 1, 128, 256, 8, 2),
