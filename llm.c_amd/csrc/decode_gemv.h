@@ -1,0 +1,402 @@
+// decode_gemv.h — building blocks of the bandwidth-bound decode expert
+// products (decode.hip) and of the fused decode-layer kernel (layer.hip).
+//
+// Weights stream from HBM straight into v_mfma_f32_16x16x4f32 operands: a
+// lane holds a 16-byte piece of one weight row (K contiguous), the MFMA's
+// k-row h (lane/16) takes the piece's 4 elements in turn, and the
+// activations come from LDS as 128-bit reads with the same k mapping.
+// Weights are in the unit layout (16 x 16 tiles in MFMA operand order, see
+// gemm.hip): a K step of 16 is one contiguous 1 KB unit per wave.
+#pragma once
+#include <type_traits>
+
+#include "moe_internal.h"
+#include "moe_math.h"
+
+namespace moe {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRows = 32;        // rows per pass (two 16-row MFMA blocks)
+constexpr int kChunk = 512;      // K elements staged per LDS fill
+constexpr int kLd = kChunk + 4;  // padded LDS row
+
+constexpr int kUnit = 256;      // floats per 16 x 16 unit = one K step of 16
+constexpr int kHLd = 64 + 4;    // padded LDS row of the fused kernel's H block
+
+__device__ inline floatx4 mfma16(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Ascending list of the assignments a < n with ids[a] == e, built by the
+// workgroup's four waves with ballots, and (tok != nullptr) the token a / topk
+// of each; returns the list length.  Every thread calls this, with id0 =
+// ids[threadIdx.x] (or -1 past n) loaded by the caller before its first
+// weight loads so that waiting for it does not wait for them; wcnt is 4 ints
+// of LDS.
+__device__ inline void slot_chunk(int i, int n, int e, int id, int topk, int *list, int *tok,
+                                  int *wcnt, int &total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const bool hit = i < n && id == e;
+    const uint64_t m = __ballot(hit);
+    if (lane == 0) wcnt[wave] = __popcll(m);
+    __syncthreads();
+    int off = total;
+    for (int w = 0; w < wave; ++w) off += wcnt[w];
+    if (hit) {
+        const int at = off + __popcll(m & below);
+        list[at] = i;
+        if (tok) tok[at] = i / topk;
+    }
+    total += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+    __syncthreads();
+}
+
+// An expert id: COHERENT reads one written earlier in the same launch by
+// another workgroup (device-scope atomic load).
+template <bool COHERENT>
+__device__ inline int load_id(const int *p) {
+    if (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+
+template <bool COHERENT>
+__device__ int expert_slots(const int *ids, int n, int e, int id0, int topk, int *list, int *tok,
+                            int *wcnt) {
+    int total = 0;
+    slot_chunk(threadIdx.x, n, e, id0, topk, list, tok, wcnt, total);
+    for (int base = 256; base < n; base += 256) {
+        const int i = base + threadIdx.x;
+        slot_chunk(i, n, e, load_id<COHERENT>(ids + min(i, n - 1)), topk, list, tok, wcnt, total);
+    }
+    return total;
+}
+
+// Spins (thread 0, bounded) until *ctr >= target, read with device-scope
+// atomic loads; past the bound it raises *err and goes on, so every wave
+// always ends.  The workgroup then passes a barrier (no fence: pending
+// weight loads need not complete).
+constexpr int kSpinLimit = 1 << 20;
+
+__device__ inline void wait_count(const int *ctr, int target, int *err) {
+    if (threadIdx.x == 0) {
+        int spins = 0;
+        while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (++spins > kSpinLimit) {
+                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(16);   // ~1000 cycles: hundreds of pollers stay light
+        }
+    }
+    __builtin_amdgcn_s_barrier();
+}
+
+// Staging of rows rowlist[pos0 .. pos0 + rows) of src, columns [k0, k0 + kc),
+// into LDS rows of stride kLd by global-to-LDS DMA (no registers): wave w
+// copies rows w, w + 4, ... as two 1 KB pieces each (64 lanes x 16 bytes),
+// columns clamped to the source row.  Columns past kc and rows past rows are
+// never read.
+__device__ inline void stage_lds(float *xs, const float *src, int ld, const int *rowlist,
+                                 int pos0, int rows, int k0, int kc) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int r = wave; r < rows; r += 4) {
+        const float *srow = src + (size_t)rowlist[pos0 + r] * ld;
+#pragma unroll
+        for (int p = 0; p < kChunk / 256; ++p)
+            if (256 * p < kc)
+                __builtin_amdgcn_global_load_lds(srow + min(k0 + 256 * p + 4 * lane, ld - 4),
+                                                 xs + r * kLd + 256 * p, 16, 0, 0);
+    }
+}
+
+// s_waitcnt with only the vector-memory count limited (expcnt and lgkmcnt at
+// their maxima).
+#define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | 0x0F70)
+
+// Streams NB weight rows (NB = 2: gate and up of the lane's feature, NB = 1:
+// one down row) over nq 16-wide K steps against RB 16-row activation blocks
+// in LDS.  The stream is cut into groups of kU = 8/NB steps held in two
+// register sets; the loads of group g + 2 are issued as soon as group g's
+// MFMAs are done, so one to two groups (8 to 16 16-byte loads per lane) stay
+// in flight.
+template <int NB> struct Unroll { static constexpr int kU = 8 / NB; };
+
+template <int NB>
+using WGroup = floatx4[Unroll<NB>::kU][NB];
+
+// Loads steps q .. q + kU - 1 of the stream, each clamped to step last (so
+// a short chunk never reads past its weights).
+template <int NB>
+__device__ inline void wload(const float *const (&pb)[2], int q, int last, WGroup<NB> &w) {
+#pragma unroll
+    for (int u = 0; u < Unroll<NB>::kU; ++u)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            w[u][b] = *reinterpret_cast<const floatx4 *>(pb[b] + kUnit * min(q + u, last));
+}
+
+// Issues the loads of groups 0 and 1 of a chunk of nq steps, unconditionally
+// (wait counts stay exact); groups the chunk lacks are never used.
+template <int NB>
+__device__ inline void gemv_prime(const float *p0, const float *p1, int nq, WGroup<NB> &wa,
+                                  WGroup<NB> &wb) {
+    constexpr int kU = Unroll<NB>::kU;
+    const float *const pb[2] = {p0, p1};
+    wload<NB>(pb, 0, nq - 1, wa);
+    wload<NB>(pb, kU, nq - 1, wb);
+}
+
+template <int NB, int RB>
+__device__ inline void gemv_group(const float *as, int q, const WGroup<NB> &w,
+                                  floatx4 (&acc)[2][NB]) {
+#pragma unroll
+    for (int u = 0; u < Unroll<NB>::kU; ++u) {
+        floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 16 * (q + u));
+        floatx4 a1;
+        if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as + 16 * kLd + 16 * (q + u));
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                acc[0][b] = mfma16(a0[s], w[u][b][s], acc[0][b]);
+                if (RB == 2) acc[1][b] = mfma16(a1[s], w[u][b][s], acc[1][b]);
+            }
+    }
+}
+
+// wa / wb must hold groups 0 / 1 (gemv_prime).
+template <int NB, int RB>
+__device__ inline void gemv_loop(const float *p0, const float *p1, const float *as, int nq,
+                                 floatx4 (&acc)[2][NB], WGroup<NB> &wa, WGroup<NB> &wb) {
+    constexpr int kU = Unroll<NB>::kU;
+    const float *const pb[2] = {p0, p1};
+    const int ng = nq / kU;
+    int g = 0;
+    // Steady state with unconditional loads (exact wait counts).
+    // (Scheduling barriers keep each group's loads right after the MFMAs
+    // that free its registers.)
+    for (; g + 4 <= ng; g += 2) {
+        gemv_group<NB, RB>(as, kU * g, wa, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        wload<NB>(pb, kU * (g + 2), nq - 1, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        wload<NB>(pb, kU * (g + 3), nq - 1, wb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const int left = ng - g;   // 0 .. 3 groups, the first two already loaded
+    if (left == 3) {
+        gemv_group<NB, RB>(as, kU * g, wa, acc);
+        wload<NB>(pb, kU * (g + 2), nq - 1, wa);
+        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
+        gemv_group<NB, RB>(as, kU * (g + 2), wa, acc);
+    } else if (left == 2) {
+        gemv_group<NB, RB>(as, kU * g, wa, acc);
+        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
+    } else if (left == 1) {
+        gemv_group<NB, RB>(as, kU * g, wa, acc);
+    }
+    for (int q = kU * ng; q < nq; ++q) {
+        floatx4 w[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) w[b] = *reinterpret_cast<const floatx4 *>(pb[b] + kUnit * q);
+        floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 16 * q);
+        floatx4 a1;
+        if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as + 16 * kLd + 16 * q);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                acc[0][b] = mfma16(a0[s], w[b][s], acc[0][b]);
+                if (RB == 2) acc[1][b] = mfma16(a1[s], w[b][s], acc[1][b]);
+            }
+    }
+}
+
+// Down-projection units of the fused kernel: 8 units (two 16-column blocks
+// of 4 feature units each) per group, clamped to the wave's last unit.
+__device__ inline void dload(const float *pd, int fq, int g, int last, floatx4 (&w)[8]) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+        const int q = min(8 * g + v, last);
+        w[v] = *reinterpret_cast<const floatx4 *>(pd + ((size_t)(q >> 2) * fq + (q & 3)) * kUnit);
+    }
+}
+
+// MFMAs of one down group: column blocks 2g and 2g + 1 of the wave (those
+// below nbw), K = the block's 64 features (A operands from the H block in
+// LDS at as), each block written at yoff + its column once complete
+// (yoff < 0: a row past the pass).
+template <int RB>
+__device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int nbw, int cb0,
+                              const int (&yoff)[2][4], float *yp, int j) {
+    floatx4 ha[2][4];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            ha[b][u] = *reinterpret_cast<const floatx4 *>(as + b * 16 * kHLd + 16 * u);
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+        floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                acc[0] = mfma16(ha[0][u][s], w[4 * bi + u][s], acc[0]);
+                if (RB == 2) acc[1] = mfma16(ha[1][u][s], w[4 * bi + u][s], acc[1]);
+            }
+        const int cb = 2 * g + bi;
+        if (cb < nbw) {
+            const int col = 16 * (cb0 + cb) + j;
+#pragma unroll
+            for (int b = 0; b < RB; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (yoff[b][r] >= 0) yp[yoff[b][r] + col] = acc[b][r];
+        }
+    }
+}
+
+// One gate/up item: expert e, features 64*fb .. 64*fb + 63.  FUSED = false:
+// writes H [n x F] by assignment.  FUSED = true: keeps the 64 H columns in
+// LDS and multiplies them by the matching 64 rows of W_down, writing the
+// split-K partial Yp[fb][a][0 .. d) (the combine adds the F/64 partials in
+// order).  xs: the dynamic LDS (rows, slot list, token list); wcnt: 4 ints
+// of LDS.  MEGA: expert ids come from the same launch (device-scope loads)
+// and, when routed is set, the item first waits for the router.
+template <bool FUSED, bool MEGA>
+__device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *wcnt,
+                            const int *routed, int routed_target, int *err) {
+    int *list = reinterpret_cast<int *>(xs + kRows * kLd);
+    int *tok = list + a.nslots;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, h = lane >> 4;
+    const int f = fb * 64 + wave * 16 + j;
+    // Gate rows of this wave's 16 features form unit row nbg; up rows are
+    // 32 packed rows (2 unit rows) further.
+    const int nbg = 8 * fb + 4 * (wave >> 1) + (wave & 1);
+    const float *pg = a.w + (size_t)e * 2 * a.F * a.d + (size_t)nbg * (a.d / 16) * kUnit + 4 * lane;
+    const float *pu = pg + (size_t)2 * (a.d / 16) * kUnit;
+
+    // Standalone: the slot list first (its loads are not queued behind
+    // weight loads), then per chunk the activation rows (DMA), the first two
+    // weight groups and a wait for the rows only.  MEGA: the first chunk's
+    // weights go out before waiting for the router (routed reaching
+    // routed_target), as they depend on nothing it computes.
+    WGroup<2> wa, wb;
+    if (MEGA && routed) {
+        gemv_prime<2>(pg, pu, min(kChunk, a.d) / 16, wa, wb);
+        wait_count(routed, routed_target, err);
+    }
+    const int id0 = (int)threadIdx.x < a.nslots ? load_id<MEGA>(a.ids + threadIdx.x) : -1;
+    const int cnt = expert_slots<MEGA>(a.ids, a.nslots, e, id0, a.topk, list, tok, wcnt);
+    if (cnt == 0) return;
+    for (int r0 = 0; r0 < cnt; r0 += kRows) {
+        const int rows = min(kRows, cnt - r0);
+        floatx4 acc[2][2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int g = 0; g < 2; ++g) acc[b][g] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int k0 = 0; k0 < a.d; k0 += kChunk) {
+            const int kc = min(kChunk, a.d - k0);
+            __syncthreads();   // every wave is done with the previous rows
+            stage_lds(xs, a.x, a.d, tok, r0, rows, k0, kc);
+            if (MEGA && routed && r0 == 0 && k0 == 0) {
+                WAIT_VMCNT(0);   // primed before the rows
+            } else {
+                gemv_prime<2>(pg + 16 * k0, pu + 16 * k0, kc / 16, wa, wb);
+                WAIT_VMCNT(4 * Unroll<2>::kU);   // the rows, not the weights behind them
+            }
+            __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
+            const float *as = xs + j * kLd + 4 * h;
+            if (rows > 16) gemv_loop<2, 2>(pg + 16 * k0, pu + 16 * k0, as, kc / 16, acc, wa, wb);
+            else           gemv_loop<2, 1>(pg + 16 * k0, pu + 16 * k0, as, kc / 16, acc, wa, wb);
+        }
+        // 16x16 accumulator: lane holds rows 4*(lane/16) + r, column lane%16.
+        if (!FUSED) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = b * 16 + 4 * h + r;
+                    if (row < rows)
+                        a.out[(size_t)list[r0 + row] * a.F + f] =
+                            swiglu_fast(acc[b][0][r], acc[b][1][r]);
+                }
+            continue;
+        }
+        // Down weights first: they depend on nothing computed here.
+        const int fq = a.F / 16;
+        const int nbw = a.d / 64;                      // 16-column blocks per wave
+        const int last = 4 * nbw - 1;
+        const int ngd = (nbw + 1) / 2;
+        const float *pd = a.w2 + (size_t)e * a.d * a.F +
+                          ((size_t)(wave * nbw) * fq + 4 * fb) * kUnit + 4 * lane;
+        // The gate/up weight registers carry the down stream (the next pass,
+        // if any, primes them again).
+        floatx4 (&da)[8] = reinterpret_cast<floatx4 (&)[8]>(wa);
+        floatx4 (&db)[8] = reinterpret_cast<floatx4 (&)[8]>(wb);
+        dload(pd, fq, 0, last, da);
+        dload(pd, fq, 1, last, db);
+        // H block [rows][64] in LDS over the x rows (every wave is past them).
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
+        __builtin_amdgcn_s_barrier();
+        float *hs = xs;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                hs[(b * 16 + 4 * h + r) * kHLd + wave * 16 + j] = swiglu_fast(acc[b][0][r], acc[b][1][r]);
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_s_barrier();
+        const float *as = hs + j * kHLd + 4 * h;
+        // Partial offsets fit in 32 bits: the host caps the partial buffer.
+        int yoff[2][4];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = b * 16 + 4 * h + r;
+                yoff[b][r] = row < rows ? (fb * a.nslots + list[r0 + row]) * a.d : -1;
+            }
+        const int cb0 = wave * nbw;
+        auto run = [&](auto rb) {
+            constexpr int RB = decltype(rb)::value;
+            int g = 0;
+            for (; g + 4 <= ngd; g += 2) {
+                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
+                __builtin_amdgcn_sched_barrier(0);
+                dload(pd, fq, g + 2, last, da);
+                __builtin_amdgcn_sched_barrier(0);
+                dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
+                __builtin_amdgcn_sched_barrier(0);
+                dload(pd, fq, g + 3, last, db);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const int left = ngd - g;
+            if (left == 3) {
+                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
+                dload(pd, fq, g + 2, last, da);
+                dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(da, as, g + 2, nbw, cb0, yoff, a.out, j);
+            } else if (left == 2) {
+                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
+            } else if (left == 1) {
+                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
+            }
+        };
+        if (rows > 16) run(std::integral_constant<int, 2>{});
+        else           run(std::integral_constant<int, 1>{});
+    }
+}
+
+
+}  // namespace
+}  // namespace moe

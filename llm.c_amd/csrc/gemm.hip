@@ -259,6 +259,53 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     }
 }
 
+// The same for many split-K partials (the fused decode kernel writes one per
+// 64 features): G lanes share an output float4, each summing up to 8
+// consecutive partials of a slot in split order; lane 0 adds the G group
+// sums in a fixed tree order and applies the slot's gate weight.
+template <int G>
+__global__ __launch_bounds__(256) void combine_groups_kernel(CombineArgs a) {
+    const int d4 = a.d >> 2;
+    const size_t gid = ((size_t)blockIdx.x * 256 + threadIdx.x) / G;
+    const int g = threadIdx.x % G;
+    const bool valid = gid < (size_t)a.T * d4;
+    const int t = valid ? (int)(gid / d4) : 0, c4 = valid ? (int)(gid % d4) : 0;
+    const int s0 = 8 * g, s1 = min(s0 + 8, a.ksplit);
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int ki = 0; ki < a.k; ++ki) {
+        const float *yp = a.ys + ((size_t)t * a.k + ki) * a.d + 4 * c4;
+        floatx4 p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            p[u] = *reinterpret_cast<const floatx4 *>(yp + (size_t)min(s0 + u, a.ksplit - 1) * a.split_stride);
+        floatx4 y = {0.f, 0.f, 0.f, 0.f};
+        if (s0 < s1) y = p[0];
+#pragma unroll
+        for (int u = 1; u < 8; ++u)
+            if (s0 + u < s1)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) y[j] = y[j] + p[u][j];
+#pragma unroll
+        for (int m = G / 2; m >= 1; m >>= 1)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = y[j] + __shfl_xor(y[j], m, G);
+        const float w = a.gw[(size_t)t * a.k + ki];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = fmaf(w, y[j], acc[j]);
+    }
+    if (valid && g == 0) {
+        floatx4 *o = reinterpret_cast<floatx4 *>(a.out + (size_t)t * a.d + 4 * c4);
+        if (a.accumulate) {
+            floatx4 v = *o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = v[j] + acc[j];
+            *o = v;
+        } else {
+            *o = acc;
+        }
+    }
+}
+
 // Packs source matrix src [K x N] (reference layout) into the unit layout
 // (unpack != 0: the inverse).  Source column c goes to packed row
 // c (mode 0, down), 64*(c/32) + c%32 (mode 1, gate) or that + 32 (mode 2,
@@ -310,6 +357,20 @@ hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) { return launch_
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) { return launch_mode<1>(a, s); }
 
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
+    if (a.ksplit > 8 && a.ksplit <= 128) {
+        const int groups = (a.ksplit + 7) / 8;
+        const size_t n = (size_t)a.T * (a.d >> 2);
+        if (n == 0) return hipSuccess;
+        auto go = [&](auto kern, int G) {
+            hipLaunchKernelGGL(kern, dim3((unsigned)((n * G + 255) / 256)), dim3(256), 0, s, a);
+        };
+        if (groups <= 2)       go(combine_groups_kernel<2>, 2);
+        else if (groups <= 4)  go(combine_groups_kernel<4>, 4);
+        else if (groups <= 8)  go(combine_groups_kernel<8>, 8);
+        else if (groups <= 16) go(combine_groups_kernel<16>, 16);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     size_t total = (size_t)a.T * (a.d >> 2);
     if (total == 0) return hipSuccess;
     unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);

@@ -35,7 +35,7 @@ bool g_timing = false;
 hipEvent_t g_ev[6] = {};
 hipEvent_t g_tev[2] = {};
 bool g_have_times = false;
-int g_path = 0;   // 0 auto, 1 grouped GEMM, 2 skinny decode GEMV
+int g_path = 0;   // 0 auto, 1 grouped GEMM, 2 decode GEMVs, 3 unfused, 4 fused, routed apart
 int g_rpath = 0;  // 0 auto, 1 token x expert tiles, 2 one token per lane
 
 int set_err(int code, const char *fmt, ...) {
@@ -113,6 +113,10 @@ Workspace g_ws;
 // does the tail work"); it is zero between launches because the last
 // workgroup resets it, so it is cleared only when allocated.
 constexpr int kMaxCounters = 64;
+// Further device ints in the same buffer: the decode-layer launch's four
+// counters and its wait-gave-up flag.
+constexpr int kLayerSync = 8;
+constexpr int kLayerErr = 12;
 int ensure_counters() {
     if (g_ws.counters.bytes >= sizeof(int) * kMaxCounters) return MOE_HIP_OK;
     TRY(g_ws.counters.reserve(sizeof(int) * kMaxCounters));
@@ -460,23 +464,68 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
     // Expert products: skinny decode GEMVs (which find their own slots from
     // the expert ids, so routing skips the dispatch) or grouped GEMMs.
     const bool decode_ok = F % 64 == 0 && n <= (size_t)moe::kDecodeMaxSlots;
-    if (g_path == 2 && !decode_ok)
+    if (g_path >= 2 && !decode_ok)
         return set_err(MOE_HIP_ERR_UNSUPPORTED,
                        "decode kernels need ffn_hidden %% 64 == 0 and T*k <= %d", moe::kDecodeMaxSlots);
-    const bool use_decode = g_path == 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
-    TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm, s,
-                   !use_decode));
+    const bool use_decode = g_path >= 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
+    const size_t fused_bytes = sizeof(float) * (size_t)(F / 64) * n * d;
+    const bool fused = use_decode && g_path != 3 && fused_bytes <= moe::kFusedPartialBytes;
+    // Mode 2 runs routing and the fused expert items as one launch where it
+    // fits; everything else routes first (the one-launch layer is not yet
+    // faster: its router competes with the expert weight stream).
+    const bool one_launch = fused && g_path == 2 && g_rpath != 1 &&
+                            moe::decode_layer_supported(d, E);
+    if (!one_launch)
+        TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm,
+                       s, !use_decode));
     int ksplit = 1;
     if (use_decode) {
-        ksplit = moe::decode_ksplit(d, F, E);
-        TRY(g_ws.ys.reserve(sizeof(float) * n * d * ksplit));
-        moe::DecodeArgs gu{x, ids_d, k, L->wgu, g_ws.h.as<float>(), d, F, E, 1, (int)n};
-        HIP_TRY(moe::launch_decode_gateup(gu, s));
-        if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
-        moe::DecodeArgs dn{g_ws.h.as<float>(), ids_d, k, L->wdT, g_ws.ys.as<float>(), d, F,
-                           E, ksplit, (int)n};
-        HIP_TRY(moe::launch_decode_down(dn, s));
-        if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
+        // Fused gate/up + split-K down while its partials stay small, else
+        // gate/up then down.
+        moe::DecodeArgs gu{};
+        gu.x = x; gu.ids = ids_d; gu.topk = k; gu.w = L->wgu;
+        gu.d = d; gu.F = F; gu.E = E; gu.ksplit = 1; gu.nslots = (int)n;
+        if (one_launch) {
+            TRY(ensure_counters());
+            ksplit = F / 64;
+            TRY(g_ws.ys.reserve(fused_bytes));
+            gu.out = g_ws.ys.as<float>();
+            gu.w2 = L->wdT;
+            moe::LayerArgs la{};
+            la.r = moe::RouteArgs{x, L->wr, L->bias, T, d, E, k, probs, ids_d, gw};
+            la.r.wrT = L->wrT;
+            la.r.wr_nonfinite = L->wr_nonfinite;
+            la.r.no_dispatch = 1;
+            la.g = gu;
+            la.sync = g_ws.counters.as<int>() + kLayerSync;
+            la.err = g_ws.counters.as<int>() + kLayerErr;
+            if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
+            HIP_TRY(moe::launch_decode_layer(la, s));
+            if (g_timing)
+                for (int i = 1; i <= 4; ++i) HIP_TRY(hipEventRecord(g_ev[i], s));
+        } else if (fused) {
+            ksplit = F / 64;
+            TRY(g_ws.ys.reserve(fused_bytes));
+            gu.out = g_ws.ys.as<float>();
+            gu.w2 = L->wdT;
+            HIP_TRY(moe::launch_decode_gateup(gu, s));
+            if (g_timing) {
+                HIP_TRY(hipEventRecord(g_ev[3], s));
+                HIP_TRY(hipEventRecord(g_ev[4], s));
+            }
+        } else {
+            ksplit = moe::decode_ksplit(d, F, E);
+            TRY(g_ws.ys.reserve(sizeof(float) * n * d * ksplit));
+            gu.out = g_ws.h.as<float>();
+            HIP_TRY(moe::launch_decode_gateup(gu, s));
+            if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
+            moe::DecodeArgs dn{};
+            dn.x = g_ws.h.as<float>(); dn.ids = ids_d; dn.topk = k; dn.w = L->wdT;
+            dn.out = g_ws.ys.as<float>(); dn.d = d; dn.F = F; dn.E = E; dn.ksplit = ksplit;
+            dn.nslots = (int)n;
+            HIP_TRY(moe::launch_decode_down(dn, s));
+            if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
+        }
     } else {
         const int max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
         const int *tile_e = g_ws.tile_expert.as<int>();
@@ -505,7 +554,7 @@ int moe_hip_set_router_path(int mode) {
 }
 
 int moe_hip_set_expert_path(int mode) {
-    if (mode < 0 || mode > 2) return set_err(MOE_HIP_ERR_ARG, "expert path mode %d", mode);
+    if (mode < 0 || mode > 4) return set_err(MOE_HIP_ERR_ARG, "expert path mode %d", mode);
     g_path = mode;
     return MOE_HIP_OK;
 }
@@ -684,4 +733,15 @@ int moe_hip_graph_destroy(void *graph) {
     if (G->graph) (void)hipGraphDestroy(G->graph);
     delete G;
     return MOE_HIP_OK;
+}
+
+int moe_hip_device_check(void) {
+    TRY(ensure_init());
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    if (g_ws.counters.bytes < sizeof(int) * kMaxCounters) return MOE_HIP_OK;
+    int flag = 0;
+    HIP_TRY(hipMemcpy(&flag, g_ws.counters.as<int>() + kLayerErr, sizeof(int), hipMemcpyDeviceToHost));
+    if (!flag) return MOE_HIP_OK;
+    HIP_TRY(hipMemset(g_ws.counters.as<int>() + kLayerErr, 0, sizeof(int)));
+    return set_err(MOE_HIP_ERR_HIP, "a bounded device-side wait gave up (results invalid)");
 }

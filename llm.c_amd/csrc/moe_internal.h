@@ -82,7 +82,9 @@ struct DecodeArgs {
     const int *ids;      // [n] expert of each assignment a = t*k + slot
     int topk;
     const float *w;      // packed weights (wgu or wdT)
-    float *out;          // gate/up: H [n x F]; down: Yp [ksplit][n][d], both by assignment
+    float *out;          // gate/up: H [n x F]; down: Yp [ksplit][n][d], both by assignment;
+                         // fused gate/up + down: Yp [F/64][n][d]
+    const float *w2;     // gate/up only: wdT for the fused kernel, or nullptr
     int d, F, E;
     int ksplit;          // down: splits of the F reduction
     int nslots;          // n = T * k
@@ -90,6 +92,21 @@ struct DecodeArgs {
 
 // Most assignments (T * k) the decode kernels take (LDS slot list).
 constexpr int kDecodeMaxSlots = 4096;
+// Largest split-K partial buffer ([F/64][T*k][d] floats) the fused decode
+// kernel may write; larger layers use the separate down kernel.
+constexpr size_t kFusedPartialBytes = (size_t)32 << 20;
+
+// One launch per decode layer: routing plus fused gate/up + split-K down
+// items (layer.hip).  sync: 4 ints, zero between launches; err: raised if a
+// bounded device-side wait gave up.
+struct LayerArgs {
+    RouteArgs r;         // wrT set; ids written device-coherently; no dispatch
+    DecodeArgs g;        // w2 set: fused items writing Yp [F/64][n][d]
+    int *sync;
+    int *err;
+};
+bool decode_layer_supported(int d, int E);
+hipError_t launch_decode_layer(const LayerArgs &a, hipStream_t s);
 
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);

@@ -1,0 +1,307 @@
+// route_rows.h — the row-block router as a device function, shared by the
+// routing kernel (route.hip) and the fused decode-layer kernel (layer.hip).
+// Both translation units are built with fp32 denormal flushing, matching
+// the FTZ/DAZ mode of the reference's -ffast-math executables.
+#pragma once
+#include "moe_internal.h"
+#include "moe_math.h"
+
+namespace moe {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Row-block router.  A workgroup owns 16 tokens and every expert, so routing
+// needs no cross-workgroup exchange.  Lane 16*r + c of wave w runs the
+// chains of token t0 + c with experts 4*(w*RE + j) + r, j < RE, over k
+// ascending.  x reaches the lanes through LDS (float4 reads; the four 16-lane
+// rows read the same token row); each expert's router row sits in VGPRs
+// sixteen k-values at a time (lane c of row r holds k0 + c of row r's
+// expert) and reaches all lanes of the row through DPP row_newbcast inside
+// the FMA, so the broadcast costs no instruction.
+//
+// Zero-skip: the reference skips x == 0 (src/matrix.c:394).  For finite
+// router weights fma(0, w, acc) returns acc up to the sign of a zero
+// accumulator, and a logit of +0 or -0 gives the same probabilities bit for
+// bit (every path of the softmax maps both to the same value), so SKIP = false
+// is exact for them.  Router weights holding an inf or NaN (0 * inf = NaN)
+// take the SKIP = true variant, which applies the skip per step.
+// ---------------------------------------------------------------------------
+
+// acc = fma(w from lane 16*row + J, x[J], acc) for J = 0..15 in order.  The
+// leading s_nop gives the wait states a DPP source read needs after a VALU
+// write of that register or of EXEC.
+__device__ inline void chain16_dpp(float &acc, float w, const float (&x)[16]) {
+    asm("s_nop 4\n\t"
+        "v_fmac_f32_dpp %0, %1, %2 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %3 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %4 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %10 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %11 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %12 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %13 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %14 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %15 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %16 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_fmac_f32_dpp %0, %1, %17 row_newbcast:15 row_mask:0xf bank_mask:0xf\n\t"
+        : "+v"(acc)
+        : "v"(w), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
+}
+
+template <int J>
+__device__ inline float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xF, 0xF, true));
+}
+
+// The same chain with the reference's per-step zero-skip.
+template <int J>
+struct SkipChain {
+    __device__ static inline void run(float &acc, float w, const float (&x)[16]) {
+        SkipChain<J - 1>::run(acc, w, x);
+        const float wj = row_bcast<J - 1>(w);
+        acc = (x[J - 1] != 0.0f) ? fmaf(x[J - 1], wj, acc) : acc;
+    }
+};
+template <>
+struct SkipChain<0> {
+    __device__ static inline void run(float &, float, const float (&)[16]) {}
+};
+
+// Lane l of each aligned group of 8 lanes reads lane l ^ M (DPP moves).
+template <int CTRL>
+__device__ inline int dpp_mov(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int M> __device__ inline int xor8(int v);
+template <> __device__ inline int xor8<1>(int v) { return dpp_mov<0xB1>(v); }   // quad_perm [1,0,3,2]
+template <> __device__ inline int xor8<2>(int v) { return dpp_mov<0x4E>(v); }   // quad_perm [2,3,0,1]
+template <> __device__ inline int xor8<4>(int v) {
+    const int up = dpp_mov<0x104>(v);   // row_shl:4, lane i reads lane i + 4
+    const int dn = dpp_mov<0x114>(v);   // row_shr:4, lane i reads lane i - 4
+    return (threadIdx.x & 4) ? dn : up;
+}
+template <int M> __device__ inline float xor8f(float v) {
+    return __int_as_float(xor8<M>(__float_as_int(v)));
+}
+
+// Eight consecutive lanes finish one token: lane l plays lane l of the
+// reference's 8-wide vectors, so softmax_rows (src/matrix.c:529-586) keeps
+// its per-lane maxima and sums and hsum256's fold order
+// (include/simd.h:110-121) becomes three butterfly steps; every lane then
+// runs the scalar tail in the reference's order.  Top-k
+// (src/transformer.c:317-331) is k rounds of an argmax over the experts not
+// yet chosen, ties to the lowest index, reduced across the eight lanes; lane
+// 0 records each round's expert and probability in id_out / p_out and the
+// returned value is the renormalisation factor (src/transformer.c:334-336).
+// Every lane of the wave calls this together.
+__device__ inline float finish_token8(const RouteArgs &a, float *row, int l, int *id_out,
+                                      float *p_out) {
+    const int E = a.E, k = a.k;
+    const int nb = E >> 3, tail = E - 8 * nb;
+    float m = -1e38f;
+    for (int b = 0; b < nb; ++b) m = fmaxf(m, row[8 * b + l]);
+    m = fmaxf(m, xor8f<4>(m));
+    m = fmaxf(m, xor8f<2>(m));
+    m = fmaxf(m, xor8f<1>(m));
+    for (int j = 8 * nb; j < E; ++j) {
+        const float v = row[j];
+        if (v > m) m = v;
+    }
+    float vs = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const float ex = exp_poly(row[8 * b + l] - m);
+        row[8 * b + l] = ex;
+        vs = vs + ex;
+    }
+    vs = vs + xor8f<4>(vs);   // v_l + v_(l+4)
+    vs = vs + xor8f<1>(vs);   // (v0+v4) + (v1+v5) and (v2+v6) + (v3+v7)
+    vs = vs + xor8f<2>(vs);   // the two halves
+    for (int j = 8 * nb; j < E; ++j) {
+        const float ex = glibc_expf(row[j] - m);
+        vs = vs + ex;
+        if (l == 0) row[j] = ex;
+    }
+    const float inv = 1.0f / vs;
+    for (int b = 0; b < nb; ++b) row[8 * b + l] = ftz_f(row[8 * b + l] * inv);
+    if (l < tail) row[8 * nb + l] = ftz_f(row[8 * nb + l] * inv);
+
+    uint64_t chosen0 = 0, chosen1 = 0;
+    float s = 0.0f;
+    for (int ki = 0; ki < k; ++ki) {
+        float best = -1.0f;
+        int be = 0x7fffffff;
+        auto consider = [&](int e) {
+            const uint64_t bit = e < 64 ? (chosen0 >> e) & 1ull : (chosen1 >> (e - 64)) & 1ull;
+            const float v = row[e];
+            if (!bit && v > best) { best = v; be = e; }
+        };
+        for (int b = 0; b < nb; ++b) consider(8 * b + l);
+        if (l < tail) consider(8 * nb + l);
+        auto merge = [&](float ob, int oe) {
+            if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; }
+        };
+        merge(xor8f<4>(best), xor8<4>(be));
+        merge(xor8f<2>(best), xor8<2>(be));
+        merge(xor8f<1>(best), xor8<1>(be));
+        if (be == 0x7fffffff) be = 0;   // nothing beat -1: the reference keeps best_e = 0
+        if (be < 64) chosen0 |= 1ull << be;
+        else         chosen1 |= 1ull << (be - 64);
+        const float p = row[be];
+        s = s + p;
+        if (l == 0) { id_out[ki] = be; p_out[ki] = p; }
+    }
+    return (s > 1e-9f) ? 1.0f / s : 0.0f;
+}
+
+// LDS layout of route_rows_block (floats): x chunks, logits rows, chosen
+// probabilities and experts, renormalisation factors.
+template <int KC>
+struct RowsSmem {
+    static constexpr int kLd = KC + 4;
+    static constexpr int kLg = 2 * 16 * kLd;
+    static constexpr int kPSel = kLg + 16 * (kMaxExperts + 1);
+    static constexpr int kIdSel = kPSel + 16 * kMaxTopK;
+    static constexpr int kInv = kIdSel + 16 * kMaxTopK;
+    static constexpr int kFloats = kInv + 16;
+};
+
+// Routes token block tb (tokens 16*tb ..) with NWV waves; every thread of
+// the workgroup calls this.  smem: RowsSmem<KC>::kFloats floats of LDS,
+// 16-byte aligned.  COHERENT: expert ids are stored with device-scope
+// atomic stores, for other workgroups of the same launch to read, and
+// *loaded (if set) is incremented once the first chunk of x and router
+// rows is in LDS.
+template <int NWV, int RE, int KC, bool SKIP, bool COHERENT>
+__device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *loaded = nullptr) {
+    static_assert(NWV >= 2, "two waves finish the block's 16 tokens");
+    constexpr int NT = 64 * NWV;
+    constexpr int LD = KC + 4;                     // padded LDS row of x (floats)
+    constexpr int XQ = 16 * KC / 4;                // float4s of x per chunk
+    constexpr int XL = (XQ + NT - 1) / NT;
+    constexpr int WV = KC / 16;                    // router VGPRs per expert per chunk
+    using S = RowsSmem<KC>;
+    float (*xs)[16][LD] = reinterpret_cast<float (*)[16][LD]>(smem);
+    float (*lg)[kMaxExperts + 1] = reinterpret_cast<float (*)[kMaxExperts + 1]>(smem + S::kLg);
+    float (*p_sel)[kMaxTopK] = reinterpret_cast<float (*)[kMaxTopK]>(smem + S::kPSel);
+    int (*id_sel)[kMaxTopK] = reinterpret_cast<int (*)[kMaxTopK]>(smem + S::kIdSel);
+    float *inv_sel = smem + S::kInv;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r = lane >> 4, c = lane & 15;
+    const int T = a.T, d = a.d, E = a.E, k = a.k;
+    const int t0 = tb * 16;
+
+    // Experts past E repeat expert E - 1 and store nothing; rows past T read
+    // row T - 1 (all lanes stay active for the DPP reads) and store nothing.
+    const float *wrow[RE];
+#pragma unroll
+    for (int j = 0; j < RE; ++j)
+        wrow[j] = a.wrT + (size_t)min(4 * (w * RE + j) + r, E - 1) * d + c;
+
+    float4 rx[XL];
+    float rw[RE][WV], wc[RE][WV];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < XL; ++i) {
+            const int q = min(tid + NT * i, XQ - 1);
+            const int rr = q / (KC / 4), c4 = q % (KC / 4);
+            const int t = min(t0 + rr, T - 1);
+            rx[i] = *reinterpret_cast<const float4 *>(a.x + (size_t)t * d + k0 + 4 * c4);
+        }
+#pragma unroll
+        for (int j = 0; j < RE; ++j)
+#pragma unroll
+            for (int s4 = 0; s4 < WV; ++s4) rw[j][s4] = wrow[j][k0 + 16 * s4];
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XL; ++i) {
+            const int q = tid + NT * i;
+            if (XQ % NT == 0 || q < XQ) {
+                const int rr = q / (KC / 4), c4 = q % (KC / 4);
+                float4 v = rx[i];
+                if (SKIP) v = make_float4(ftz_f(v.x), ftz_f(v.y), ftz_f(v.z), ftz_f(v.w));
+                *reinterpret_cast<float4 *>(&xs[buf][rr][4 * c4]) = v;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < RE; ++j)
+#pragma unroll
+            for (int s4 = 0; s4 < WV; ++s4) wc[j][s4] = rw[j][s4];
+    };
+
+    float acc[RE];
+#pragma unroll
+    for (int j = 0; j < RE; ++j) acc[j] = 0.0f;
+    const int nchunk = d / KC;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    if (COHERENT && loaded && tid == 0)
+        __hip_atomic_fetch_add(loaded, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int ch = 0; ch < nchunk; ++ch) {
+        const int buf = ch & 1;
+        if (ch + 1 < nchunk) gload((ch + 1) * KC);
+        // x of the next 16 steps is read while the FMAs of these run.
+        auto xread = [&](float (&xv)[16], int s4) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = *reinterpret_cast<const float4 *>(&xs[buf][c][16 * s4 + 4 * q]);
+                xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
+            }
+        };
+        auto chains = [&](const float (&xv)[16], int s4) {
+#pragma unroll
+            for (int j = 0; j < RE; ++j) {
+                if (SKIP) SkipChain<16>::run(acc[j], wc[j][s4], xv);
+                else      chain16_dpp(acc[j], wc[j][s4], xv);
+            }
+        };
+        float xa[16], xb[16];
+        xread(xa, 0);
+#pragma unroll
+        for (int s4 = 0; s4 < WV; s4 += 2) {
+            xread(xb, s4 + 1);
+            chains(xa, s4);
+            if (s4 + 2 < WV) xread(xa, s4 + 2);
+            chains(xb, s4 + 1);
+        }
+        if (ch + 1 < nchunk) sstore(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < RE; ++j) {
+        const int e = 4 * (w * RE + j) + r;
+        if (e < E) lg[c][e] = a.bias ? acc[j] + a.bias[e] : acc[j];
+    }
+    __syncthreads();
+    if (tid < 128) {
+        const int ct = tid >> 3, l = tid & 7;
+        const float inv = finish_token8(a, &lg[ct][0], l, &id_sel[ct][0], &p_sel[ct][0]);
+        if (l == 0) inv_sel[ct] = inv;
+    }
+    __syncthreads();
+    const int tn = min(16, T - t0);
+    if (a.ids || a.gw)
+        for (int i = tid; i < tn * k; i += NT) {
+            const int ct = i / k, ki = i - ct * k;
+            const size_t o = (size_t)(t0 + ct) * k + ki;
+            if (a.ids) {
+                if (COHERENT) __hip_atomic_store(&a.ids[o], id_sel[ct][ki], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+                else          a.ids[o] = id_sel[ct][ki];
+            }
+            if (a.gw) a.gw[o] = ftz_f(p_sel[ct][ki] * inv_sel[ct]);
+        }
+    if (a.probs)
+        for (int i = tid; i < tn * E; i += NT) {
+            const int ct = i / E, e = i - ct * E;
+            a.probs[(size_t)(t0 + ct) * E + e] = lg[ct][e];
+        }
+}
+
+}  // namespace
+}  // namespace moe

@@ -60,6 +60,7 @@ SIGNATURES = {
     "moe_hip_set_timing": (C.c_int, [C.c_int]),
     "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
     "moe_hip_set_router_path": (C.c_int, [C.c_int]),
+    "moe_hip_device_check": (C.c_int, []),
     "moe_hip_timer_start": (C.c_int, []),
     "moe_hip_timer_stop": (C.c_int, [_F]),
     "moe_hip_dev_alloc": (C.c_int, [C.POINTER(_P), C.c_size_t]),
@@ -266,8 +267,15 @@ class Graph:
 
 
 def set_expert_path(mode):
-    """0 automatic, 1 grouped GEMMs, 2 skinny decode GEMVs."""
+    """0 automatic, 1 grouped GEMMs, 2 decode GEMVs (fused gate/up + down,
+    routed in the same launch where supported), 3 decode GEMVs as two
+    launches, 4 fused decode GEMVs routed by a launch of their own."""
     check(lib().moe_hip_set_expert_path(int(mode)))
+
+
+def device_check():
+    """Raises if a bounded device-side wait gave up since the last check."""
+    check(lib().moe_hip_device_check())
 
 
 def set_router_path(mode):

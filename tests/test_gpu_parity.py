@@ -300,7 +300,7 @@ def test_decode_batch_c4():
     assert_close(x_one - x0[:1], o1, "c4 decode step")
 
 
-@pytest.mark.parametrize("path", [2, 1], ids=["gemv", "gemm"])
+@pytest.mark.parametrize("path", [2, 3, 4, 1], ids=["gemv", "gemv2", "gemv4", "gemm"])
 def test_graph_replay(path):
     """A captured forward (two layers, accumulating) replays to the same bits
     as the eager calls, replay after replay, with eager work and
@@ -333,7 +333,7 @@ def test_graph_replay(path):
             for i in ids:
                 i.zero()
             g.launch()
-            mh.synchronize()
+            mh.device_check()
             assert np.array_equal(bits(out.to_host()), bits(ref)), f"replay {rep}: output differs"
             for i, r in zip(ids, ref_ids):
                 assert np.array_equal(i.to_host(), r), f"replay {rep}: expert ids differ"
@@ -398,12 +398,22 @@ def test_error_paths():
 
 
 FORCED_PATH_CASES = [
-    # name, T, d, F, E, k, path (1 = grouped GEMMs, 2 = decode GEMVs)
+    # name, T, d, F, E, k, path (1 = grouped GEMMs, 2 = fused decode GEMVs,
+    # routed in the same launch where supported, 3 = decode GEMVs as two
+    # launches, 4 = fused decode GEMVs routed by their own launch)
     ("c4_gemv", 64, 512, 2048, 16, 2, 2),
+    ("c4_gemv2", 64, 512, 2048, 16, 2, 3),
+    ("c4_gemv4", 64, 512, 2048, 16, 2, 4),
+    ("e64_layer", 48, 256, 256, 64, 4, 2),           # 4 experts per lane row
+    ("many_blocks_layer", 1500, 128, 128, 8, 2, 2),  # 94 router blocks, 16 items
     ("c4_gemm", 64, 512, 2048, 16, 2, 1),
     ("multipass_gemv", 200, 128, 256, 4, 2, 2),     # ~100 rows per expert: 4 passes
+    ("multipass_gemv2", 200, 128, 256, 4, 2, 3),
     ("kchunks_gemv", 48, 1024, 512, 16, 2, 2),      # d = 1024: two K chunks
+    ("kchunks_gemv2", 48, 1024, 512, 16, 2, 3),
+    ("oddblocks_gemv", 40, 192, 128, 8, 2, 2),      # d / 64 = 3 column blocks per wave
     ("tiny_gemv", 5, 64, 64, 8, 3, 2),
+    ("tiny_gemv2", 5, 64, 64, 8, 3, 3),
     ("wide_gemm", 300, 256, 1024, 8, 2, 1),
 ]
 
@@ -418,6 +428,7 @@ def test_forced_expert_paths(name, T, d, F, E, k, path):
     mh.set_expert_path(path)
     try:
         out, probs, ids = mh.moe_forward(x, hw)
+        mh.device_check()
     finally:
         mh.set_expert_path(0)
     o_ref, p_ref, i_ref = orc.moe_forward(x, hw)
