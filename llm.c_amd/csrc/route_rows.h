@@ -98,25 +98,34 @@ template <int M> __device__ inline float xor8f(float v) {
 // 0 records each round's expert and probability in id_out / p_out and the
 // returned value is the renormalisation factor (src/transformer.c:334-336).
 // Every lane of the wave calls this together.
+template <int NBM>
 __device__ inline float finish_token8(const RouteArgs &a, float *row, int l, int *id_out,
                                       float *p_out) {
+    // Lane l keeps its vector elements 8*b + l (b < nb <= NBM) in registers;
+    // the E % 8 tail stays in LDS, read by every lane in order.
     const int E = a.E, k = a.k;
     const int nb = E >> 3, tail = E - 8 * nb;
+    float v[NBM];
+#pragma unroll
+    for (int b = 0; b < NBM; ++b) v[b] = b < nb ? row[8 * b + l] : 0.0f;
     float m = -1e38f;
-    for (int b = 0; b < nb; ++b) m = fmaxf(m, row[8 * b + l]);
+#pragma unroll
+    for (int b = 0; b < NBM; ++b)
+        if (b < nb) m = fmaxf(m, v[b]);
     m = fmaxf(m, xor8f<4>(m));
     m = fmaxf(m, xor8f<2>(m));
     m = fmaxf(m, xor8f<1>(m));
     for (int j = 8 * nb; j < E; ++j) {
-        const float v = row[j];
-        if (v > m) m = v;
+        const float t = row[j];
+        if (t > m) m = t;
     }
     float vs = 0.0f;
-    for (int b = 0; b < nb; ++b) {
-        const float ex = exp_poly(row[8 * b + l] - m);
-        row[8 * b + l] = ex;
-        vs = vs + ex;
-    }
+#pragma unroll
+    for (int b = 0; b < NBM; ++b)
+        if (b < nb) {
+            v[b] = exp_poly(v[b] - m);
+            vs = vs + v[b];
+        }
     vs = vs + xor8f<4>(vs);   // v_l + v_(l+4)
     vs = vs + xor8f<1>(vs);   // (v0+v4) + (v1+v5) and (v2+v6) + (v3+v7)
     vs = vs + xor8f<2>(vs);   // the two halves
@@ -126,31 +135,44 @@ __device__ inline float finish_token8(const RouteArgs &a, float *row, int l, int
         if (l == 0) row[j] = ex;
     }
     const float inv = 1.0f / vs;
-    for (int b = 0; b < nb; ++b) row[8 * b + l] = ftz_f(row[8 * b + l] * inv);
-    if (l < tail) row[8 * nb + l] = ftz_f(row[8 * nb + l] * inv);
+#pragma unroll
+    for (int b = 0; b < NBM; ++b)
+        if (b < nb) {
+            v[b] = ftz_f(v[b] * inv);
+            row[8 * b + l] = v[b];
+        }
+    float tv = 0.0f;
+    if (l < tail) {
+        tv = ftz_f(row[8 * nb + l] * inv);
+        row[8 * nb + l] = tv;
+    }
 
     uint64_t chosen0 = 0, chosen1 = 0;
     float s = 0.0f;
     for (int ki = 0; ki < k; ++ki) {
         float best = -1.0f;
         int be = 0x7fffffff;
-        auto consider = [&](int e) {
+        auto consider = [&](int e, float p) {
             const uint64_t bit = e < 64 ? (chosen0 >> e) & 1ull : (chosen1 >> (e - 64)) & 1ull;
-            const float v = row[e];
-            if (!bit && v > best) { best = v; be = e; }
+            if (!bit && p > best) { best = p; be = e; }
         };
-        for (int b = 0; b < nb; ++b) consider(8 * b + l);
-        if (l < tail) consider(8 * nb + l);
+#pragma unroll
+        for (int b = 0; b < NBM; ++b)
+            if (b < nb) consider(8 * b + l, v[b]);
+        if (l < tail) consider(8 * nb + l, tv);
         auto merge = [&](float ob, int oe) {
             if (ob > best || (ob == best && oe < be)) { best = ob; be = oe; }
         };
         merge(xor8f<4>(best), xor8<4>(be));
         merge(xor8f<2>(best), xor8<2>(be));
         merge(xor8f<1>(best), xor8<1>(be));
-        if (be == 0x7fffffff) be = 0;   // nothing beat -1: the reference keeps best_e = 0
+        float p = best;   // the chosen probability itself
+        if (be == 0x7fffffff) {   // nothing beat -1: the reference keeps best_e = 0
+            be = 0;
+            p = row[0];
+        }
         if (be < 64) chosen0 |= 1ull << be;
         else         chosen1 |= 1ull << (be - 64);
-        const float p = row[be];
         s = s + p;
         if (l == 0) { id_out[ki] = be; p_out[ki] = p; }
     }
@@ -280,7 +302,8 @@ __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *l
     __syncthreads();
     if (tid < 128) {
         const int ct = tid >> 3, l = tid & 7;
-        const float inv = finish_token8(a, &lg[ct][0], l, &id_sel[ct][0], &p_sel[ct][0]);
+        const float inv = finish_token8<(4 * NWV * RE + 7) / 8>(a, &lg[ct][0], l, &id_sel[ct][0],
+                                                                &p_sel[ct][0]);
         if (l == 0) inv_sel[ct] = inv;
     }
     __syncthreads();
