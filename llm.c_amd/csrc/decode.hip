@@ -42,11 +42,13 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
     const int rem = blockIdx.x % (ncb * S);
     const int cb = rem / S, sp = rem % S;
     const int kspan = a.F / S, kbeg = sp * kspan;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const unsigned lo = 16u * lane;   // the lane's column of each weight unit
     const int j = lane & 15, h = lane >> 4;
     const int col = cb * 64 + wave * 16 + j;
-    const float *pw = a.w + (size_t)e * a.d * a.F +
-                      ((size_t)(cb * 4 + wave) * (a.F / 16) + kbeg / 16) * kUnit + 4 * lane;
+    const WSrc ws = wsrc(a.w + (size_t)e * a.d * a.F, (size_t)a.d * a.F, lo);
+    const int ow = kUnitBytes * ((cb * 4 + wave) * (a.F / 16) + kbeg / 16);
     const size_t nslots = (size_t)a.nslots;
 
     const int id0 = (int)threadIdx.x < a.nslots ? a.ids[threadIdx.x] : -1;
@@ -60,12 +62,12 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
             const int kc = min(kChunk, kspan - k0);
             __syncthreads();   // every wave is done with the previous rows
             stage_lds(hs, a.x, a.F, list, r0, rows, kbeg + k0, kc);
-            gemv_prime<1>(pw + 16 * k0, nullptr, kc / 16, wa, wb);
+            gemv_prime<1>(ws, ow + 64 * k0, 0, kc / 16, wa, wb);
             WAIT_VMCNT(2 * Unroll<1>::kU);   // the rows, not the weights behind them
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
             const float *as = hs + j * kLd + 4 * h;
-            if (rows > 16) gemv_loop<1, 2>(pw + 16 * k0, nullptr, as, kc / 16, acc, wa, wb);
-            else           gemv_loop<1, 1>(pw + 16 * k0, nullptr, as, kc / 16, acc, wa, wb);
+            if (rows > 16) gemv_loop<1, 2>(ws, ow + 64 * k0, 0, as, kc / 16, acc, wa, wb);
+            else           gemv_loop<1, 1>(ws, ow + 64 * k0, 0, as, kc / 16, acc, wa, wb);
         }
 #pragma unroll
         for (int b = 0; b < 2; ++b)

@@ -127,26 +127,52 @@ template <int NB> struct Unroll { static constexpr int kU = 8 / NB; };
 template <int NB>
 using WGroup = floatx4[Unroll<NB>::kU][NB];
 
-// Loads steps q .. q + kU - 1 of the stream, each clamped to step last (so
-// a short chunk never reads past its weights).
-template <int NB>
-__device__ inline void wload(const float *const (&pb)[2], int q, int last, WGroup<NB> &w) {
+// One expert's packed weight block as a buffer resource (four SGPRs,
+// range-checked against the block's size) plus the lane's byte offset lo
+// (one VGPR): every weight load is then lo + a wave-uniform byte offset
+// (SGPR and immediate), which keeps address arithmetic off the VGPRs.
+// Blocks stay below 2 GiB (the host checks), so offsets fit an int.
+struct WSrc {
+    __amdgpu_buffer_rsrc_t r;
+    unsigned lo;
+};
+
+__device__ inline WSrc wsrc(const float *block, size_t nfloats, unsigned lo) {
+    // dword 3 = 0x00020000: 32-bit data format, the gfx9 raw-buffer form.
+    return WSrc{__builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(block), (short)0,
+                                                  (int)(nfloats * sizeof(float)), 0x00020000),
+                lo};
+}
+
+// The 16-byte piece at byte offset off (wave-uniform) of a weight row.
+__device__ inline floatx4 ldw(const WSrc &s, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(s.r, s.lo, off, 0);
+}
+
+// Byte size of a unit (a 16-wide K step of 16 rows).
+constexpr int kUnitBytes = kUnit * (int)sizeof(float);
+
+// Loads steps q .. q + kU - 1 of the stream rows at byte offsets ob[b], each
+// clamped to step last (CLAMP; so a short chunk never reads past its
+// weights).
+template <int NB, bool CLAMP = true>
+__device__ inline void wload(const WSrc &s, const int (&ob)[2], int q, int last, WGroup<NB> &w) {
 #pragma unroll
     for (int u = 0; u < Unroll<NB>::kU; ++u)
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-            w[u][b] = *reinterpret_cast<const floatx4 *>(pb[b] + kUnit * min(q + u, last));
+            w[u][b] = ldw(s, ob[b] + kUnitBytes * (CLAMP ? min(q + u, last) : q + u));
 }
 
 // Issues the loads of groups 0 and 1 of a chunk of nq steps, unconditionally
 // (wait counts stay exact); groups the chunk lacks are never used.
 template <int NB>
-__device__ inline void gemv_prime(const float *p0, const float *p1, int nq, WGroup<NB> &wa,
+__device__ inline void gemv_prime(const WSrc &s, int o0, int o1, int nq, WGroup<NB> &wa,
                                   WGroup<NB> &wb) {
     constexpr int kU = Unroll<NB>::kU;
-    const float *const pb[2] = {p0, p1};
-    wload<NB>(pb, 0, nq - 1, wa);
-    wload<NB>(pb, kU, nq - 1, wb);
+    const int ob[2] = {o0, o1};
+    wload<NB>(s, ob, 0, nq - 1, wa);
+    wload<NB>(s, ob, kU, nq - 1, wb);
 }
 
 template <int NB, int RB>
@@ -167,33 +193,69 @@ __device__ inline void gemv_group(const float *as, int q, const WGroup<NB> &w,
     }
 }
 
+// Down-projection units of the fused kernel: 8 units (two 16-column blocks
+// of 4 feature units each) per group, clamped to the wave's last unit.
+__device__ inline void dload(const WSrc &s, int od, int fq, int g, int last, floatx4 (&w)[8]) {
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+        const int q = min(8 * g + v, last);
+        w[v] = ldw(s, od + kUnitBytes * ((q >> 2) * fq + (q & 3)));
+    }
+}
+
+// Where the fused kernel's down stream starts: its first two groups go out
+// from the tail of the last gate/up chunk (into the registers that chunk
+// frees), so the weight stream does not drain between the two products.
+struct DownHead {
+    WSrc s;
+    int od, fq, last;
+};
+
 // wa / wb must hold groups 0 / 1 (gemv_prime).
-template <int NB, int RB>
-__device__ inline void gemv_loop(const float *p0, const float *p1, const float *as, int nq,
-                                 floatx4 (&acc)[2][NB], WGroup<NB> &wa, WGroup<NB> &wb) {
+// HEAD: also issues down groups 0 and 1 into wa and wb (NB = 2 only).
+template <int NB, int RB, bool HEAD = false>
+__device__ inline void gemv_loop(const WSrc &s, int o0, int o1, const float *as, int nq,
+                                 floatx4 (&acc)[2][NB], WGroup<NB> &wa, WGroup<NB> &wb,
+                                 const DownHead &dh = DownHead{}) {
     constexpr int kU = Unroll<NB>::kU;
-    const float *const pb[2] = {p0, p1};
+    static_assert(!HEAD || NB == 2, "the down stream reuses the gate/up registers");
+    auto head = [&](int g, WGroup<NB> &w) {
+        if constexpr (HEAD)
+            dload(dh.s, dh.od, dh.fq, g, dh.last, reinterpret_cast<floatx4 (&)[8]>(w));
+    };
+    const int ob[2] = {o0, o1};
     const int ng = nq / kU;
     int g = 0;
-    // Steady state with unconditional loads (exact wait counts).
+    // Steady state with unconditional loads (exact wait counts); groups
+    // g + 2 and g + 3 lie inside the chunk, so they go unclamped.
     // (Scheduling barriers keep each group's loads right after the MFMAs
     // that free its registers.)
     for (; g + 4 <= ng; g += 2) {
         gemv_group<NB, RB>(as, kU * g, wa, acc);
         __builtin_amdgcn_sched_barrier(0);
-        wload<NB>(pb, kU * (g + 2), nq - 1, wa);
+        wload<NB, false>(s, ob, kU * (g + 2), nq - 1, wa);
         __builtin_amdgcn_sched_barrier(0);
         gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
         __builtin_amdgcn_sched_barrier(0);
-        wload<NB>(pb, kU * (g + 3), nq - 1, wb);
+        wload<NB, false>(s, ob, kU * (g + 3), nq - 1, wb);
         __builtin_amdgcn_sched_barrier(0);
     }
     const int left = ng - g;   // 0 .. 3 groups, the first two already loaded
     if (left == 3) {
         gemv_group<NB, RB>(as, kU * g, wa, acc);
-        wload<NB>(pb, kU * (g + 2), nq - 1, wa);
+        wload<NB>(s, ob, kU * (g + 2), nq - 1, wa);
         gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
         gemv_group<NB, RB>(as, kU * (g + 2), wa, acc);
+    } else if (left == 2 && nq == kU * ng) {
+        // (the common case: each down group goes out as its registers free)
+        gemv_group<NB, RB>(as, kU * g, wa, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        head(0, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        head(1, wb);
+        return;
     } else if (left == 2) {
         gemv_group<NB, RB>(as, kU * g, wa, acc);
         gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
@@ -203,7 +265,7 @@ __device__ inline void gemv_loop(const float *p0, const float *p1, const float *
     for (int q = kU * ng; q < nq; ++q) {
         floatx4 w[NB];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) w[b] = *reinterpret_cast<const floatx4 *>(pb[b] + kUnit * q);
+        for (int b = 0; b < NB; ++b) w[b] = ldw(s, ob[b] + kUnitBytes * q);
         floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 16 * q);
         floatx4 a1;
         if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as + 16 * kLd + 16 * q);
@@ -215,16 +277,8 @@ __device__ inline void gemv_loop(const float *p0, const float *p1, const float *
                 if (RB == 2) acc[1][b] = mfma16(a1[s], w[b][s], acc[1][b]);
             }
     }
-}
-
-// Down-projection units of the fused kernel: 8 units (two 16-column blocks
-// of 4 feature units each) per group, clamped to the wave's last unit.
-__device__ inline void dload(const float *pd, int fq, int g, int last, floatx4 (&w)[8]) {
-#pragma unroll
-    for (int v = 0; v < 8; ++v) {
-        const int q = min(8 * g + v, last);
-        w[v] = *reinterpret_cast<const floatx4 *>(pd + ((size_t)(q >> 2) * fq + (q & 3)) * kUnit);
-    }
+    head(0, wa);
+    head(1, wb);
 }
 
 // MFMAs of one down group: column blocks 2g and 2g + 1 of the wave (those
@@ -274,23 +328,39 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
                             const int *routed, int routed_target, int *err) {
     int *list = reinterpret_cast<int *>(xs + kRows * kLd);
     int *tok = list + a.nslots;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // (e, fb and the wave index are uniform: weight addresses keep their
+    // common part in SGPRs, the lane's 16-byte column in lo)
+    e = __builtin_amdgcn_readfirstlane(e);
+    fb = __builtin_amdgcn_readfirstlane(fb);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const unsigned lo = 16u * lane;
     const int j = lane & 15, h = lane >> 4;
     const int f = fb * 64 + wave * 16 + j;
     // Gate rows of this wave's 16 features form unit row nbg; up rows are
     // 32 packed rows (2 unit rows) further.
     const int nbg = 8 * fb + 4 * (wave >> 1) + (wave & 1);
-    const float *pg = a.w + (size_t)e * 2 * a.F * a.d + (size_t)nbg * (a.d / 16) * kUnit + 4 * lane;
-    const float *pu = pg + (size_t)2 * (a.d / 16) * kUnit;
+    const WSrc gs = wsrc(a.w + (size_t)e * 2 * a.F * a.d, (size_t)2 * a.F * a.d, lo);
+    const int og = kUnitBytes * nbg * (a.d / 16);
+    const int ou = og + kUnitBytes * 2 * (a.d / 16);
 
     // Standalone: the slot list first (its loads are not queued behind
     // weight loads), then per chunk the activation rows (DMA), the first two
     // weight groups and a wait for the rows only.  MEGA: the first chunk's
     // weights go out before waiting for the router (routed reaching
     // routed_target), as they depend on nothing it computes.
+    // Down weights (FUSED): wave w's 16-column blocks w*nbw .. of the
+    // expert's W_down, this item's 4 feature units.
+    const int fq = a.F / 16;
+    const int nbw = a.d / 64;                      // 16-column blocks per wave
+    const int last = 4 * nbw - 1;
+    const int ngd = (nbw + 1) / 2;
+    const WSrc ds = wsrc(FUSED ? a.w2 + (size_t)e * a.d * a.F : a.w, (size_t)a.d * a.F, lo);
+    const int od = kUnitBytes * ((wave * nbw) * fq + 4 * fb);
+    const DownHead dh{ds, od, fq, last};
     WGroup<2> wa, wb;
     if (MEGA && routed) {
-        gemv_prime<2>(pg, pu, min(kChunk, a.d) / 16, wa, wb);
+        gemv_prime<2>(gs, og, ou, min(kChunk, a.d) / 16, wa, wb);
         wait_count(routed, routed_target, err);
     }
     const int id0 = (int)threadIdx.x < a.nslots ? load_id<MEGA>(a.ids + threadIdx.x) : -1;
@@ -310,13 +380,19 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             if (MEGA && routed && r0 == 0 && k0 == 0) {
                 WAIT_VMCNT(0);   // primed before the rows
             } else {
-                gemv_prime<2>(pg + 16 * k0, pu + 16 * k0, kc / 16, wa, wb);
+                gemv_prime<2>(gs, og + 64 * k0, ou + 64 * k0, kc / 16, wa, wb);
                 WAIT_VMCNT(4 * Unroll<2>::kU);   // the rows, not the weights behind them
             }
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
             const float *as = xs + j * kLd + 4 * h;
-            if (rows > 16) gemv_loop<2, 2>(pg + 16 * k0, pu + 16 * k0, as, kc / 16, acc, wa, wb);
-            else           gemv_loop<2, 1>(pg + 16 * k0, pu + 16 * k0, as, kc / 16, acc, wa, wb);
+            const int g0 = og + 64 * k0, u0 = ou + 64 * k0;   // (16 floats per K column)
+            if (FUSED && k0 + kc == a.d) {   // last chunk: hand over to the down stream
+                if (rows > 16) gemv_loop<2, 2, true>(gs, g0, u0, as, kc / 16, acc, wa, wb, dh);
+                else           gemv_loop<2, 1, true>(gs, g0, u0, as, kc / 16, acc, wa, wb, dh);
+            } else {
+                if (rows > 16) gemv_loop<2, 2>(gs, g0, u0, as, kc / 16, acc, wa, wb);
+                else           gemv_loop<2, 1>(gs, g0, u0, as, kc / 16, acc, wa, wb);
+            }
         }
         // 16x16 accumulator: lane holds rows 4*(lane/16) + r, column lane%16.
         if (!FUSED) {
@@ -331,19 +407,11 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
                 }
             continue;
         }
-        // Down weights first: they depend on nothing computed here.
-        const int fq = a.F / 16;
-        const int nbw = a.d / 64;                      // 16-column blocks per wave
-        const int last = 4 * nbw - 1;
-        const int ngd = (nbw + 1) / 2;
-        const float *pd = a.w2 + (size_t)e * a.d * a.F +
-                          ((size_t)(wave * nbw) * fq + 4 * fb) * kUnit + 4 * lane;
-        // The gate/up weight registers carry the down stream (the next pass,
-        // if any, primes them again).
+        // The gate/up weight registers carry the down stream, whose first
+        // two groups the last chunk's loop issued (the next pass, if any,
+        // primes them again).
         floatx4 (&da)[8] = reinterpret_cast<floatx4 (&)[8]>(wa);
         floatx4 (&db)[8] = reinterpret_cast<floatx4 (&)[8]>(wb);
-        dload(pd, fq, 0, last, da);
-        dload(pd, fq, 1, last, db);
         // H block [rows][64] in LDS over the x rows (every wave is past them).
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
         __builtin_amdgcn_s_barrier();
@@ -372,17 +440,17 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             for (; g + 4 <= ngd; g += 2) {
                 dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
-                dload(pd, fq, g + 2, last, da);
+                dload(ds, od, fq, g + 2, last, da);
                 __builtin_amdgcn_sched_barrier(0);
                 dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
-                dload(pd, fq, g + 3, last, db);
+                dload(ds, od, fq, g + 3, last, db);
                 __builtin_amdgcn_sched_barrier(0);
             }
             const int left = ngd - g;
             if (left == 3) {
                 dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
-                dload(pd, fq, g + 2, last, da);
+                dload(ds, od, fq, g + 2, last, da);
                 dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
                 dgroup<RB>(da, as, g + 2, nbw, cb0, yoff, a.out, j);
             } else if (left == 2) {

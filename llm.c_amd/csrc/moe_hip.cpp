@@ -463,10 +463,14 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
 
     // Expert products: skinny decode GEMVs (which find their own slots from
     // the expert ids, so routing skips the dispatch) or grouped GEMMs.
-    const bool decode_ok = F % 64 == 0 && n <= (size_t)moe::kDecodeMaxSlots;
+    // (the decode kernels address one expert's gate/up block, 2*F*d floats,
+    // with 32-bit byte offsets)
+    const bool decode_ok = F % 64 == 0 && n <= (size_t)moe::kDecodeMaxSlots &&
+                           sizeof(float) * 2 * (size_t)F * d < ((size_t)1 << 31);
     if (g_path >= 2 && !decode_ok)
         return set_err(MOE_HIP_ERR_UNSUPPORTED,
-                       "decode kernels need ffn_hidden %% 64 == 0 and T*k <= %d", moe::kDecodeMaxSlots);
+                       "decode kernels need ffn_hidden %% 64 == 0, T*k <= %d and "
+                       "8*ffn_hidden*d_model < 2^31", moe::kDecodeMaxSlots);
     const bool use_decode = g_path >= 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
     const size_t fused_bytes = sizeof(float) * (size_t)(F / 64) * n * d;
     const bool fused = use_decode && g_path != 3 && fused_bytes <= moe::kFusedPartialBytes;
