@@ -164,15 +164,25 @@ __device__ inline void wload(const WSrc &s, const int (&ob)[2], int q, int last,
             w[u][b] = ldw(s, ob[b] + kUnitBytes * (CLAMP ? min(q + u, last) : q + u));
 }
 
+// First step of stream group g when the stream of ng whole groups starts at
+// group g0 (0 < g0 < ng, so that the workgroups sharing the memory system
+// are spread over it) and wraps around; g0 = 0: group g itself.
+template <int NB>
+__device__ inline int group_step(int g, int g0, int ng) {
+    const int r = g + g0;
+    return Unroll<NB>::kU * (g0 && r >= ng ? r - ng : r);
+}
+
 // Issues the loads of groups 0 and 1 of a chunk of nq steps, unconditionally
-// (wait counts stay exact); groups the chunk lacks are never used.
+// (wait counts stay exact); groups the chunk lacks are never used.  g0: the
+// rotation gemv_loop is given (nonzero only for chunks of whole groups).
 template <int NB>
 __device__ inline void gemv_prime(const WSrc &s, int o0, int o1, int nq, WGroup<NB> &wa,
-                                  WGroup<NB> &wb) {
-    constexpr int kU = Unroll<NB>::kU;
+                                  WGroup<NB> &wb, int g0 = 0) {
+    const int ng = nq / Unroll<NB>::kU;
     const int ob[2] = {o0, o1};
-    wload<NB>(s, ob, 0, nq - 1, wa);
-    wload<NB>(s, ob, kU, nq - 1, wb);
+    wload<NB>(s, ob, group_step<NB>(0, g0, ng), nq - 1, wa);
+    wload<NB>(s, ob, group_step<NB>(1, g0, ng), nq - 1, wb);
 }
 
 template <int NB, int RB>
@@ -209,58 +219,62 @@ __device__ inline void dload(const WSrc &s, int od, int fq, int g, int last, flo
 struct DownHead {
     WSrc s;
     int od, fq, last;
+    int g0, ng;   // the down stream's ng groups start at group g0 (see group_step)
+    __device__ int rot(int g) const { return g0 && g + g0 >= ng ? g + g0 - ng : g + g0; }
 };
 
-// wa / wb must hold groups 0 / 1 (gemv_prime).
-// HEAD: also issues down groups 0 and 1 into wa and wb (NB = 2 only).
+// wa / wb must hold groups 0 / 1 (gemv_prime, same g0).  g0 != 0 rotates
+// the stream (requires nq = kU * ng).
+// HEAD: also issues the first two down groups into wa and wb (NB = 2 only).
 template <int NB, int RB, bool HEAD = false>
 __device__ inline void gemv_loop(const WSrc &s, int o0, int o1, const float *as, int nq,
                                  floatx4 (&acc)[2][NB], WGroup<NB> &wa, WGroup<NB> &wb,
-                                 const DownHead &dh = DownHead{}) {
+                                 const DownHead &dh = DownHead{}, int g0 = 0) {
     constexpr int kU = Unroll<NB>::kU;
     static_assert(!HEAD || NB == 2, "the down stream reuses the gate/up registers");
     auto head = [&](int g, WGroup<NB> &w) {
         if constexpr (HEAD)
-            dload(dh.s, dh.od, dh.fq, g, dh.last, reinterpret_cast<floatx4 (&)[8]>(w));
+            dload(dh.s, dh.od, dh.fq, dh.rot(g), dh.last, reinterpret_cast<floatx4 (&)[8]>(w));
     };
     const int ob[2] = {o0, o1};
     const int ng = nq / kU;
+    auto qg = [&](int gg) { return group_step<NB>(gg, g0, ng); };
     int g = 0;
     // Steady state with unconditional loads (exact wait counts); groups
     // g + 2 and g + 3 lie inside the chunk, so they go unclamped.
     // (Scheduling barriers keep each group's loads right after the MFMAs
     // that free its registers.)
     for (; g + 4 <= ng; g += 2) {
-        gemv_group<NB, RB>(as, kU * g, wa, acc);
+        gemv_group<NB, RB>(as, qg(g), wa, acc);
         __builtin_amdgcn_sched_barrier(0);
-        wload<NB, false>(s, ob, kU * (g + 2), nq - 1, wa);
+        wload<NB, false>(s, ob, qg(g + 2), nq - 1, wa);
         __builtin_amdgcn_sched_barrier(0);
-        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
+        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
         __builtin_amdgcn_sched_barrier(0);
-        wload<NB, false>(s, ob, kU * (g + 3), nq - 1, wb);
+        wload<NB, false>(s, ob, qg(g + 3), nq - 1, wb);
         __builtin_amdgcn_sched_barrier(0);
     }
     const int left = ng - g;   // 0 .. 3 groups, the first two already loaded
     if (left == 3) {
-        gemv_group<NB, RB>(as, kU * g, wa, acc);
-        wload<NB>(s, ob, kU * (g + 2), nq - 1, wa);
-        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
-        gemv_group<NB, RB>(as, kU * (g + 2), wa, acc);
+        gemv_group<NB, RB>(as, qg(g), wa, acc);
+        wload<NB>(s, ob, qg(g + 2), nq - 1, wa);
+        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
+        gemv_group<NB, RB>(as, qg(g + 2), wa, acc);
     } else if (left == 2 && nq == kU * ng) {
         // (the common case: each down group goes out as its registers free)
-        gemv_group<NB, RB>(as, kU * g, wa, acc);
+        gemv_group<NB, RB>(as, qg(g), wa, acc);
         __builtin_amdgcn_sched_barrier(0);
         head(0, wa);
         __builtin_amdgcn_sched_barrier(0);
-        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
+        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
         __builtin_amdgcn_sched_barrier(0);
         head(1, wb);
         return;
     } else if (left == 2) {
-        gemv_group<NB, RB>(as, kU * g, wa, acc);
-        gemv_group<NB, RB>(as, kU * (g + 1), wb, acc);
+        gemv_group<NB, RB>(as, qg(g), wa, acc);
+        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
     } else if (left == 1) {
-        gemv_group<NB, RB>(as, kU * g, wa, acc);
+        gemv_group<NB, RB>(as, qg(g), wa, acc);
     }
     for (int q = kU * ng; q < nq; ++q) {
         floatx4 w[NB];
@@ -357,10 +371,17 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
     const int ngd = (nbw + 1) / 2;
     const WSrc ds = wsrc(FUSED ? a.w2 + (size_t)e * a.d * a.F : a.w, (size_t)a.d * a.F, lo);
     const int od = kUnitBytes * ((wave * nbw) * fq + 4 * fb);
-    const DownHead dh{ds, od, fq, last};
+    // Each wave starts its streams at its own group (gate/up: chunks of whole
+    // groups only), spreading the concurrent reads over the memory system.
+    const int spread = 4 * (e * (a.F / 64) + fb) + wave;
+    auto rot_of = [&](int nq) {   // rotation of a gate/up chunk of nq steps
+        const int ng = nq / Unroll<2>::kU;
+        return nq % Unroll<2>::kU == 0 && ng >= 2 ? (5 * spread) % ng : 0;
+    };
+    const DownHead dh{ds, od, fq, last, ngd >= 2 ? (3 * spread) % ngd : 0, ngd};
     WGroup<2> wa, wb;
     if (MEGA && routed) {
-        gemv_prime<2>(gs, og, ou, min(kChunk, a.d) / 16, wa, wb);
+        gemv_prime<2>(gs, og, ou, min(kChunk, a.d) / 16, wa, wb, rot_of(min(kChunk, a.d) / 16));
         wait_count(routed, routed_target, err);
     }
     const int id0 = (int)threadIdx.x < a.nslots ? load_id<MEGA>(a.ids + threadIdx.x) : -1;
@@ -380,18 +401,19 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             if (MEGA && routed && r0 == 0 && k0 == 0) {
                 WAIT_VMCNT(0);   // primed before the rows
             } else {
-                gemv_prime<2>(gs, og + 64 * k0, ou + 64 * k0, kc / 16, wa, wb);
+                gemv_prime<2>(gs, og + 64 * k0, ou + 64 * k0, kc / 16, wa, wb, rot_of(kc / 16));
                 WAIT_VMCNT(4 * Unroll<2>::kU);   // the rows, not the weights behind them
             }
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
             const float *as = xs + j * kLd + 4 * h;
-            const int g0 = og + 64 * k0, u0 = ou + 64 * k0;   // (16 floats per K column)
+            const int go = og + 64 * k0, uo = ou + 64 * k0;   // (16 floats per K column)
+            const int g0 = rot_of(kc / 16);
             if (FUSED && k0 + kc == a.d) {   // last chunk: hand over to the down stream
-                if (rows > 16) gemv_loop<2, 2, true>(gs, g0, u0, as, kc / 16, acc, wa, wb, dh);
-                else           gemv_loop<2, 1, true>(gs, g0, u0, as, kc / 16, acc, wa, wb, dh);
+                if (rows > 16) gemv_loop<2, 2, true>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                else           gemv_loop<2, 1, true>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
             } else {
-                if (rows > 16) gemv_loop<2, 2>(gs, g0, u0, as, kc / 16, acc, wa, wb);
-                else           gemv_loop<2, 1>(gs, g0, u0, as, kc / 16, acc, wa, wb);
+                if (rows > 16) gemv_loop<2, 2>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                else           gemv_loop<2, 1>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
             }
         }
         // 16x16 accumulator: lane holds rows 4*(lane/16) + r, column lane%16.
@@ -438,26 +460,26 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             constexpr int RB = decltype(rb)::value;
             int g = 0;
             for (; g + 4 <= ngd; g += 2) {
-                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
-                dload(ds, od, fq, g + 2, last, da);
+                dload(ds, od, fq, dh.rot(g + 2), last, da);
                 __builtin_amdgcn_sched_barrier(0);
-                dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
-                dload(ds, od, fq, g + 3, last, db);
+                dload(ds, od, fq, dh.rot(g + 3), last, db);
                 __builtin_amdgcn_sched_barrier(0);
             }
             const int left = ngd - g;
             if (left == 3) {
-                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
-                dload(ds, od, fq, g + 2, last, da);
-                dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
-                dgroup<RB>(da, as, g + 2, nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dload(ds, od, fq, dh.rot(g + 2), last, da);
+                dgroup<RB>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(da, as, dh.rot(g + 2), nbw, cb0, yoff, a.out, j);
             } else if (left == 2) {
-                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
-                dgroup<RB>(db, as, g + 1, nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
             } else if (left == 1) {
-                dgroup<RB>(da, as, g, nbw, cb0, yoff, a.out, j);
+                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
             }
         };
         if (rows > 16) run(std::integral_constant<int, 2>{});
