@@ -262,41 +262,55 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 // The same for many split-K partials (the fused decode kernel writes one per
 // 64 features): G lanes share an output float4, each summing up to 8
 // consecutive partials of a slot in split order; lane 0 adds the G group
-// sums in a fixed tree order and applies the slot's gate weight.
-template <int G>
+// sums in a fixed tree order and applies the slot's gate weight.  KS > 0:
+// k = KS at compile time, and every load of the lane (partials, gate
+// weights, the accumulated output) is issued before the first sum.
+template <int G, int KS>
 __global__ __launch_bounds__(256) void combine_groups_kernel(CombineArgs a) {
+    constexpr int KB = KS > 0 ? KS : 1;   // slots whose loads go out together
     const int d4 = a.d >> 2;
     const size_t gid = ((size_t)blockIdx.x * 256 + threadIdx.x) / G;
     const int g = threadIdx.x % G;
     const bool valid = gid < (size_t)a.T * d4;
     const int t = valid ? (int)(gid / d4) : 0, c4 = valid ? (int)(gid % d4) : 0;
     const int s0 = 8 * g, s1 = min(s0 + 8, a.ksplit);
+    const int k = KS > 0 ? KS : a.k;
+    floatx4 *o = reinterpret_cast<floatx4 *>(a.out + (size_t)t * a.d + 4 * c4);
+    floatx4 prev = {0.f, 0.f, 0.f, 0.f};
+    if (KS > 0 && a.accumulate && g == 0) prev = *o;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int ki = 0; ki < a.k; ++ki) {
-        const float *yp = a.ys + ((size_t)t * a.k + ki) * a.d + 4 * c4;
-        floatx4 p[8];
+    for (int k0 = 0; k0 < k; k0 += KB) {
+        floatx4 p[KB][8];
+        float w[KB];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            p[u] = *reinterpret_cast<const floatx4 *>(yp + (size_t)min(s0 + u, a.ksplit - 1) * a.split_stride);
-        floatx4 y = {0.f, 0.f, 0.f, 0.f};
-        if (s0 < s1) y = p[0];
+        for (int kb = 0; kb < KB; ++kb) {
+            const float *yp = a.ys + ((size_t)t * a.k + k0 + kb) * a.d + 4 * c4;
 #pragma unroll
-        for (int u = 1; u < 8; ++u)
-            if (s0 + u < s1)
+            for (int u = 0; u < 8; ++u)
+                p[kb][u] = *reinterpret_cast<const floatx4 *>(
+                    yp + (size_t)min(s0 + u, a.ksplit - 1) * a.split_stride);
+            w[kb] = a.gw[(size_t)t * a.k + k0 + kb];
+        }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) y[j] = y[j] + p[u][j];
+        for (int kb = 0; kb < KB; ++kb) {
+            floatx4 y = {0.f, 0.f, 0.f, 0.f};
+            if (s0 < s1) y = p[kb][0];
 #pragma unroll
-        for (int m = G / 2; m >= 1; m >>= 1)
+            for (int u = 1; u < 8; ++u)
+                if (s0 + u < s1)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) y[j] = y[j] + __shfl_xor(y[j], m, G);
-        const float w = a.gw[(size_t)t * a.k + ki];
+                    for (int j = 0; j < 4; ++j) y[j] = y[j] + p[kb][u][j];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] = fmaf(w, y[j], acc[j]);
+            for (int m = G / 2; m >= 1; m >>= 1)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) y[j] = y[j] + __shfl_xor(y[j], m, G);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = fmaf(w[kb], y[j], acc[j]);
+        }
     }
     if (valid && g == 0) {
-        floatx4 *o = reinterpret_cast<floatx4 *>(a.out + (size_t)t * a.d + 4 * c4);
         if (a.accumulate) {
-            floatx4 v = *o;
+            floatx4 v = KS > 0 ? prev : *o;
 #pragma unroll
             for (int j = 0; j < 4; ++j) v[j] = v[j] + acc[j];
             *o = v;
@@ -364,10 +378,16 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
         auto go = [&](auto kern, int G) {
             hipLaunchKernelGGL(kern, dim3((unsigned)((n * G + 255) / 256)), dim3(256), 0, s, a);
         };
-        if (groups <= 2)       go(combine_groups_kernel<2>, 2);
-        else if (groups <= 4)  go(combine_groups_kernel<4>, 4);
-        else if (groups <= 8)  go(combine_groups_kernel<8>, 8);
-        else if (groups <= 16) go(combine_groups_kernel<16>, 16);
+        auto by_k = [&](auto gc) {
+            constexpr int G = decltype(gc)::value;
+            if (a.k == 1)      go(combine_groups_kernel<G, 1>, G);
+            else if (a.k == 2) go(combine_groups_kernel<G, 2>, G);
+            else               go(combine_groups_kernel<G, 0>, G);
+        };
+        if (groups <= 2)       by_k(std::integral_constant<int, 2>{});
+        else if (groups <= 4)  by_k(std::integral_constant<int, 4>{});
+        else if (groups <= 8)  by_k(std::integral_constant<int, 8>{});
+        else if (groups <= 16) by_k(std::integral_constant<int, 16>{});
         else return hipErrorInvalidValue;
         return hipGetLastError();
     }
