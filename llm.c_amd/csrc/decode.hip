@@ -23,13 +23,15 @@
 namespace moe {
 namespace {
 
-// grid = E x (F/64): one gate/up item per workgroup.
-template <bool FUSED>
-__global__ __launch_bounds__(256, 2) void decode_gateup_kernel(DecodeArgs a) {
+// grid = E x (F/(16*NW)): one gate/up item of NW waves per workgroup (NW =
+// 8: one workgroup per CU, two waves per SIMD).
+template <bool FUSED, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void decode_gateup_kernel(DecodeArgs a) {
     extern __shared__ __align__(16) float xs[];     // [kRows][kLd], slot list, token list
-    __shared__ int wcnt[4];
-    const int nfb = a.F / 64;
-    gateup_item<FUSED, false>(a, blockIdx.x / nfb, blockIdx.x % nfb, xs, wcnt, nullptr, 0, nullptr);
+    __shared__ int wcnt[NW];
+    const int nfb = a.F / (16 * NW);
+    gateup_item<FUSED, false, NW>(a, blockIdx.x / nfb, blockIdx.x % nfb, xs, wcnt, nullptr, 0,
+                                  nullptr);
 }
 
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
@@ -65,6 +67,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
             gemv_prime<1>(ws, ow + 64 * k0, 0, kc / 16, wa, wb);
             WAIT_VMCNT(2 * Unroll<1>::kU);   // the rows, not the weights behind them
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
+            dma_landed(hs);
             const float *as = hs + j * kLd + 4 * h;
             if (rows > 16) gemv_loop<1, 2>(ws, ow + 64 * k0, 0, as, kc / 16, acc, wa, wb);
             else           gemv_loop<1, 1>(ws, ow + 64 * k0, 0, as, kc / 16, acc, wa, wb);
@@ -107,20 +110,29 @@ size_t decode_lds(const DecodeArgs &a) {
     return (size_t)kRows * kLd * sizeof(float) + 2 * sizeof(int) * (size_t)a.nslots;
 }
 
+int decode_fused_waves(int d, int F) { return d % 128 == 0 && F % 128 == 0 ? 8 : 4; }
+
 hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s) {
     const size_t lds = decode_lds(a);
-    static bool attr = false, attr_f = false;
-    dim3 grid((unsigned)(a.E * (a.F / 64)));
-    if (a.w2) {
-        hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_gateup_kernel<true>),
-                               kDecodeMaxLds, &attr_f);
+    static bool attr = false, attr_f4 = false, attr_f8 = false;
+    if (a.w2 && decode_fused_waves(a.d, a.F) == 8) {
+        hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_gateup_kernel<true, 8>),
+                               kDecodeMaxLds, &attr_f8);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(decode_gateup_kernel<true>, grid, dim3(256), lds, s, a);
+        hipLaunchKernelGGL((decode_gateup_kernel<true, 8>), dim3((unsigned)(a.E * (a.F / 128))),
+                           dim3(512), lds, s, a);
+    } else if (a.w2) {
+        hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_gateup_kernel<true, 4>),
+                               kDecodeMaxLds, &attr_f4);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((decode_gateup_kernel<true, 4>), dim3((unsigned)(a.E * (a.F / 64))),
+                           dim3(256), lds, s, a);
     } else {
-        hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_gateup_kernel<false>),
+        hipError_t e = set_lds(reinterpret_cast<const void *>(&decode_gateup_kernel<false, 4>),
                                kDecodeMaxLds, &attr);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(decode_gateup_kernel<false>, grid, dim3(256), lds, s, a);
+        hipLaunchKernelGGL((decode_gateup_kernel<false, 4>), dim3((unsigned)(a.E * (a.F / 64))),
+                           dim3(256), lds, s, a);
     }
     return hipGetLastError();
 }

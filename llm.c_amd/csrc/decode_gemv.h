@@ -23,18 +23,18 @@ constexpr int kChunk = 512;      // K elements staged per LDS fill
 constexpr int kLd = kChunk + 4;  // padded LDS row
 
 constexpr int kUnit = 256;      // floats per 16 x 16 unit = one K step of 16
-constexpr int kHLd = 64 + 4;    // padded LDS row of the fused kernel's H block
 
 __device__ inline floatx4 mfma16(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
 // Ascending list of the assignments a < n with ids[a] == e, built by the
-// workgroup's four waves with ballots, and (tok != nullptr) the token a / topk
+// workgroup's NW waves with ballots, and (tok != nullptr) the token a / topk
 // of each; returns the list length.  Every thread calls this, with id0 =
 // ids[threadIdx.x] (or -1 past n) loaded by the caller before its first
-// weight loads so that waiting for it does not wait for them; wcnt is 4 ints
-// of LDS.
+// weight loads so that waiting for it does not wait for them; wcnt is NW
+// ints of LDS.
+template <int NW>
 __device__ inline void slot_chunk(int i, int n, int e, int id, int topk, int *list, int *tok,
                                   int *wcnt, int &total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -50,7 +50,8 @@ __device__ inline void slot_chunk(int i, int n, int e, int id, int topk, int *li
         list[at] = i;
         if (tok) tok[at] = i / topk;
     }
-    total += wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) total += wcnt[w];
     __syncthreads();
 }
 
@@ -62,14 +63,15 @@ __device__ inline int load_id(const int *p) {
     return *p;
 }
 
-template <bool COHERENT>
+template <bool COHERENT, int NW = 4>
 __device__ int expert_slots(const int *ids, int n, int e, int id0, int topk, int *list, int *tok,
                             int *wcnt) {
     int total = 0;
-    slot_chunk(threadIdx.x, n, e, id0, topk, list, tok, wcnt, total);
-    for (int base = 256; base < n; base += 256) {
+    slot_chunk<NW>(threadIdx.x, n, e, id0, topk, list, tok, wcnt, total);
+    for (int base = 64 * NW; base < n; base += 64 * NW) {
         const int i = base + threadIdx.x;
-        slot_chunk(i, n, e, load_id<COHERENT>(ids + min(i, n - 1)), topk, list, tok, wcnt, total);
+        slot_chunk<NW>(i, n, e, load_id<COHERENT>(ids + min(i, n - 1)), topk, list, tok, wcnt,
+                       total);
     }
     return total;
 }
@@ -95,14 +97,15 @@ __device__ inline void wait_count(const int *ctr, int target, int *err) {
 }
 
 // Staging of rows rowlist[pos0 .. pos0 + rows) of src, columns [k0, k0 + kc),
-// into LDS rows of stride kLd by global-to-LDS DMA (no registers): wave w
-// copies rows w, w + 4, ... as two 1 KB pieces each (64 lanes x 16 bytes),
-// columns clamped to the source row.  Columns past kc and rows past rows are
-// never read.
+// into LDS rows of stride kLd by global-to-LDS DMA (no registers): wave w of
+// NW copies rows w, w + NW, ... as two 1 KB pieces each (64 lanes x 16
+// bytes), columns clamped to the source row.  Columns past kc and rows past
+// rows are never read.
+template <int NW = 4>
 __device__ inline void stage_lds(float *xs, const float *src, int ld, const int *rowlist,
                                  int pos0, int rows, int k0, int kc) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int r = wave; r < rows; r += 4) {
+    for (int r = wave; r < rows; r += NW) {
         const float *srow = src + (size_t)rowlist[pos0 + r] * ld;
 #pragma unroll
         for (int p = 0; p < kChunk / 256; ++p)
@@ -115,6 +118,16 @@ __device__ inline void stage_lds(float *xs, const float *src, int ld, const int 
 // s_waitcnt with only the vector-memory count limited (expcnt and lgkmcnt at
 // their maxima).
 #define WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | 0x0F70)
+
+// After the rows staged by DMA are known to have landed (an explicit wait):
+// one read of them, so that the compiler's own wait tracking also counts the
+// DMA as complete.  Otherwise it assumes the DMA may still be writing LDS
+// and waits for every outstanding load before each later LDS read, which
+// drains the weight stream in every loop iteration.
+__device__ inline void dma_landed(const float *xs) {
+    const float v = xs[threadIdx.x & 63];
+    asm volatile("" ::"v"(v));
+}
 
 // Streams NB weight rows (NB = 2: gate and up of the lane's feature, NB = 1:
 // one down row) over nq 16-wide K steps against RB 16-row activation blocks
@@ -203,19 +216,22 @@ __device__ inline void gemv_group(const float *as, int q, const WGroup<NB> &w,
     }
 }
 
-// Down-projection units of the fused kernel: 8 units (two 16-column blocks
-// of 4 feature units each) per group, clamped to the wave's last unit.
+// Down-projection units of the fused kernel: 8 units per group (8 / NW
+// 16-column blocks of NW feature units each), clamped to the wave's last
+// unit.
+template <int NW>
 __device__ inline void dload(const WSrc &s, int od, int fq, int g, int last, floatx4 (&w)[8]) {
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
         const int q = min(8 * g + v, last);
-        w[v] = ldw(s, od + kUnitBytes * ((q >> 2) * fq + (q & 3)));
+        w[v] = ldw(s, od + kUnitBytes * ((q / NW) * fq + q % NW));
     }
 }
 
 // Where the fused kernel's down stream starts: its first two groups go out
 // from the tail of the last gate/up chunk (into the registers that chunk
 // frees), so the weight stream does not drain between the two products.
+template <int NW>
 struct DownHead {
     WSrc s;
     int od, fq, last;
@@ -226,15 +242,15 @@ struct DownHead {
 // wa / wb must hold groups 0 / 1 (gemv_prime, same g0).  g0 != 0 rotates
 // the stream (requires nq = kU * ng).
 // HEAD: also issues the first two down groups into wa and wb (NB = 2 only).
-template <int NB, int RB, bool HEAD = false>
+template <int NB, int RB, bool HEAD = false, int NW = 4>
 __device__ inline void gemv_loop(const WSrc &s, int o0, int o1, const float *as, int nq,
                                  floatx4 (&acc)[2][NB], WGroup<NB> &wa, WGroup<NB> &wb,
-                                 const DownHead &dh = DownHead{}, int g0 = 0) {
+                                 const DownHead<NW> &dh = DownHead<NW>{}, int g0 = 0) {
     constexpr int kU = Unroll<NB>::kU;
     static_assert(!HEAD || NB == 2, "the down stream reuses the gate/up registers");
     auto head = [&](int g, WGroup<NB> &w) {
         if constexpr (HEAD)
-            dload(dh.s, dh.od, dh.fq, dh.rot(g), dh.last, reinterpret_cast<floatx4 (&)[8]>(w));
+            dload<NW>(dh.s, dh.od, dh.fq, dh.rot(g), dh.last, reinterpret_cast<floatx4 (&)[8]>(w));
     };
     const int ob[2] = {o0, o1};
     const int ng = nq / kU;
@@ -295,30 +311,34 @@ __device__ inline void gemv_loop(const WSrc &s, int o0, int o1, const float *as,
     head(1, wb);
 }
 
-// MFMAs of one down group: column blocks 2g and 2g + 1 of the wave (those
-// below nbw), K = the block's 64 features (A operands from the H block in
-// LDS at as), each block written at yoff + its column once complete
-// (yoff < 0: a row past the pass).
-template <int RB>
+// Padded LDS row of the fused kernel's H block (16 * NW features).
+template <int NW> constexpr int hld() { return 16 * NW + 4; }
+
+// MFMAs of one down group: column blocks CB*g .. CB*g + CB - 1 of the wave
+// (CB = 8 / NW; those below nbw), K = the block's 16 * NW features (A
+// operands from the H block in LDS at as), each block written at yoff + its
+// column once complete (yoff < 0: a row past the pass).
+template <int RB, int NW>
 __device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int nbw, int cb0,
                               const int (&yoff)[2][4], float *yp, int j) {
-    floatx4 ha[2][4];
+    constexpr int CB = 8 / NW;
+    floatx4 ha[2][NW];
 #pragma unroll
     for (int b = 0; b < RB; ++b)
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            ha[b][u] = *reinterpret_cast<const floatx4 *>(as + b * 16 * kHLd + 16 * u);
+        for (int u = 0; u < NW; ++u)
+            ha[b][u] = *reinterpret_cast<const floatx4 *>(as + b * 16 * hld<NW>() + 16 * u);
 #pragma unroll
-    for (int bi = 0; bi < 2; ++bi) {
+    for (int bi = 0; bi < CB; ++bi) {
         floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < NW; ++u)
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                acc[0] = mfma16(ha[0][u][s], w[4 * bi + u][s], acc[0]);
-                if (RB == 2) acc[1] = mfma16(ha[1][u][s], w[4 * bi + u][s], acc[1]);
+                acc[0] = mfma16(ha[0][u][s], w[NW * bi + u][s], acc[0]);
+                if (RB == 2) acc[1] = mfma16(ha[1][u][s], w[NW * bi + u][s], acc[1]);
             }
-        const int cb = 2 * g + bi;
+        const int cb = CB * g + bi;
         if (cb < nbw) {
             const int col = 16 * (cb0 + cb) + j;
 #pragma unroll
@@ -330,16 +350,18 @@ __device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int
     }
 }
 
-// One gate/up item: expert e, features 64*fb .. 64*fb + 63.  FUSED = false:
-// writes H [n x F] by assignment.  FUSED = true: keeps the 64 H columns in
-// LDS and multiplies them by the matching 64 rows of W_down, writing the
-// split-K partial Yp[fb][a][0 .. d) (the combine adds the F/64 partials in
-// order).  xs: the dynamic LDS (rows, slot list, token list); wcnt: 4 ints
-// of LDS.  MEGA: expert ids come from the same launch (device-scope loads)
-// and, when routed is set, the item first waits for the router.
-template <bool FUSED, bool MEGA>
+// One gate/up item of NW waves: expert e, features 16*NW*fb .. + 16*NW - 1
+// (16 per wave).  FUSED = false: writes H [n x F] by assignment.  FUSED =
+// true: keeps the item's H columns in LDS and multiplies them by the matching
+// rows of W_down, writing the split-K partial Yp[fb][a][0 .. d) (the combine
+// adds the F/(16*NW) partials in order).  xs: the dynamic LDS (rows, slot
+// list, token list); wcnt: NW ints of LDS.  MEGA: expert ids come from the
+// same launch (device-scope loads) and, when routed is set, the item first
+// waits for the router.
+template <bool FUSED, bool MEGA, int NW = 4>
 __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *wcnt,
                             const int *routed, int routed_target, int *err) {
+    static_assert(NW == 4 || NW == 8, "an item is 4 or 8 waves of 16 features");
     int *list = reinterpret_cast<int *>(xs + kRows * kLd);
     int *tok = list + a.nslots;
     // (e, fb and the wave index are uniform: weight addresses keep their
@@ -350,10 +372,11 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const unsigned lo = 16u * lane;
     const int j = lane & 15, h = lane >> 4;
-    const int f = fb * 64 + wave * 16 + j;
-    // Gate rows of this wave's 16 features form unit row nbg; up rows are
-    // 32 packed rows (2 unit rows) further.
-    const int nbg = 8 * fb + 4 * (wave >> 1) + (wave & 1);
+    const int m = NW * fb + wave;                 // this wave's 16-feature block
+    const int f = 16 * m + j;
+    // Gate rows of feature block m form unit row nbg (packed rows interleave
+    // 32 gate and 32 up rows); up rows are 2 unit rows further.
+    const int nbg = 4 * (m >> 1) + (m & 1);
     const WSrc gs = wsrc(a.w + (size_t)e * 2 * a.F * a.d, (size_t)2 * a.F * a.d, lo);
     const int og = kUnitBytes * nbg * (a.d / 16);
     const int ou = og + kUnitBytes * 2 * (a.d / 16);
@@ -364,28 +387,28 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
     // weights go out before waiting for the router (routed reaching
     // routed_target), as they depend on nothing it computes.
     // Down weights (FUSED): wave w's 16-column blocks w*nbw .. of the
-    // expert's W_down, this item's 4 feature units.
+    // expert's W_down, this item's NW feature units.
     const int fq = a.F / 16;
-    const int nbw = a.d / 64;                      // 16-column blocks per wave
-    const int last = 4 * nbw - 1;
-    const int ngd = (nbw + 1) / 2;
+    const int nbw = a.d / (16 * NW);               // 16-column blocks per wave
+    const int last = NW * nbw - 1;
+    const int ngd = (NW * nbw + 7) / 8;
     const WSrc ds = wsrc(FUSED ? a.w2 + (size_t)e * a.d * a.F : a.w, (size_t)a.d * a.F, lo);
-    const int od = kUnitBytes * ((wave * nbw) * fq + 4 * fb);
+    const int od = kUnitBytes * ((wave * nbw) * fq + NW * fb);
     // Each wave starts its streams at its own group (gate/up: chunks of whole
     // groups only), spreading the concurrent reads over the memory system.
-    const int spread = 4 * (e * (a.F / 64) + fb) + wave;
+    const int spread = NW * (e * (a.F / (16 * NW)) + fb) + wave;
     auto rot_of = [&](int nq) {   // rotation of a gate/up chunk of nq steps
         const int ng = nq / Unroll<2>::kU;
         return nq % Unroll<2>::kU == 0 && ng >= 2 ? (5 * spread) % ng : 0;
     };
-    const DownHead dh{ds, od, fq, last, ngd >= 2 ? (3 * spread) % ngd : 0, ngd};
+    const DownHead<NW> dh{ds, od, fq, last, ngd >= 2 ? (3 * spread) % ngd : 0, ngd};
     WGroup<2> wa, wb;
     if (MEGA && routed) {
         gemv_prime<2>(gs, og, ou, min(kChunk, a.d) / 16, wa, wb, rot_of(min(kChunk, a.d) / 16));
         wait_count(routed, routed_target, err);
     }
     const int id0 = (int)threadIdx.x < a.nslots ? load_id<MEGA>(a.ids + threadIdx.x) : -1;
-    const int cnt = expert_slots<MEGA>(a.ids, a.nslots, e, id0, a.topk, list, tok, wcnt);
+    const int cnt = expert_slots<MEGA, NW>(a.ids, a.nslots, e, id0, a.topk, list, tok, wcnt);
     if (cnt == 0) return;
     for (int r0 = 0; r0 < cnt; r0 += kRows) {
         const int rows = min(kRows, cnt - r0);
@@ -397,7 +420,7 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
         for (int k0 = 0; k0 < a.d; k0 += kChunk) {
             const int kc = min(kChunk, a.d - k0);
             __syncthreads();   // every wave is done with the previous rows
-            stage_lds(xs, a.x, a.d, tok, r0, rows, k0, kc);
+            stage_lds<NW>(xs, a.x, a.d, tok, r0, rows, k0, kc);
             if (MEGA && routed && r0 == 0 && k0 == 0) {
                 WAIT_VMCNT(0);   // primed before the rows
             } else {
@@ -405,15 +428,20 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
                 WAIT_VMCNT(4 * Unroll<2>::kU);   // the rows, not the weights behind them
             }
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
+            dma_landed(xs);
             const float *as = xs + j * kLd + 4 * h;
             const int go = og + 64 * k0, uo = ou + 64 * k0;   // (16 floats per K column)
             const int g0 = rot_of(kc / 16);
             if (FUSED && k0 + kc == a.d) {   // last chunk: hand over to the down stream
-                if (rows > 16) gemv_loop<2, 2, true>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
-                else           gemv_loop<2, 1, true>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                if (rows > 16)
+                    gemv_loop<2, 2, true, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                else
+                    gemv_loop<2, 1, true, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
             } else {
-                if (rows > 16) gemv_loop<2, 2>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
-                else           gemv_loop<2, 1>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                if (rows > 16)
+                    gemv_loop<2, 2, false, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                else
+                    gemv_loop<2, 1, false, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
             }
         }
         // 16x16 accumulator: lane holds rows 4*(lane/16) + r, column lane%16.
@@ -434,7 +462,8 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
         // primes them again).
         floatx4 (&da)[8] = reinterpret_cast<floatx4 (&)[8]>(wa);
         floatx4 (&db)[8] = reinterpret_cast<floatx4 (&)[8]>(wb);
-        // H block [rows][64] in LDS over the x rows (every wave is past them).
+        // H block [rows][16 * NW] in LDS over the x rows (every wave is past
+        // them).
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
         __builtin_amdgcn_s_barrier();
         float *hs = xs;
@@ -442,10 +471,11 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                hs[(b * 16 + 4 * h + r) * kHLd + wave * 16 + j] = swiglu_fast(acc[b][0][r], acc[b][1][r]);
+                hs[(b * 16 + 4 * h + r) * hld<NW>() + wave * 16 + j] =
+                    swiglu_fast(acc[b][0][r], acc[b][1][r]);
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_s_barrier();
-        const float *as = hs + j * kHLd + 4 * h;
+        const float *as = hs + j * hld<NW>() + 4 * h;
         // Partial offsets fit in 32 bits: the host caps the partial buffer.
         int yoff[2][4];
 #pragma unroll
@@ -460,26 +490,26 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             constexpr int RB = decltype(rb)::value;
             int g = 0;
             for (; g + 4 <= ngd; g += 2) {
-                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
-                dload(ds, od, fq, dh.rot(g + 2), last, da);
+                dload<NW>(ds, od, fq, dh.rot(g + 2), last, da);
                 __builtin_amdgcn_sched_barrier(0);
-                dgroup<RB>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
-                dload(ds, od, fq, dh.rot(g + 3), last, db);
+                dload<NW>(ds, od, fq, dh.rot(g + 3), last, db);
                 __builtin_amdgcn_sched_barrier(0);
             }
             const int left = ngd - g;
             if (left == 3) {
-                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
-                dload(ds, od, fq, dh.rot(g + 2), last, da);
-                dgroup<RB>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
-                dgroup<RB>(da, as, dh.rot(g + 2), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dload<NW>(ds, od, fq, dh.rot(g + 2), last, da);
+                dgroup<RB, NW>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW>(da, as, dh.rot(g + 2), nbw, cb0, yoff, a.out, j);
             } else if (left == 2) {
-                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
-                dgroup<RB>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
             } else if (left == 1) {
-                dgroup<RB>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
             }
         };
         if (rows > 16) run(std::integral_constant<int, 2>{});

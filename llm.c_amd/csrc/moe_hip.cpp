@@ -472,13 +472,14 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
                        "decode kernels need ffn_hidden %% 64 == 0, T*k <= %d and "
                        "8*ffn_hidden*d_model < 2^31", moe::kDecodeMaxSlots);
     const bool use_decode = g_path >= 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
-    const size_t fused_bytes = sizeof(float) * (size_t)(F / 64) * n * d;
+    // Mode 2 runs routing and the fused expert items (4 waves) as one launch
+    // where it fits; everything else routes first (the one-launch layer is
+    // not yet faster: its router competes with the expert weight stream).
+    const bool one_launch_ok = g_path == 2 && g_rpath != 1 && moe::decode_layer_supported(d, E);
+    const int fused_splits = F / (16 * (one_launch_ok ? 4 : moe::decode_fused_waves(d, F)));
+    const size_t fused_bytes = sizeof(float) * (size_t)fused_splits * n * d;
     const bool fused = use_decode && g_path != 3 && fused_bytes <= moe::kFusedPartialBytes;
-    // Mode 2 runs routing and the fused expert items as one launch where it
-    // fits; everything else routes first (the one-launch layer is not yet
-    // faster: its router competes with the expert weight stream).
-    const bool one_launch = fused && g_path == 2 && g_rpath != 1 &&
-                            moe::decode_layer_supported(d, E);
+    const bool one_launch = fused && one_launch_ok;
     if (!one_launch)
         TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm,
                        s, !use_decode));
@@ -491,7 +492,7 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
         gu.d = d; gu.F = F; gu.E = E; gu.ksplit = 1; gu.nslots = (int)n;
         if (one_launch) {
             TRY(ensure_counters());
-            ksplit = F / 64;
+            ksplit = fused_splits;
             TRY(g_ws.ys.reserve(fused_bytes));
             gu.out = g_ws.ys.as<float>();
             gu.w2 = L->wdT;
@@ -508,7 +509,7 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
             if (g_timing)
                 for (int i = 1; i <= 4; ++i) HIP_TRY(hipEventRecord(g_ev[i], s));
         } else if (fused) {
-            ksplit = F / 64;
+            ksplit = fused_splits;
             TRY(g_ws.ys.reserve(fused_bytes));
             gu.out = g_ws.ys.as<float>();
             gu.w2 = L->wdT;

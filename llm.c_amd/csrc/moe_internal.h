@@ -92,8 +92,8 @@ struct DecodeArgs {
 
 // Most assignments (T * k) the decode kernels take (LDS slot list).
 constexpr int kDecodeMaxSlots = 4096;
-// Largest split-K partial buffer ([F/64][T*k][d] floats) the fused decode
-// kernel may write; larger layers use the separate down kernel.
+// Largest split-K partial buffer ([F/(16*waves)][T*k][d] floats) the fused
+// decode kernel may write; larger layers use the separate down kernel.
 constexpr size_t kFusedPartialBytes = (size_t)32 << 20;
 
 // One launch per decode layer: routing plus fused gate/up + split-K down
@@ -114,6 +114,9 @@ hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s);
+// Waves per item of the fused decode kernel (8 when d and F allow, else 4);
+// its split-K partials number F / (16 * waves).
+int decode_fused_waves(int d, int F);
 // Number of reduction splits the decode down-projection uses.
 int decode_ksplit(int d, int F, int E);
 
