@@ -123,6 +123,19 @@ void moe_decode_step(const MoEWeights *w, const ModelConfig *cfg,
 int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg,
                      const float *x_norm, int n_rows, float *x);
 
+/* The FFN half of block_forward for a MoE block (src/transformer.c:760-767):
+ * cache->x_norm_ffn = rms_norm(x; rms_ffn, cfg->rms_norm_eps) (src/matrix.c:
+ * 666-711), cache->ffn_out = moe_forward(x_norm_ffn) with router_probs and
+ * expert_ids, then x += ffn_out.  The normalisation runs on the GPU with the
+ * layer; cache->x_norm_ffn and ffn_out must be T x d views.  Aborts on error.
+ * The reference build evaluates 1/sqrt with the x86 RSQRTSS estimate and a
+ * Newton step; here it is correctly rounded, so x_norm_ffn agrees with the
+ * reference's to a few ulp (every later step is the reference's recipe). */
+void moe_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w, const ModelConfig *cfg,
+                   ForwardCache *cache);
+int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,
+                      const ModelConfig *cfg, ForwardCache *cache);
+
 /* ---------------------------------------------------------------------------
  * Library state and residency
  * ------------------------------------------------------------------------- */
@@ -170,6 +183,21 @@ int moe_hip_layer_get_router(MoeHipLayer *layer, float *wr);
  * accumulate != 0 adds into out instead (x += MoE(x_norm) decode form). */
 int moe_hip_forward_dev(MoeHipLayer *layer, const float *x, int T, float *out,
                         float *probs, int *ids, int accumulate, void *stream);
+
+/* rms_norm (src/matrix.c:666-711) on device rows: y [rows x cols] =
+ * (x * inv_rms) * w with the reference's summation order and fused
+ * multiply-adds, and a correctly rounded 1/sqrt (see moe_block_ffn). */
+int moe_hip_rms_norm_dev(const float *x, const float *w, float eps, int rows, int cols,
+                         float *y, void *stream);
+
+/* The MoE block's FFN sublayer on a device-resident residual stream x
+ * [T x d], in place: x += MoE(rms_norm(x; rms_w, eps)) (src/transformer.c:
+ * 760-767 with the residual add of :767; also the decode form of
+ * src/inference.c:310-343 for T rows).  x_norm [T x d] receives the
+ * normalised rows (NULL: library workspace); probs and ids as in
+ * moe_hip_forward_dev.  No host round trip. */
+int moe_hip_ffn_sublayer_dev(MoeHipLayer *layer, float *x, const float *rms_w, float eps, int T,
+                             float *x_norm, float *probs, int *ids, void *stream);
 
 /* Routing and dispatch only: probs [T x E], ids [T x k], gate weights
  * gw [T x k] (renormalised), counts [E], offsets [E+1], perm [T x k]

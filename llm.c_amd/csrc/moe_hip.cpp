@@ -100,10 +100,10 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, stage,
-        counters;
+        counters, xn, rmsw;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
-                         &tile_expert, &perm, &h, &ys, &stage, &counters};
+                         &tile_expert, &perm, &h, &ys, &stage, &counters, &xn, &rmsw};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -653,6 +653,77 @@ int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x
 
 void moe_decode_step(const MoEWeights *w, const ModelConfig *cfg, const float *x_norm, float *x) {
     die_on(moe_decode_batch(w, cfg, x_norm, 1, x), "moe_decode_step");
+}
+
+int moe_hip_rms_norm_dev(const float *x, const float *w, float eps, int rows, int cols, float *y,
+                         void *stream) {
+    if (rows < 0 || cols <= 0 || (rows > 0 && (!x || !w || !y)))
+        return set_err(MOE_HIP_ERR_ARG, "bad rms_norm arguments");
+    if (rows == 0) return MOE_HIP_OK;
+    TRY(ensure_init());
+    HIP_TRY(moe::launch_rms_norm(x, w, eps, rows, cols, y, pick_stream(stream)));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_ffn_sublayer_dev(MoeHipLayer *L, float *x, const float *rms_w, float eps, int T,
+                             float *x_norm, float *probs, int *ids, void *stream) {
+    if (!L || T < 0 || (T > 0 && (!x || !rms_w)))
+        return set_err(MOE_HIP_ERR_ARG, "bad sublayer arguments");
+    if (T == 0) return MOE_HIP_OK;
+    TRY(ensure_init());
+    float *xn = x_norm;
+    if (!xn) {
+        TRY(g_ws.xn.reserve(sizeof(float) * (size_t)T * L->d));
+        xn = g_ws.xn.as<float>();
+    }
+    HIP_TRY(moe::launch_rms_norm(x, rms_w, eps, T, L->d, xn, pick_stream(stream)));
+    return moe_hip_forward_dev(L, xn, T, x, probs, ids, 1, stream);
+}
+
+int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,
+                      const ModelConfig *cfg, ForwardCache *cache) {
+    if (!x || !rms_ffn || !w || !cfg || !cache) return set_err(MOE_HIP_ERR_ARG, "null argument");
+    const int T = x->rows, d = x->cols, F = cfg->ffn_hidden, E = w->n_experts, k = w->top_k;
+    if (d != cfg->d_model) return set_err(MOE_HIP_ERR_ARG, "x has %d columns, d_model %d", d, cfg->d_model);
+    const Matrix &xn = cache->x_norm_ffn, &fo = cache->ffn_out;
+    if (xn.rows != T || xn.cols != d || fo.rows != T || fo.cols != d)
+        return set_err(MOE_HIP_ERR_ARG, "cache x_norm_ffn / ffn_out must be %dx%d", T, d);
+    TRY(check_shapes(d, F, E, k));
+    if (T == 0) return MOE_HIP_OK;
+    if (!x->data || !xn.data || !fo.data || !cache->router_probs || !cache->expert_ids)
+        return set_err(MOE_HIP_ERR_ARG, "null data pointer");
+    TRY(ensure_init());
+    MoeHipLayer *L = nullptr;
+    TRY(resident_layer(w, d, F, &L));
+    const size_t xd = (size_t)T * d;
+    TRY(g_ws.x.reserve(sizeof(float) * xd));
+    TRY(g_ws.xn.reserve(sizeof(float) * xd));
+    TRY(g_ws.out.reserve(sizeof(float) * xd));
+    TRY(g_ws.rmsw.reserve(sizeof(float) * d));
+    TRY(g_ws.probs.reserve(sizeof(float) * (size_t)T * E));
+    TRY(g_ws.ids.reserve(sizeof(int) * (size_t)T * k));
+    float *dx = g_ws.x.as<float>(), *dxn = g_ws.xn.as<float>(), *dout = g_ws.out.as<float>();
+    float *dw = g_ws.rmsw.as<float>(), *dprobs = g_ws.probs.as<float>();
+    int *dids = g_ws.ids.as<int>();
+    HIP_TRY(hipMemcpyAsync(dx, x->data, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipMemcpyAsync(dw, rms_ffn, sizeof(float) * d, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(moe::launch_rms_norm(dx, dw, cfg->rms_norm_eps, T, d, dxn, g_stream));
+    TRY(moe_hip_forward_dev(L, dxn, T, dout, dprobs, dids, 0, g_stream));
+    HIP_TRY(hipMemcpyAsync(xn.data, dxn, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipMemcpyAsync(fo.data, dout, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipMemcpyAsync(cache->router_probs, dprobs, sizeof(float) * (size_t)T * E,
+                           hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
+                           hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    // Residual 2 (src/transformer.c:767, mat_add_inplace).
+    for (size_t i = 0; i < xd; ++i) x->data[i] = x->data[i] + fo.data[i];
+    return MOE_HIP_OK;
+}
+
+void moe_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w, const ModelConfig *cfg,
+                   ForwardCache *cache) {
+    die_on(moe_hip_block_ffn(x, rms_ffn, w, cfg, cache), "moe_block_ffn");
 }
 
 int moe_hip_dev_alloc(void **ptr, size_t bytes) {

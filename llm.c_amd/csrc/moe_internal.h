@@ -131,6 +131,9 @@ hipError_t launch_unpack_down(const float *src, float *wd, int F, int d,
                               hipStream_t s);
 // Elementwise exp_poly (which = 0) or glibc-expf (which = 1) on the device,
 // exactly as the routing kernels evaluate them.
+// rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
+hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,
+                           float *y, hipStream_t s);
 // dst[c][r] = src[r][c] for a rows x cols matrix.
 hipError_t launch_transpose(const float *src, float *dst, int rows, int cols, hipStream_t s);
 hipError_t launch_eval_exp(int which, const float *x, float *y, size_t n, hipStream_t s);

@@ -411,6 +411,56 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float *src, float 
         if (c0 + i < cols && r0 + tx < rows) dst[(size_t)(c0 + i) * rows + r0 + tx] = tile[tx][i];
 }
 
+// rms_norm (src/matrix.c:666-711) rows: y = (x * inv_rms) * w.  Four lanes
+// per row, lane q owning columns 16b + 4q .. 16b + 4q + 3 of every 16-column
+// block, i.e. the reference's accumulator lanes l = 4q .. 4q + 3 (l < 8 of
+// its first 8-wide register, l - 8 of its second).  Then: first += second
+// lane-wise, one 8-column block into the first, hsum256's fold
+// ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)), the scalar tail as FMAs, and
+// inv_rms = 1 / sqrt(fma(ss, 1/cols, eps)) correctly rounded (the reference
+// build estimates it with RSQRTSS and one Newton-Raphson step).
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const float *w, float eps,
+                                                       int rows, int cols, float rcp_cols,
+                                                       float *y) {
+    const int q = threadIdx.x & 3;
+    const int row = blockIdx.x * 64 + (threadIdx.x >> 2);
+    const bool live = row < rows;
+    const float *xr = x + (size_t)(live ? row : 0) * cols;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    const int nb = cols / 16;
+    for (int b = 0; b < nb; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = xr[16 * b + 4 * q + i];
+            a[i] = fmaf(v, v, a[i]);
+        }
+    // Lanes 0, 1 hold accumulator lanes 0..7; add lanes 8..15 from 2, 3.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = a[i] + __shfl_down(a[i], 2, 4);
+    int j = 16 * nb;
+    if (j + 8 <= cols) {
+        if (q < 2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = xr[j + 4 * q + i];
+                a[i] = fmaf(v, v, a[i]);
+            }
+        j += 8;
+    }
+    float s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = a[i] + __shfl_down(a[i], 1, 4);   // v_i + v_{i+4}
+    float ss = (s[0] + s[1]) + (s[2] + s[3]);
+    for (int t = j; t < cols; ++t) ss = fmaf(xr[t], xr[t], ss);
+    const float inv = __shfl(1.0f / sqrtf(fmaf(ss, rcp_cols, eps)), 0, 4);
+    if (!live) return;
+    float *yr = y + (size_t)row * cols;
+    for (int c = 4 * q; c < cols; c += 16)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (c + i < cols) yr[c + i] = (xr[c + i] * inv) * w[c + i];
+}
+
 __global__ __launch_bounds__(256) void eval_exp_kernel(int which, const float *x, float *y,
                                                       size_t n) {
     for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
@@ -423,6 +473,14 @@ hipError_t launch_transpose(const float *src, float *dst, int rows, int cols, hi
     if (rows <= 0 || cols <= 0) return hipSuccess;
     dim3 grid((cols + 31) / 32, (rows + 31) / 32);
     hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, s, src, dst, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,
+                           float *y, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(256), 0, s, x, w,
+                       eps, rows, cols, 1.0f / (float)cols, y);
     return hipGetLastError();
 }
 

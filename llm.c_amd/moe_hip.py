@@ -38,6 +38,10 @@ SIGNATURES = {
     "moe_decode_step": (None, [C.POINTER(MoEWeights), C.POINTER(ModelConfig), _F, _F]),
     "moe_decode_batch": (C.c_int, [C.POINTER(MoEWeights), C.POINTER(ModelConfig), _F,
                                    C.c_int, _F]),
+    "moe_block_ffn": (None, [C.POINTER(Matrix), _F, C.POINTER(MoEWeights),
+                             C.POINTER(ModelConfig), C.POINTER(ForwardCache)]),
+    "moe_hip_block_ffn": (C.c_int, [C.POINTER(Matrix), _F, C.POINTER(MoEWeights),
+                                    C.POINTER(ModelConfig), C.POINTER(ForwardCache)]),
     "moe_hip_init": (C.c_int, [C.c_int]),
     "moe_hip_shutdown": (None, []),
     "moe_hip_invalidate": (C.c_int, [C.POINTER(MoEWeights)]),
@@ -53,6 +57,8 @@ SIGNATURES = {
     "moe_hip_layer_get_router": (C.c_int, [_P, _F]),
     "moe_hip_forward_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
     "moe_hip_route_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P, _P, _P, _P]),
+    "moe_hip_rms_norm_dev": (C.c_int, [_P, _P, C.c_float, C.c_int, C.c_int, _P, _P]),
+    "moe_hip_ffn_sublayer_dev": (C.c_int, [_P, _P, _P, C.c_float, C.c_int, _P, _P, _P, _P]),
     "moe_hip_fill_normal_dev": (C.c_int, [_P, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float,
                                           C.c_float, _P]),
     "moe_hip_eval_exp": (C.c_int, [C.c_int, _P, _P, C.c_size_t, _P]),
@@ -126,6 +132,27 @@ def decode_batch(x_norm, x, hw):
     return xo
 
 
+def block_ffn(x, rms_w, hw):
+    """The FFN half of a MoE block_forward through moe_hip_block_ffn: returns
+    (x + ffn_out, x_norm_ffn, ffn_out, probs, ids) for x [T x d] (numpy)."""
+    xo = np.array(x, dtype=np.float32, copy=True, order="C")
+    T = xo.shape[0]
+    xn = np.zeros((T, hw.d), np.float32)
+    fo = np.zeros((T, hw.d), np.float32)
+    fc, probs, ids = make_cache(T, hw.E, hw.k)
+    fc.x_norm_ffn = matrix(xn)
+    fc.ffn_out = matrix(fo)
+    w = np.ascontiguousarray(rms_w, dtype=np.float32)
+    cfg = hw.config(T)
+    check(lib().moe_hip_block_ffn(C.byref(matrix(xo)), fptr(w), C.byref(hw.weights),
+                                  C.byref(cfg), C.byref(fc)))
+    return xo, xn, fo, probs, ids
+
+
+def rms_norm_dev(x_ptr, w_ptr, eps, rows, cols, y_ptr, stream=None):
+    check(lib().moe_hip_rms_norm_dev(x_ptr, w_ptr, eps, rows, cols, y_ptr, stream))
+
+
 class Layer:
     """Device-resident MoE layer (packed weights in HBM)."""
 
@@ -176,6 +203,12 @@ class Layer:
                     stream=None):
         check(lib().moe_hip_forward_dev(self.h, x_ptr, T, out_ptr, probs_ptr, ids_ptr,
                                         accumulate, stream))
+
+    def ffn_sublayer_dev(self, x_ptr, rms_w_ptr, eps, T, x_norm_ptr=None, probs_ptr=None,
+                         ids_ptr=None, stream=None):
+        """x += MoE(rms_norm(x)) in place on device rows x [T x d]."""
+        check(lib().moe_hip_ffn_sublayer_dev(self.h, x_ptr, rms_w_ptr, eps, T, x_norm_ptr,
+                                             probs_ptr, ids_ptr, stream))
 
     def route_dev(self, x_ptr, T, probs=None, ids=None, gw=None, counts=None, offsets=None,
                   perm=None, stream=None):

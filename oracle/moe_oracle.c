@@ -25,6 +25,9 @@
  *   orc_moe_forward     moe_forward src/transformer.c:287-366 with
  *                       ffn_forward src/transformer.c:157-165
  *   orc_moe_forward_f64 textbook fp64 MoE layer (tolerance reference)
+ *   orc_rms_norm        rms_norm src/matrix.c:666-711 (AVX2+FMA build) as
+ *                       the reference build compiles it, except 1/sqrt:
+ *                       see the function
  *
  * Numerics: compile with -ffp-contract=off; every fused multiply-add the
  * reference performs is an explicit fmaf()/fma() here.
@@ -392,6 +395,45 @@ static void swiglu_impl(const float *g, const float *u, float *h, int n) {
 void orc_swiglu(const float *g, const float *u, float *h, int n) {
     unsigned int csr = fpenv_enter();
     swiglu_impl(g, u, h, n);
+    fpenv_leave(csr);
+}
+
+/* ------------------------------------------------------------------------
+ * rms_norm (src/matrix.c:666-711), AVX2+FMA build, per row:
+ *   ss: lanes l < 8 of two 8-wide FMA accumulators over 16-column blocks
+ *       (v0 takes columns 16b + l, v1 columns 16b + 8 + l), v0 += v1
+ *       lane-wise, one more 8-column block into v0 if present, hsum256 fold
+ *       ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)), then the scalar tail as FMAs;
+ *   inv_rms = 1 / sqrt(ss / cols + eps), which the compiled reference (GCC
+ *       -ffast-math, our build of matrix.c) evaluates as fma(ss, 1/cols, eps)
+ *       followed by RSQRTSS and one Newton-Raphson step.  RSQRTSS's table is
+ *       the x86 vendor's, so here (and on the GPU) 1/sqrt is correctly
+ *       rounded instead: the two agree to an ulp or two, not bit for bit;
+ *   y = (x * inv_rms) * w.
+ * Columns not a multiple of 8 take a scalar tail here; the compiled
+ * reference vectorises that tail loop (another summation order).
+ * ---------------------------------------------------------------------- */
+void orc_rms_norm(const float *x, const float *w, float eps, int rows, int cols, float *y) {
+    unsigned int csr = fpenv_enter();
+    const float rcp_cols = 1.0f / (float)cols;
+    for (int i = 0; i < rows; ++i) {
+        const float *xr = x + (size_t)i * cols;
+        float *yr = y + (size_t)i * cols;
+        float v0[8] = {0, 0, 0, 0, 0, 0, 0, 0}, v1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int j = 0;
+        for (; j + 16 <= cols; j += 16)
+            for (int l = 0; l < 8; ++l) {
+                v0[l] = fmaf(xr[j + l], xr[j + l], v0[l]);
+                v1[l] = fmaf(xr[j + 8 + l], xr[j + 8 + l], v1[l]);
+            }
+        for (int l = 0; l < 8; ++l) v0[l] = v0[l] + v1[l];
+        for (; j + 8 <= cols; j += 8)
+            for (int l = 0; l < 8; ++l) v0[l] = fmaf(xr[j + l], xr[j + l], v0[l]);
+        float ss = ((v0[0] + v0[4]) + (v0[1] + v0[5])) + ((v0[2] + v0[6]) + (v0[3] + v0[7]));
+        for (; j < cols; ++j) ss = fmaf(xr[j], xr[j], ss);
+        const float inv = 1.0f / sqrtf(fmaf(ss, rcp_cols, eps));
+        for (int k = 0; k < cols; ++k) yr[k] = (xr[k] * inv) * w[k];
+    }
     fpenv_leave(csr);
 }
 

@@ -48,6 +48,7 @@ def orc():
         L.orc_expf_array.argtypes = [_F, _F, C.c_longlong]
         L.orc_exp_poly_array.argtypes = [_F, _F, C.c_longlong]
         L.orc_set_softmax_tail_recip.argtypes = [C.c_int]
+        L.orc_rms_norm.argtypes = [_F, _F, C.c_float, C.c_int, C.c_int, _F]
         L.orc_softmax_rows.argtypes = [_F, C.c_int, C.c_int]
         L.orc_topk.argtypes = [_F, C.c_int, C.c_int, C.c_int, _I, _F]
         L.orc_dispatch.argtypes = [_I, C.c_int, C.c_int, C.c_int, _I, _I, _I]
@@ -81,6 +82,17 @@ def synth(shape, seed, stream, std, mean=0.0):
     a = np.empty(shape, np.float32)
     orc().orc_synth_normal(fptr(a), a.size, seed, stream, mean, std)
     return a
+
+
+def rms_norm(x, w, eps):
+    """rms_norm (src/matrix.c:666-711) rows of x with weight w; see
+    orc_rms_norm for the one deliberate difference (correctly rounded
+    1/sqrt instead of the x86 RSQRTSS estimate)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    orc().orc_rms_norm(fptr(x), fptr(np.ascontiguousarray(w, np.float32)), eps, x.shape[0],
+                       x.shape[1], fptr(y))
+    return y
 
 
 def router_logits(x, wr, bias=None):

@@ -13,6 +13,8 @@ small .npz fixtures next to this script:
   golden_route.npz     probs/ids of token samples at every config's router
                        shape (config 5 with its Zipf bias)
   golden_moe.npz       layer outputs of token samples at configs 2-5
+  golden_rms.npz       rms_norm (src/matrix.c:666-711) rows at the configs'
+                       widths and at widths with 8-column and scalar tails
 
 The reference MoE has no router bias (src/transformer.c:299-300).  Config 5
 is run through the reference's own moe_forward with x extended by a column of
@@ -20,6 +22,7 @@ ones and W_router by the bias row: the FMA chain's last term is then 1*b[e],
 i.e. logits + b rounded once — the mat_mul_add form the library implements.
 
 Run (where the reference sources are present): python tests/golden/make_golden.py
+(`... make_golden.py rms` writes golden_rms.npz only)
 """
 import ctypes as C
 import hashlib
@@ -209,5 +212,37 @@ def main():
     np.savez_compressed(os.path.join(HERE, "golden_moe.npz"), **mo)
 
 
+RMS_WIDTHS = (128, 256, 512, 2048, 24, 8, 100, 7)
+
+
+def rms_inputs(cols):
+    """rms_norm golden inputs: 12 rows of N(0, 1) scaled per row over six
+    decades, one all-zero row (ss = 0), weights N(1, 0.1); eps 1e-5."""
+    x = orc.synth((14, cols), 55, cols, 1.0)
+    x *= (10.0 ** np.linspace(-3, 3, 14, dtype=np.float32))[:, None]
+    x[13] = 0.0
+    w = orc.synth((cols,), 55, 1000 + cols, 0.1, mean=1.0)
+    return np.ascontiguousarray(x), w
+
+
+def main_rms():
+    if not orc.ref_available():
+        sys.exit("oracle/_ref/libref_moe.so missing: run `make -C oracle ref` first")
+    orc.orc().orc_set_ftz_daz(1)
+    ref = orc.ref()
+    ref.rms_norm.argtypes = [C.c_void_p, C.c_void_p, C.c_float, C.c_void_p]
+    rs = {}
+    for cols in RMS_WIDTHS:
+        x, w = rms_inputs(cols)
+        y = np.zeros_like(x)
+        ref.rms_norm(C.byref(matrix(x)), w.ctypes.data, C.c_float(1e-5), C.byref(matrix(y)))
+        rs[f"out_{cols}"], rs[f"sha_x_{cols}"], rs[f"sha_w_{cols}"] = y, sha(x), sha(w)
+    np.savez_compressed(os.path.join(HERE, "golden_rms.npz"), **rs)
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["rms"]:
+        main_rms()
+    else:
+        main()
+        main_rms()

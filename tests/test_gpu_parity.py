@@ -300,6 +300,74 @@ def test_decode_batch_c4():
     assert_close(x_one - x0[:1], o1, "c4 decode step")
 
 
+# --------------------------------------------------------------------- rms_norm + FFN sublayer
+@pytest.mark.parametrize("cols", [128, 256, 512, 2048, 24, 8, 100, 7])
+def test_rms_norm_device_bitexact(cols):
+    """Device rms_norm against the oracle, bit for bit: the reference's
+    accumulator lanes and fold, fused multiply-adds, a correctly rounded
+    1/sqrt; 300 rows over six decades, one all-zero row."""
+    rows = 300
+    scale = (10.0 ** np.linspace(-3, 3, rows)).astype(np.float32)[:, None]
+    x = np.ascontiguousarray(orc.synth((rows, cols), 21, cols, 1.0) * scale)
+    x[7] = 0.0
+    w = orc.synth((cols,), 21, 500 + cols, 0.1, mean=1.0)
+    dx, dw = mh.DeviceArray.from_host(x), mh.DeviceArray.from_host(w)
+    dy = mh.DeviceArray((rows, cols))
+    mh.rms_norm_dev(dx.ptr, dw.ptr, 1e-5, rows, cols, dy.ptr)
+    mh.synchronize()
+    ref = orc.rms_norm(x, w, 1e-5)
+    nd = int((bits(dy.to_host()) != bits(ref)).sum())
+    assert nd == 0, f"{nd} of {ref.size} normalised values differ in bits"
+
+
+@pytest.mark.parametrize("name,T", [("c4", 64), ("c2", 512)])
+def test_ffn_sublayer_dev(name, T):
+    """x += MoE(rms_norm(x)) in place on a device-resident residual stream:
+    x_norm bit-exact, routing bit-exact, x within the layer tolerance."""
+    c = CONFIGS[name]
+    d, F, E, k = c["d"], c["F"], c["E"], c["k"]
+    say(f"ffn sublayer {name}: T={T} d={d} F={F} E={E} k={k}")
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(11, c["std_router"], c["std_expert"])
+    hw = host_layer(d, F, E, k, 11, c["std_router"], c["std_expert"])
+    x = np.ascontiguousarray(orc.synth((T, d), 11, 0, 1.0) * np.float32(3.0))
+    w = orc.synth((d,), 11, 9, 0.1, mean=1.0)
+    dx, dw = mh.DeviceArray.from_host(x), mh.DeviceArray.from_host(w)
+    dxn = mh.DeviceArray((T, d))
+    dprobs = mh.DeviceArray((T, E))
+    dids = mh.DeviceArray((T, k), np.int32)
+    layer.ffn_sublayer_dev(dx.ptr, dw.ptr, 1e-5, T, dxn.ptr, dprobs.ptr, dids.ptr)
+    mh.synchronize()
+    xn_ref = orc.rms_norm(x, w, 1e-5)
+    assert np.array_equal(bits(dxn.to_host()), bits(xn_ref))
+    o_ref, p_ref, i_ref = orc.moe_forward(xn_ref, hw, nthreads=16)
+    assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+    assert np.array_equal(dids.to_host(), i_ref)
+    assert_close(dx.to_host(), x + o_ref, f"{name} sublayer")
+    # The workspace form (x_norm not returned) gives the same bits.
+    dx2 = mh.DeviceArray.from_host(x)
+    layer.ffn_sublayer_dev(dx2.ptr, dw.ptr, 1e-5, T)
+    mh.synchronize()
+    assert np.array_equal(bits(dx2.to_host()), bits(dx.to_host()))
+    layer.close()
+
+
+def test_block_ffn_dropin_c1():
+    """moe_block_ffn (host pointers): the FFN half of a MoE block_forward."""
+    c = CONFIGS["c1"]
+    hw = host_layer(c["d"], c["F"], c["E"], c["k"], 0, c["std_router"], c["std_expert"])
+    x = orc.synth((c["T"], c["d"]), 0, 5, 1.0)
+    w = orc.synth((c["d"],), 0, 6, 0.1, mean=1.0)
+    x1, xn, fo, probs, ids = mh.block_ffn(x, w, hw)
+    xn_ref = orc.rms_norm(x, w, 1e-5)
+    assert np.array_equal(bits(xn), bits(xn_ref))
+    o_ref, p_ref, i_ref = orc.moe_forward(xn_ref, hw)
+    assert np.array_equal(bits(probs), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    assert_close(fo, o_ref, "c1 block ffn_out")
+    assert np.array_equal(bits(x1), bits(x + fo))
+
+
 @pytest.mark.parametrize("path", [2, 3, 4, 1], ids=["gemv", "gemv2", "gemv4", "gemm"])
 def test_graph_replay(path):
     """A captured forward (two layers, accumulating) replays to the same bits

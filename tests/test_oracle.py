@@ -293,6 +293,68 @@ def test_oracle_vs_compiled_reference_live():
         orc.orc().orc_set_ftz_daz(0)
 
 
+# ------------------------------------------------------------------ rms_norm
+def ulps(a, b):
+    ia = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    ib = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("cols", mg.RMS_WIDTHS)
+def test_rms_norm_close_to_compiled_reference(cols):
+    """Against rms_norm compiled from src/matrix.c: the reference build takes
+    1/sqrt from RSQRTSS plus a Newton step (x86-vendor tables), the oracle
+    correctly rounded, so the rows agree to a few ulp, not bitwise.  Rows
+    span six decades; the last row is all zeros."""
+    g = load("golden_rms.npz")
+    x, w = mg.rms_inputs(cols)
+    assert mg.sha(x) == str(g[f"sha_x_{cols}"]) and mg.sha(w) == str(g[f"sha_w_{cols}"])
+    orc.orc().orc_set_ftz_daz(1)
+    try:
+        y = orc.rms_norm(x, w, 1e-5)
+    finally:
+        orc.orc().orc_set_ftz_daz(0)
+    ref = g[f"out_{cols}"]
+    assert int(ulps(y, ref).max()) <= 4
+    assert np.array_equal(y[13], ref[13]) and not np.any(y[13])
+
+
+def test_rms_norm_textbook_fp64():
+    x = orc.synth((64, 300), 8, 0, 1.0) * 7.0
+    w = orc.synth((300,), 8, 1, 0.2, mean=1.0)
+    y = orc.rms_norm(x, w, 1e-5)
+    xd = x.astype(np.float64)
+    yd = xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + 1e-5) * w.astype(np.float64)
+    assert float(np.abs(y - yd).max() / np.abs(yd).max()) < 1e-6
+
+
+def test_rms_norm_power_of_two_scaling_is_exact():
+    """eps = 0: scaling a row by 2^j scales ss by 4^j and 1/sqrt by 2^-j
+    exactly, so y is unchanged bit for bit (any reordering of the squares or
+    a dropped term would survive this, a wrong mean would not: see below)."""
+    x = orc.synth((16, 512), 9, 0, 1.0)
+    w = orc.synth((512,), 9, 1, 0.1, mean=1.0)
+    y = orc.rms_norm(x, w, 0.0)
+    for j in (-6, -1, 3, 10):
+        assert np.array_equal(bits(orc.rms_norm(x * np.float32(2.0 ** j), w, 0.0)), bits(y))
+    # Constant rows c = 2^j, eps = 0: inv_rms = 1/|c| exactly, y = sign(c) * w.
+    for c in (0.25, -8.0, 1.0):
+        xc = np.full((1, 48), c, np.float32)
+        assert np.array_equal(bits(orc.rms_norm(xc, w[:48], 0.0)[0]),
+                              bits(np.float32(math.copysign(1.0, c)) * w[:48]))
+
+
+def test_rms_norm_mean_uses_all_columns():
+    """One large column among zeros: ss = v^2 whatever the block it falls
+    in (16-blocks, the 8-block, the scalar tail), y = v / sqrt(v^2/cols)."""
+    for cols in (40, 100, 7):
+        for j in range(cols):
+            x = np.zeros((1, cols), np.float32)
+            x[0, j] = 4.0
+            y = orc.rms_norm(x, np.ones(cols, np.float32), 0.0)
+            assert y[0, j] == np.float32(4.0) / np.sqrt(np.float32(16.0 / cols)), (cols, j)
+
+
 # ------------------------------------------------------------------ inputs
 def test_synthetic_generator():
     a = orc.synth((200000,), 1, 2, 1.0)
