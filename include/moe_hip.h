@@ -206,6 +206,24 @@ int moe_hip_route_dev(MoeHipLayer *layer, const float *x, int T, float *probs,
                       int *ids, float *gw, int *counts, int *offsets, int *perm,
                       void *stream);
 
+/* ---------------------------------------------------------------------------
+ * Checkpoints: the MoE blocks of a file written by model_save
+ * (src/transformer.c:573-616, read back by model_load :624-700) straight into
+ * packed device layers, one matrix at a time (host memory: 3 x d x F floats
+ * of pinned staging), with every block's rms_ffn scale on the device.
+ * Embeddings, attention, dense FFN blocks and the head are skipped.  Every
+ * block is MoE when n_experts > 1 (src/transformer.c:437), else none is.
+ * ------------------------------------------------------------------------- */
+typedef struct MoeHipModel MoeHipModel;
+
+int moe_hip_model_load(const char *path, MoeHipModel **model);
+int moe_hip_model_free(MoeHipModel *model);
+int moe_hip_model_config(const MoeHipModel *model, ModelConfig *cfg);
+/* Block l's MoE layer (owned by the model), or NULL for a dense block. */
+MoeHipLayer *moe_hip_model_layer(MoeHipModel *model, int layer);
+/* Block l's rms_ffn scale [d_model] in device memory. */
+const float *moe_hip_model_rms_ffn(const MoeHipModel *model, int layer);
+
 /* Device synthetic fill: dst[i] = N(mean, std) sample of (seed, stream, i). */
 int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed,
                             uint64_t stream_id, float mean, float std,

@@ -9,6 +9,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <algorithm>
 #include <vector>
 
 #include "moe_internal.h"
@@ -298,30 +299,176 @@ int moe_hip_layer_destroy(MoeHipLayer *L) {
     return MOE_HIP_OK;
 }
 
+// Router [d x E] from host memory: device copy, its transpose, and the
+// non-finite check that selects the zero-skipping router.
+static int upload_router(MoeHipLayer *L, const float *wr) {
+    HIP_TRY(hipMemcpyAsync(L->wr, wr, sizeof(float) * (size_t)L->d * L->E, hipMemcpyHostToDevice,
+                           g_stream));
+    HIP_TRY(moe::launch_transpose(L->wr, L->wrT, L->d, L->E, g_stream));
+    L->wr_nonfinite = 0;
+    for (size_t i = 0; i < (size_t)L->d * L->E; ++i)
+        if (!std::isfinite(wr[i])) { L->wr_nonfinite = 1; break; }
+    return MOE_HIP_OK;
+}
+
+// Expert e from host memory (reference layout) into the packed arrays,
+// through the device staging buffer (3 d F floats).
+static int upload_expert(MoeHipLayer *L, int e, const float *wg, const float *wu,
+                         const float *wd) {
+    const size_t dF = (size_t)L->d * L->F;
+    TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
+    float *st = g_ws.stage.as<float>();
+    HIP_TRY(hipMemcpyAsync(st, wg, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipMemcpyAsync(st + dF, wu, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipMemcpyAsync(st + 2 * dF, wd, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(moe::launch_pack_gateup(st, st + dF, L->wgu + 2 * dF * e, L->d, L->F, g_stream));
+    HIP_TRY(moe::launch_pack_down(st + 2 * dF, L->wdT + dF * e, L->F, L->d, g_stream));
+    return MOE_HIP_OK;
+}
+
 int moe_hip_layer_load(MoeHipLayer *L, const MoEWeights *w) {
     if (!L) return set_err(MOE_HIP_ERR_ARG, "null layer");
     if (!w || w->n_experts != L->E || w->top_k != L->k)
         return set_err(MOE_HIP_ERR_ARG, "weights do not match the layer (E=%d k=%d)", L->E, L->k);
     TRY(validate_weights(w, L->d, L->F));
-    const size_t dF = (size_t)L->d * L->F;
-    TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
-    float *st = g_ws.stage.as<float>();
-    HIP_TRY(hipMemcpyAsync(L->wr, w->W_router.data, sizeof(float) * (size_t)L->d * L->E,
-                           hipMemcpyHostToDevice, g_stream));
-    HIP_TRY(moe::launch_transpose(L->wr, L->wrT, L->d, L->E, g_stream));
-    L->wr_nonfinite = 0;
-    for (size_t i = 0; i < (size_t)L->d * L->E; ++i)
-        if (!std::isfinite(w->W_router.data[i])) { L->wr_nonfinite = 1; break; }
+    TRY(upload_router(L, w->W_router.data));
     for (int e = 0; e < L->E; ++e) {
         const FFNWeights &f = w->experts[e];
-        HIP_TRY(hipMemcpyAsync(st, f.W_gate.data, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
-        HIP_TRY(hipMemcpyAsync(st + dF, f.W_up.data, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
-        HIP_TRY(hipMemcpyAsync(st + 2 * dF, f.W_down.data, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
-        HIP_TRY(moe::launch_pack_gateup(st, st + dF, L->wgu + 2 * dF * e, L->d, L->F, g_stream));
-        HIP_TRY(moe::launch_pack_down(st + 2 * dF, L->wdT + dF * e, L->F, L->d, g_stream));
+        TRY(upload_expert(L, e, f.W_gate.data, f.W_up.data, f.W_down.data));
     }
     HIP_TRY(hipStreamSynchronize(g_stream));
     return MOE_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Checkpoints written by model_save (src/transformer.c:573-616): uint32
+// magic 0x4C4C4D43, ModelConfig, embed [vocab x d], then per block
+// rms_attn [d], W_Q [d x nh*hd], W_K, W_V [d x nkv*hd], W_O [nh*hd x d],
+// rms_ffn [d] and either W_gate, W_up [d x F], W_down [F x d] (dense) or
+// W_router [d x E] and each expert's W_gate, W_up, W_down (n_experts > 1,
+// src/transformer.c:437); finally rms_final [d] and lm_head [d x vocab].
+// All fp32, row-major, no padding.
+struct MoeHipModel {
+    ModelConfig cfg{};
+    std::vector<MoeHipLayer *> layers;   // null for dense blocks
+    std::vector<float *> rms_ffn;        // device [d], every block
+};
+
+namespace {
+
+struct CkptFile {
+    FILE *f = nullptr;
+    ~CkptFile() { if (f) fclose(f); }
+    bool skip(size_t floats) { return fseeko(f, (off_t)(floats * sizeof(float)), SEEK_CUR) == 0; }
+    bool read(float *dst, size_t floats) { return fread(dst, sizeof(float), floats, f) == floats; }
+};
+
+}  // namespace
+
+int moe_hip_model_free(MoeHipModel *m) {
+    if (!m) return MOE_HIP_OK;
+    for (MoeHipLayer *L : m->layers)
+        if (L) moe_hip_layer_destroy(L);
+    for (float *p : m->rms_ffn)
+        if (p) (void)hipFree(p);
+    delete m;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_model_load(const char *path, MoeHipModel **out) {
+    if (!path || !out) return set_err(MOE_HIP_ERR_ARG, "null argument");
+    *out = nullptr;
+    TRY(ensure_init());
+    CkptFile cf;
+    cf.f = fopen(path, "rb");
+    if (!cf.f) return set_err(MOE_HIP_ERR_ARG, "cannot open %s", path);
+    uint32_t magic = 0;
+    ModelConfig cfg;
+    if (fread(&magic, sizeof(magic), 1, cf.f) != 1 || magic != 0x4C4C4D43u ||
+        fread(&cfg, sizeof(cfg), 1, cf.f) != 1)
+        return set_err(MOE_HIP_ERR_ARG, "%s: not a model checkpoint (magic/config)", path);
+    const int d = cfg.d_model, F = cfg.ffn_hidden, E = cfg.n_experts, k = cfg.top_k_experts;
+    if (d <= 0 || F <= 0 || cfg.n_layers < 0 || cfg.vocab_size < 0 || cfg.n_heads <= 0 ||
+        cfg.n_kv_heads <= 0 || cfg.head_dim <= 0 || E < 1)
+        return set_err(MOE_HIP_ERR_ARG, "%s: implausible config", path);
+    const bool moe = E > 1;
+    if (moe) TRY(check_shapes(d, F, E, k));
+    const size_t qd = (size_t)cfg.n_heads * cfg.head_dim, kd = (size_t)cfg.n_kv_heads * cfg.head_dim;
+    const size_t dF = (size_t)d * F;
+    // The whole file must be there, as model_load reads it to the end.
+    const size_t per_block = (size_t)d + d * qd + 2 * d * kd + qd * d + d +
+                             (moe ? (size_t)d * E + (size_t)E * 3 * dF : 3 * dF);
+    const size_t floats = (size_t)cfg.vocab_size * d + (size_t)cfg.n_layers * per_block + d +
+                          (size_t)d * cfg.vocab_size;
+    const off_t header = (off_t)(sizeof(magic) + sizeof(cfg));
+    if (fseeko(cf.f, 0, SEEK_END) != 0 || ftello(cf.f) < header + (off_t)(floats * sizeof(float)) ||
+        fseeko(cf.f, header, SEEK_SET) != 0)
+        return set_err(MOE_HIP_ERR_ARG, "%s: shorter than its config implies (%zu floats)", path,
+                       floats);
+    auto *m = new MoeHipModel;
+    m->cfg = cfg;
+    int rc = MOE_HIP_OK;
+    std::vector<float> host;
+    float *hb = nullptr;   // pinned staging for the expert matrices
+    auto fail = [&](int code) {
+        if (hb) (void)hipHostFree(hb);
+        moe_hip_model_free(m);
+        return code;
+    };
+    auto trunc = [&](int l) {
+        return fail(set_err(MOE_HIP_ERR_ARG, "%s: truncated in block %d", path, l));
+    };
+    if (!cf.skip((size_t)cfg.vocab_size * d)) return trunc(-1);
+    if (moe && hipHostMalloc((void **)&hb, sizeof(float) * 3 * dF, hipHostMallocDefault) != hipSuccess) {
+        hb = nullptr;
+        return fail(set_err(MOE_HIP_ERR_NOMEM, "pinned staging of %zu bytes", sizeof(float) * 3 * dF));
+    }
+    host.resize(std::max<size_t>((size_t)d * E, d));
+    for (int l = 0; l < cfg.n_layers; ++l) {
+        if (!cf.skip(d + d * qd + 2 * d * kd + qd * d)) return trunc(l);
+        if (!cf.read(host.data(), d)) return trunc(l);
+        float *rw = nullptr;
+        if (hipMalloc(&rw, sizeof(float) * d) != hipSuccess)
+            return fail(set_err(MOE_HIP_ERR_NOMEM, "rms_ffn of block %d", l));
+        m->rms_ffn.push_back(rw);
+        if (hipMemcpy(rw, host.data(), sizeof(float) * d, hipMemcpyHostToDevice) != hipSuccess)
+            return fail(set_err(MOE_HIP_ERR_HIP, "rms_ffn upload"));
+        if (!moe) {
+            m->layers.push_back(nullptr);
+            if (!cf.skip(3 * dF)) return trunc(l);
+            continue;
+        }
+        MoeHipLayer *L = nullptr;
+        if ((rc = moe_hip_layer_create(d, F, E, k, &L)) != MOE_HIP_OK) return fail(rc);
+        m->layers.push_back(L);
+        if (!cf.read(host.data(), (size_t)d * E)) return trunc(l);
+        if ((rc = upload_router(L, host.data())) != MOE_HIP_OK) return fail(rc);
+        for (int e = 0; e < E; ++e) {
+            // (the previous expert's copies out of hb must be done first)
+            if (hipStreamSynchronize(g_stream) != hipSuccess)
+                return fail(set_err(MOE_HIP_ERR_HIP, "expert upload"));
+            if (!cf.read(hb, 3 * dF)) return trunc(l);
+            if ((rc = upload_expert(L, e, hb, hb + dF, hb + 2 * dF)) != MOE_HIP_OK) return fail(rc);
+        }
+    }
+    if (hipStreamSynchronize(g_stream) != hipSuccess) return fail(set_err(MOE_HIP_ERR_HIP, "sync"));
+    if (hb) (void)hipHostFree(hb);
+    *out = m;   // (rms_final and lm_head are not needed here)
+    return MOE_HIP_OK;
+}
+
+int moe_hip_model_config(const MoeHipModel *m, ModelConfig *cfg) {
+    if (!m || !cfg) return set_err(MOE_HIP_ERR_ARG, "null argument");
+    *cfg = m->cfg;
+    return MOE_HIP_OK;
+}
+
+MoeHipLayer *moe_hip_model_layer(MoeHipModel *m, int l) {
+    return m && l >= 0 && l < (int)m->layers.size() ? m->layers[l] : nullptr;
+}
+
+const float *moe_hip_model_rms_ffn(const MoeHipModel *m, int l) {
+    return m && l >= 0 && l < (int)m->rms_ffn.size() ? m->rms_ffn[l] : nullptr;
 }
 
 int moe_hip_layer_set_router_bias(MoeHipLayer *L, const float *bias) {

@@ -58,6 +58,11 @@ SIGNATURES = {
     "moe_hip_forward_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
     "moe_hip_route_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P, _P, _P, _P]),
     "moe_hip_rms_norm_dev": (C.c_int, [_P, _P, C.c_float, C.c_int, C.c_int, _P, _P]),
+    "moe_hip_model_load": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "moe_hip_model_free": (C.c_int, [_P]),
+    "moe_hip_model_config": (C.c_int, [_P, C.POINTER(ModelConfig)]),
+    "moe_hip_model_layer": (_P, [_P, C.c_int]),
+    "moe_hip_model_rms_ffn": (_P, [_P, C.c_int]),
     "moe_hip_ffn_sublayer_dev": (C.c_int, [_P, _P, _P, C.c_float, C.c_int, _P, _P, _P, _P]),
     "moe_hip_fill_normal_dev": (C.c_int, [_P, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float,
                                           C.c_float, _P]),
@@ -156,16 +161,19 @@ def rms_norm_dev(x_ptr, w_ptr, eps, rows, cols, y_ptr, stream=None):
 class Layer:
     """Device-resident MoE layer (packed weights in HBM)."""
 
-    def __init__(self, d, F, E, k):
+    def __init__(self, d, F, E, k, handle=None):
+        """A new layer, or (handle set) a view of one owned elsewhere."""
         self.d, self.F, self.E, self.k = d, F, E, k
-        h = _P()
-        check(lib().moe_hip_layer_create(d, F, E, k, C.byref(h)))
-        self.h = h
+        self.owned = handle is None
+        if handle is None:
+            handle = _P()
+            check(lib().moe_hip_layer_create(d, F, E, k, C.byref(handle)))
+        self.h = handle
 
     def close(self):
-        if self.h:
+        if self.h and self.owned:
             lib().moe_hip_layer_destroy(self.h)
-            self.h = _P()
+        self.h = _P()
 
     def __del__(self):
         try:
@@ -214,6 +222,44 @@ class Layer:
                   perm=None, stream=None):
         check(lib().moe_hip_route_dev(self.h, x_ptr, T, probs, ids, gw, counts, offsets, perm,
                                       stream))
+
+
+class Model:
+    """The MoE blocks of a model_save checkpoint, loaded into packed device
+    layers (moe_hip_model_load)."""
+
+    def __init__(self, path):
+        h = _P()
+        check(lib().moe_hip_model_load(path.encode(), C.byref(h)))
+        self.h = h
+        cfg = ModelConfig()
+        check(lib().moe_hip_model_config(h, C.byref(cfg)))
+        self.cfg = cfg
+
+    def config(self):
+        return {f: getattr(self.cfg, f) for f, _ in ModelConfig._fields_}
+
+    def layer(self, l):
+        """Block l's MoE layer (a view owned by the model) or None."""
+        h = lib().moe_hip_model_layer(self.h, l)
+        if not h:
+            return None
+        c = self.cfg
+        return Layer(c.d_model, c.ffn_hidden, c.n_experts, c.top_k_experts, handle=_P(h))
+
+    def rms_ffn_ptr(self, l):
+        return lib().moe_hip_model_rms_ffn(self.h, l)
+
+    def close(self):
+        if self.h:
+            lib().moe_hip_model_free(self.h)
+            self.h = _P()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def fill_normal_dev(ptr, n, seed, stream_id, mean, std, stream=None):
