@@ -132,16 +132,20 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
     ms_step = dev_ms / steps
     used = [int((np.bincount(i.to_host().ravel(), minlength=E) > 0).sum()) for i in ids]
     bytes_layer = [4.0 * (3 * d * F * u + d * E + 2 * T * d) for u in used]
-    bytes_gu = [4.0 * 2 * d * F * u for u in used]
+    bytes_experts = [4.0 * 3 * d * F * u for u in used]
     dev_ms_layer = ms_step / n_layers
+    # Events: [route, (dispatch: none in decode), gate/up (the fused kernel
+    # does gate/up and down), down (only in the two-launch mode), combine].
+    experts_ms = phase[2] + phase[3]
     res = dict(layers=n_layers, T=T, d=d, F=F, E=E, k=k, ms_per_step=ms_step,
                wall_ms_per_step=wall * 1e3 / steps, graph_ms_per_step=graph_ms,
                tokens_per_s=T / (ms_step * 1e-3),
-               device_ms_per_layer=dev_ms_layer, phase_ms=phase.tolist(),
+               device_ms_per_layer=dev_ms_layer,
+               phase_ms={"route": phase[0], "experts": experts_ms, "combine": phase[4]},
                experts_used=used,
                hbm_gbs_layer=float(np.mean(bytes_layer)) / (dev_ms_layer * 1e-3) / 1e9,
                hbm_gbs_step=float(np.sum(bytes_layer)) / (ms_step * 1e-3) / 1e9,
-               gateup_gbs=float(np.mean(bytes_gu)) / (phase[2] * 1e-3) / 1e9)
+               experts_gbs=float(np.mean(bytes_experts)) / (experts_ms * 1e-3) / 1e9)
     for L in layers:
         L.close()
     return res
@@ -259,8 +263,9 @@ def main():
             "graph_ms_per_step": dec["graph_ms_per_step"],
             "device_ms_per_layer": dec["device_ms_per_layer"],
             "hbm_gbs": dec["hbm_gbs_layer"], "hbm_frac": dec["hbm_gbs_layer"] / PEAK_HBM_GBS,
-            "gateup_gbs": dec["gateup_gbs"], "phase_ms_per_layer": dict(zip(
-                ["route", "dispatch", "gate_up", "down", "combine"], dec["phase_ms"])),
+            "experts_gbs": dec["experts_gbs"],
+            # (per-phase HIP events add a few microseconds to each phase)
+            "phase_ms_per_layer": dec["phase_ms"],
         }
     print(json.dumps(line), flush=True)
 
