@@ -207,6 +207,39 @@ int moe_hip_route_dev(MoeHipLayer *layer, const float *x, int T, float *probs,
                       void *stream);
 
 /* ---------------------------------------------------------------------------
+ * The attention half of the KV-cache decode step (src/inference.c:252-308)
+ * on the GPU, for B sequences at once, each at its own position.
+ * ------------------------------------------------------------------------- */
+typedef struct MoeHipAttn MoeHipAttn;
+
+/* One block's attention: n_heads query heads, n_kv_heads kv heads of
+ * head_dim (<= 64, multiple of 8, at most 8 query heads per kv head),
+ * positions < max_seq_len. */
+int moe_hip_attn_create(int d_model, int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                        MoeHipAttn **attn);
+int moe_hip_attn_destroy(MoeHipAttn *attn);
+/* Host weights in the reference layout (src/attention.c:133-144): W_Q
+ * [d x nh*hd], W_K and W_V [d x nkv*hd], W_O [nh*hd x d]; rms_attn [d]. */
+int moe_hip_attn_load(MoeHipAttn *attn, const float *wq, const float *wk, const float *wv,
+                      const float *wo, const float *rms_attn);
+/* The model's RoPE tables (RoPEBuffer, src/attention.c:151-167): cos and
+ * sin [max_seq_len x head_dim/2], host pointers. */
+int moe_hip_attn_set_rope(MoeHipAttn *attn, const float *cos_table, const float *sin_table);
+
+/* x [B x d] device residual rows, in place: x += W_O . GQA(RoPE(q), cache)
+ * with q, k, v = rms_norm(x; rms_attn, eps) . W_Q, W_K, W_V; k and v are
+ * written at row pos[b] of sequence b's caches k_cache, v_cache
+ * [B][max_seq_len][nkv*hd] (a LayerKVCache per sequence, contiguous), and
+ * head h attends positions 0 .. pos[b] of kv head h / (nh/nkv).  pos: device
+ * ints.  rms_norm follows src/matrix.c:666-711 (see moe_block_ffn); the
+ * projections are the reference's matvec chains; the softmax and V sums
+ * run in 256-position chunks, so results match the reference within the
+ * layer tolerance rather than bit for bit.  A pos[b] outside [0, max_seq_len)
+ * leaves sequence b's caches and x row unchanged. */
+int moe_hip_attn_decode_dev(MoeHipAttn *attn, float *x, int B, const int *pos, float *k_cache,
+                            float *v_cache, float eps, void *stream);
+
+/* ---------------------------------------------------------------------------
  * Checkpoints: the MoE blocks of a file written by model_save
  * (src/transformer.c:573-616, read back by model_load :624-700) straight into
  * packed device layers, one matrix at a time (host memory: 3 x d x F floats

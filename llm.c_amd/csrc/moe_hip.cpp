@@ -101,10 +101,11 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, stage,
-        counters, xn, rmsw;
+        counters, xn, rmsw, aq, ao, apart;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
-                         &tile_expert, &perm, &h, &ys, &stage, &counters, &xn, &rmsw};
+                         &tile_expert, &perm, &h, &ys, &stage, &counters, &xn, &rmsw,
+                         &aq, &ao, &apart};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -337,6 +338,96 @@ int moe_hip_layer_load(MoeHipLayer *L, const MoEWeights *w) {
         TRY(upload_expert(L, e, f.W_gate.data, f.W_up.data, f.W_down.data));
     }
     HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Attention of the decode step (src/inference.c:252-308): weights in the
+// reference layout, the block's rms_attn scale and the RoPE tables.
+struct MoeHipAttn {
+    int d = 0, nh = 0, nkv = 0, hd = 0, max_seq = 0;
+    float *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
+    float *rms = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+};
+
+int moe_hip_attn_destroy(MoeHipAttn *a) {
+    if (!a) return MOE_HIP_OK;
+    for (float *p : {a->wq, a->wk, a->wv, a->wo, a->rms, a->cos_t, a->sin_t})
+        if (p) (void)hipFree(p);
+    delete a;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_attn_create(int d_model, int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                        MoeHipAttn **out) {
+    if (!out) return set_err(MOE_HIP_ERR_ARG, "null out-pointer");
+    *out = nullptr;
+    if (d_model <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_seq_len <= 0 ||
+        n_heads % n_kv_heads || head_dim % 8 || head_dim > 64 || n_heads / n_kv_heads > 8 ||
+        d_model % 4)
+        return set_err(MOE_HIP_ERR_UNSUPPORTED,
+                       "decode attention needs head_dim %% 8 == 0, head_dim <= 64, at most 8 "
+                       "query heads per kv head and d_model %% 4 == 0");
+    TRY(ensure_init());
+    auto *a = new MoeHipAttn;
+    a->d = d_model; a->nh = n_heads; a->nkv = n_kv_heads; a->hd = head_dim;
+    a->max_seq = max_seq_len;
+    const size_t qd = (size_t)n_heads * head_dim, kd = (size_t)n_kv_heads * head_dim;
+    const size_t tab = (size_t)max_seq_len * (head_dim / 2);
+    const size_t sizes[7] = {(size_t)d_model * qd, (size_t)d_model * kd, (size_t)d_model * kd,
+                             qd * d_model, (size_t)d_model, tab, tab};
+    float **ptrs[7] = {&a->wq, &a->wk, &a->wv, &a->wo, &a->rms, &a->cos_t, &a->sin_t};
+    for (int i = 0; i < 7; ++i)
+        if (hipMalloc(ptrs[i], sizeof(float) * sizes[i]) != hipSuccess) {
+            moe_hip_attn_destroy(a);
+            return set_err(MOE_HIP_ERR_NOMEM, "attention weights");
+        }
+    *out = a;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_attn_load(MoeHipAttn *a, const float *wq, const float *wk, const float *wv,
+                      const float *wo, const float *rms_attn) {
+    if (!a || !wq || !wk || !wv || !wo || !rms_attn) return set_err(MOE_HIP_ERR_ARG, "null argument");
+    const size_t qd = (size_t)a->nh * a->hd, kd = (size_t)a->nkv * a->hd;
+    HIP_TRY(hipMemcpy(a->wq, wq, sizeof(float) * a->d * qd, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(a->wk, wk, sizeof(float) * a->d * kd, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(a->wv, wv, sizeof(float) * a->d * kd, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(a->wo, wo, sizeof(float) * qd * a->d, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(a->rms, rms_attn, sizeof(float) * a->d, hipMemcpyHostToDevice));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_attn_set_rope(MoeHipAttn *a, const float *cos_table, const float *sin_table) {
+    if (!a || !cos_table || !sin_table) return set_err(MOE_HIP_ERR_ARG, "null argument");
+    const size_t tab = (size_t)a->max_seq * (a->hd / 2);
+    HIP_TRY(hipMemcpy(a->cos_t, cos_table, sizeof(float) * tab, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(a->sin_t, sin_table, sizeof(float) * tab, hipMemcpyHostToDevice));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_attn_decode_dev(MoeHipAttn *a, float *x, int B, const int *pos, float *k_cache,
+                            float *v_cache, float eps, void *stream) {
+    if (!a || B < 0 || (B > 0 && (!x || !pos || !k_cache || !v_cache)))
+        return set_err(MOE_HIP_ERR_ARG, "bad attention arguments");
+    if (B == 0) return MOE_HIP_OK;
+    TRY(ensure_init());
+    const int qd = a->nh * a->hd, kd = a->nkv * a->hd;
+    TRY(g_ws.xn.reserve(sizeof(float) * (size_t)B * a->d));
+    TRY(g_ws.aq.reserve(sizeof(float) * (size_t)B * qd));
+    TRY(g_ws.ao.reserve(sizeof(float) * (size_t)B * qd));
+    TRY(g_ws.apart.reserve(sizeof(float) * moe::attn_part_floats(B, a->nh, a->hd, a->max_seq)));
+    hipStream_t s = pick_stream(stream);
+    HIP_TRY(moe::launch_rms_norm(x, a->rms, eps, B, a->d, g_ws.xn.as<float>(), s));
+    moe::AttnArgs aa{};
+    aa.xn = g_ws.xn.as<float>(); aa.x = x;
+    aa.wq = a->wq; aa.wk = a->wk; aa.wv = a->wv; aa.wo = a->wo;
+    aa.cos_t = a->cos_t; aa.sin_t = a->sin_t; aa.kc = k_cache; aa.vc = v_cache; aa.pos = pos;
+    aa.q = g_ws.aq.as<float>(); aa.o = g_ws.ao.as<float>(); aa.part = g_ws.apart.as<float>();
+    aa.B = B; aa.d = a->d; aa.nh = a->nh; aa.nkv = a->nkv; aa.hd = a->hd; aa.qd = qd; aa.kd = kd;
+    aa.max_seq = a->max_seq;
+    aa.scale = 1.0f / sqrtf((float)a->hd);
+    HIP_TRY(moe::launch_attn_decode(aa, s));
     return MOE_HIP_OK;
 }
 

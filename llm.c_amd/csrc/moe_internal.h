@@ -129,13 +129,30 @@ hipError_t launch_unpack_gateup(const float *src, float *wg, float *wu, int d,
                                 int F, hipStream_t s);
 hipError_t launch_unpack_down(const float *src, float *wd, int F, int d,
                               hipStream_t s);
-// Elementwise exp_poly (which = 0) or glibc-expf (which = 1) on the device,
-// exactly as the routing kernels evaluate them.
+// The attention half of a decode step for B sequences (attention.hip).
+struct AttnArgs {
+    const float *xn;        // [B x d] normalised rows (rms_norm of x)
+    float *x;               // [B x d] residual stream, += the attention output
+    const float *wq, *wk, *wv, *wo;   // reference layout: [d x qd], [d x kd] x2, [qd x d]
+    const float *cos_t, *sin_t;       // RoPE tables [max_seq x hd/2]
+    float *kc, *vc;         // caches [B][max_seq][kd]
+    const int *pos;         // [B] position of each sequence's new token
+    float *q;               // [B x qd] workspace
+    float *o;               // [B x qd] workspace (merged head outputs)
+    float *part;            // attn_part_floats(...) workspace
+    int B, d, nh, nkv, hd, qd, kd, max_seq;
+    float scale;            // 1 / sqrt(hd)
+};
+size_t attn_part_floats(int B, int nh, int hd, int max_seq);
+hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s);
+
 // rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,
                            float *y, hipStream_t s);
 // dst[c][r] = src[r][c] for a rows x cols matrix.
 hipError_t launch_transpose(const float *src, float *dst, int rows, int cols, hipStream_t s);
+// Elementwise exp_poly (which = 0) or glibc-expf (which = 1) on the device,
+// exactly as the routing kernels evaluate them.
 hipError_t launch_eval_exp(int which, const float *x, float *y, size_t n, hipStream_t s);
 hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed,
                               uint64_t stream_id, float mean, float std,

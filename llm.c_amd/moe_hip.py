@@ -58,6 +58,12 @@ SIGNATURES = {
     "moe_hip_forward_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
     "moe_hip_route_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P, _P, _P, _P]),
     "moe_hip_rms_norm_dev": (C.c_int, [_P, _P, C.c_float, C.c_int, C.c_int, _P, _P]),
+    "moe_hip_attn_create": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.POINTER(_P)]),
+    "moe_hip_attn_destroy": (C.c_int, [_P]),
+    "moe_hip_attn_load": (C.c_int, [_P, _F, _F, _F, _F, _F]),
+    "moe_hip_attn_set_rope": (C.c_int, [_P, _F, _F]),
+    "moe_hip_attn_decode_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_float, _P]),
     "moe_hip_model_load": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
     "moe_hip_model_free": (C.c_int, [_P]),
     "moe_hip_model_config": (C.c_int, [_P, C.POINTER(ModelConfig)]),
@@ -222,6 +228,40 @@ class Layer:
                   perm=None, stream=None):
         check(lib().moe_hip_route_dev(self.h, x_ptr, T, probs, ids, gw, counts, offsets, perm,
                                       stream))
+
+
+class Attn:
+    """One block's decode attention on the device (moe_hip_attn_*)."""
+
+    def __init__(self, d, nh, nkv, hd, max_seq):
+        self.d, self.nh, self.nkv, self.hd, self.max_seq = d, nh, nkv, hd, max_seq
+        h = _P()
+        check(lib().moe_hip_attn_create(d, nh, nkv, hd, max_seq, C.byref(h)))
+        self.h = h
+
+    def load(self, wq, wk, wv, wo, rms_attn):
+        arrs = [np.ascontiguousarray(a, dtype=np.float32) for a in (wq, wk, wv, wo, rms_attn)]
+        check(lib().moe_hip_attn_load(self.h, *[fptr(a) for a in arrs]))
+
+    def set_rope(self, cos_t, sin_t):
+        c = np.ascontiguousarray(cos_t, dtype=np.float32)
+        s = np.ascontiguousarray(sin_t, dtype=np.float32)
+        check(lib().moe_hip_attn_set_rope(self.h, fptr(c), fptr(s)))
+
+    def decode_dev(self, x_ptr, B, pos_ptr, k_cache_ptr, v_cache_ptr, eps, stream=None):
+        check(lib().moe_hip_attn_decode_dev(self.h, x_ptr, B, pos_ptr, k_cache_ptr, v_cache_ptr,
+                                            eps, stream))
+
+    def close(self):
+        if self.h:
+            lib().moe_hip_attn_destroy(self.h)
+            self.h = _P()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Model:

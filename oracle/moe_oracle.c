@@ -28,6 +28,9 @@
  *   orc_rms_norm        rms_norm src/matrix.c:666-711 (AVX2+FMA build) as
  *                       the reference build compiles it, except 1/sqrt:
  *                       see the function
+ *   orc_attn_decode     the attention half of inference_step
+ *                       src/inference.c:252-308 (source semantics) for B
+ *                       sequences, each with its own K/V cache and position
  *
  * Numerics: compile with -ffp-contract=off; every fused multiply-add the
  * reference performs is an explicit fmaf()/fma() here.
@@ -435,6 +438,122 @@ void orc_rms_norm(const float *x, const float *w, float eps, int rows, int cols,
         for (int k = 0; k < cols; ++k) yr[k] = (xr[k] * inv) * w[k];
     }
     fpenv_leave(csr);
+}
+
+/* ------------------------------------------------------------------------
+ * Decode attention (src/inference.c:252-308, source semantics) for sequence
+ * b of B, in place on x[b] [d]; its caches K, V [max_seq x kd] get row pos.
+ *   xn = rmsnorm_vec (:209-215): sequential sum of squares (FMA),
+ *        inv = 1 / sqrtf(ss / d + eps), y = x * inv * w;
+ *   q, k, v = matvec (:174-182): per output one FMA chain over the input
+ *        index, ascending, inputs equal to zero skipped;
+ *   RoPE at pos (:187-203) on q (nh heads) and k (nkv heads), tables given;
+ *   K[pos] = k, V[pos] = v;
+ *   head h (kv head h / gqa): s_j = vec_dot(q_h, K[j]) * scale, j <= pos
+ *        (:133-155: lanes l < 8 of two 8-wide FMA accumulators over 16-blocks,
+ *        added lane-wise, an 8-block, hsum256 fold, FMA tail);
+ *        softmax_vec (:218-225): max, expf(s - max), sequential sum,
+ *        times 1/sum; o_h = axpy over j ascending (FMA);
+ *   x += matvec(W_O, o) element by element.
+ * The reference's GCC build auto-vectorises rmsnorm_vec's loop for the
+ * build machine, so its summation order is not fixed by the source.
+ * ---------------------------------------------------------------------- */
+static void matvec_chain(const float *mat, const float *vec, float *out, int M, int N) {
+    for (int n = 0; n < N; ++n) out[n] = 0.0f;
+    for (int i = 0; i < M; ++i) {
+        const float vi = vec[i];
+        if (vi == 0.0f) continue;
+        for (int n = 0; n < N; ++n) out[n] = fmaf(vi, mat[(size_t)i * N + n], out[n]);
+    }
+}
+
+static float dot_avx2(const float *a, const float *b, int n) {
+    float v0[8] = {0, 0, 0, 0, 0, 0, 0, 0}, v1[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 16 <= n; i += 16)
+        for (int l = 0; l < 8; ++l) {
+            v0[l] = fmaf(a[i + l], b[i + l], v0[l]);
+            v1[l] = fmaf(a[i + 8 + l], b[i + 8 + l], v1[l]);
+        }
+    for (int l = 0; l < 8; ++l) v0[l] = v0[l] + v1[l];
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; ++l) v0[l] = fmaf(a[i + l], b[i + l], v0[l]);
+    float r = ((v0[0] + v0[4]) + (v0[1] + v0[5])) + ((v0[2] + v0[6]) + (v0[3] + v0[7]));
+    for (; i < n; ++i) r = fmaf(a[i], b[i], r);
+    return r;
+}
+
+static void rope_pos(float *v, const float *cos_row, const float *sin_row, int heads, int hd) {
+    const int half = hd / 2;
+    for (int h = 0; h < heads; ++h) {
+        float *w = v + (size_t)h * hd;
+        for (int i = 0; i < half; ++i) {
+            const float a = w[2 * i], b = w[2 * i + 1];
+            w[2 * i] = a * cos_row[i] - b * sin_row[i];
+            w[2 * i + 1] = a * sin_row[i] + b * cos_row[i];
+        }
+    }
+}
+
+void orc_attn_decode(float *x, int B, int d, int nh, int nkv, int hd, const float *rms_w,
+                     float eps, const float *wq, const float *wk, const float *wv,
+                     const float *wo, const float *cos_t, const float *sin_t, float *kc,
+                     float *vc, int max_seq, const int *pos) {
+    unsigned int csr = fpenv_enter();
+    const int qd = nh * hd, kd = nkv * hd, gqa = nh / nkv, half = hd / 2;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float *xn = malloc(sizeof(float) * d), *q = malloc(sizeof(float) * qd);
+    float *kk = malloc(sizeof(float) * kd), *vv = malloc(sizeof(float) * kd);
+    float *ho = malloc(sizeof(float) * qd), *ao = malloc(sizeof(float) * d);
+    float *att = malloc(sizeof(float) * max_seq);
+    for (int b = 0; b < B; ++b) {
+        float *xb = x + (size_t)b * d;
+        float *K = kc + (size_t)b * max_seq * kd, *V = vc + (size_t)b * max_seq * kd;
+        const int p = pos[b];
+        float ss = 0.0f;
+        for (int i = 0; i < d; ++i) ss = fmaf(xb[i], xb[i], ss);
+        const float inv = 1.0f / sqrtf(ss / (float)d + eps);
+        for (int i = 0; i < d; ++i) xn[i] = xb[i] * inv * rms_w[i];
+        matvec_chain(wq, xn, q, d, qd);
+        matvec_chain(wk, xn, kk, d, kd);
+        matvec_chain(wv, xn, vv, d, kd);
+        rope_pos(q, cos_t + (size_t)p * half, sin_t + (size_t)p * half, nh, hd);
+        rope_pos(kk, cos_t + (size_t)p * half, sin_t + (size_t)p * half, nkv, hd);
+        memcpy(K + (size_t)p * kd, kk, sizeof(float) * kd);
+        memcpy(V + (size_t)p * kd, vv, sizeof(float) * kd);
+        for (int i = 0; i < qd; ++i) ho[i] = 0.0f;
+        for (int h = 0; h < nh; ++h) {
+            const int kvh = h / gqa;
+            for (int j = 0; j <= p; ++j)
+                att[j] = dot_avx2(q + (size_t)h * hd, K + (size_t)j * kd + kvh * hd, hd) * scale;
+            float vmax = att[0];
+            for (int j = 1; j <= p; ++j) if (att[j] > vmax) vmax = att[j];
+            float sum = 0.0f;
+            for (int j = 0; j <= p; ++j) { att[j] = expf(att[j] - vmax); sum = sum + att[j]; }
+            const float rs = 1.0f / sum;
+            for (int j = 0; j <= p; ++j) att[j] = att[j] * rs;
+            float *oh = ho + (size_t)h * hd;
+            for (int j = 0; j <= p; ++j)
+                for (int t = 0; t < hd; ++t)
+                    oh[t] = fmaf(att[j], V[(size_t)j * kd + kvh * hd + t], oh[t]);
+        }
+        matvec_chain(wo, ho, ao, qd, d);
+        for (int i = 0; i < d; ++i) xb[i] = xb[i] + ao[i];
+    }
+    free(xn); free(q); free(kk); free(vv); free(ho); free(ao); free(att);
+    fpenv_leave(csr);
+}
+
+/* RoPE tables as rope_buffer_init builds them (src/attention.c:151-167):
+ * angle = pos / powf(theta, 2i/hd), cos and sin of it (host libm). */
+void orc_rope_tables(int max_seq, int hd, float theta, float *cos_t, float *sin_t) {
+    const int half = hd / 2;
+    for (int p = 0; p < max_seq; ++p)
+        for (int i = 0; i < half; ++i) {
+            const float angle = (float)p / powf(theta, 2.f * (float)i / (float)hd);
+            cos_t[(size_t)p * half + i] = cosf(angle);
+            sin_t[(size_t)p * half + i] = sinf(angle);
+        }
 }
 
 /* ------------------------------------------------------------------------

@@ -49,6 +49,9 @@ def orc():
         L.orc_exp_poly_array.argtypes = [_F, _F, C.c_longlong]
         L.orc_set_softmax_tail_recip.argtypes = [C.c_int]
         L.orc_rms_norm.argtypes = [_F, _F, C.c_float, C.c_int, C.c_int, _F]
+        L.orc_attn_decode.argtypes = [_F, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _F,
+                                      C.c_float, _F, _F, _F, _F, _F, _F, _F, _F, C.c_int, _I]
+        L.orc_rope_tables.argtypes = [C.c_int, C.c_int, C.c_float, _F, _F]
         L.orc_softmax_rows.argtypes = [_F, C.c_int, C.c_int]
         L.orc_topk.argtypes = [_F, C.c_int, C.c_int, C.c_int, _I, _F]
         L.orc_dispatch.argtypes = [_I, C.c_int, C.c_int, C.c_int, _I, _I, _I]
@@ -93,6 +96,31 @@ def rms_norm(x, w, eps):
     orc().orc_rms_norm(fptr(x), fptr(np.ascontiguousarray(w, np.float32)), eps, x.shape[0],
                        x.shape[1], fptr(y))
     return y
+
+
+def rope_tables(max_seq, hd, theta):
+    """cos, sin [max_seq x hd/2] as rope_buffer_init (src/attention.c:151-167)
+    computes them (host libm)."""
+    c = np.empty((max_seq, hd // 2), np.float32)
+    s = np.empty((max_seq, hd // 2), np.float32)
+    orc().orc_rope_tables(max_seq, hd, theta, fptr(c), fptr(s))
+    return c, s
+
+
+def attn_decode(x, rms_w, eps, wq, wk, wv, wo, cos_t, sin_t, kc, vc, pos, nh, nkv, hd):
+    """The attention half of inference_step (src/inference.c:252-308) for
+    rows x [B x d]; returns (x', kc', vc') (inputs untouched).  kc, vc
+    [B x max_seq x nkv*hd]; pos [B]."""
+    x = np.array(x, np.float32, copy=True, order="C")
+    kc = np.array(kc, np.float32, copy=True, order="C")
+    vc = np.array(vc, np.float32, copy=True, order="C")
+    pos = np.ascontiguousarray(pos, np.int32)
+    B, d = x.shape
+    ar = [np.ascontiguousarray(a, np.float32) for a in (rms_w, wq, wk, wv, wo, cos_t, sin_t)]
+    orc().orc_attn_decode(fptr(x), B, d, nh, nkv, hd, fptr(ar[0]), eps, fptr(ar[1]), fptr(ar[2]),
+                          fptr(ar[3]), fptr(ar[4]), fptr(ar[5]), fptr(ar[6]), fptr(kc), fptr(vc),
+                          kc.shape[1], iptr(pos))
+    return x, kc, vc
 
 
 def router_logits(x, wr, bias=None):

@@ -1,0 +1,148 @@
+"""The attention half of the KV-cache decode step (src/inference.c:252-308).
+
+CPU: the oracle restatement (orc_attn_decode) pinned by an fp64 textbook
+evaluation and by closed forms (position 0 attends only the new token, so
+W_Q and W_K drop out; RoPE at position 0 is the identity).  The compiled
+reference cannot pin it: its attention.c does not build here (an unguarded
+cblas call), so the restatement follows the source, with parity to the
+reference's build unpinned beyond these checks.
+GPU: moe_hip_attn_decode_dev against the oracle within the layer tolerance
+(chunked softmax and V sums reorder the reference's sequential ones)."""
+import numpy as np
+import pytest
+
+import moe_hip as mh
+import orc
+
+D, NH, NKV, HD = 128, 8, 2, 16
+
+
+def make_case(B, max_seq, pos, seed, d=D, nh=NH, nkv=NKV, hd=HD):
+    rng = np.random.default_rng(seed)
+    qd, kd = nh * hd, nkv * hd
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    w = dict(wq=f(d, qd) / np.sqrt(d), wk=f(d, kd) / np.sqrt(d), wv=f(d, kd) / np.sqrt(d),
+             wo=f(qd, d) / np.sqrt(qd), rms=(1.0 + 0.1 * f(d)).astype(np.float32))
+    w = {k: v.astype(np.float32) for k, v in w.items()}
+    x = f(B, d)
+    kc, vc = f(B, max_seq, kd), f(B, max_seq, kd)
+    cos_t, sin_t = orc.rope_tables(max_seq, hd, 10000.0)
+    return x, w, kc, vc, np.asarray(pos, np.int32), cos_t, sin_t
+
+
+def run_oracle(x, w, kc, vc, pos, cos_t, sin_t, nh=NH, nkv=NKV, hd=HD):
+    return orc.attn_decode(x, w["rms"], 1e-5, w["wq"], w["wk"], w["wv"], w["wo"], cos_t, sin_t,
+                           kc, vc, pos, nh, nkv, hd)
+
+
+def textbook(x, w, kc, vc, pos, cos_t, sin_t, nh=NH, nkv=NKV, hd=HD):
+    """fp64 attention step with the reference's definitions."""
+    x = x.astype(np.float64)
+    out = x.copy()
+    B, d = x.shape
+    gqa, half = nh // nkv, hd // 2
+    for b in range(B):
+        p = int(pos[b])
+        xn = x[b] / np.sqrt((x[b] ** 2).mean() + 1e-5) * w["rms"]
+        q, k, v = xn @ w["wq"], xn @ w["wk"], xn @ w["wv"]
+        def rope(t, heads):
+            t = t.reshape(heads, hd).copy()
+            c, s = cos_t[p].astype(np.float64), sin_t[p].astype(np.float64)
+            a, bb = t[:, 0::2].copy(), t[:, 1::2].copy()
+            t[:, 0::2], t[:, 1::2] = a * c - bb * s, a * s + bb * c
+            return t
+        q, k = rope(q, nh), rope(k, nkv).reshape(-1)
+        K = kc[b].astype(np.float64).copy()
+        V = vc[b].astype(np.float64).copy()
+        K[p], V[p] = k, v
+        ho = np.zeros((nh, hd))
+        for h in range(nh):
+            kv = h // gqa
+            sc = K[: p + 1, kv * hd:(kv + 1) * hd] @ q[h] / np.sqrt(hd)
+            e = np.exp(sc - sc.max())
+            ho[h] = (e / e.sum()) @ V[: p + 1, kv * hd:(kv + 1) * hd]
+        out[b] = x[b] + ho.reshape(-1) @ w["wo"]
+    return out
+
+
+def test_oracle_vs_fp64_textbook():
+    pos = [0, 1, 5, 30, 63, 17]
+    x, w, kc, vc, pos, c, s = make_case(len(pos), 64, pos, 1)
+    xo, kco, vco = run_oracle(x, w, kc, vc, pos, c, s)
+    ref = textbook(x, w, kc, vc, pos, c, s)
+    assert float(np.abs(xo - ref).max() / np.abs(ref).max()) < 2e-6
+    # Cache rows other than pos are untouched, row pos holds the new k and v.
+    for b, p in enumerate(pos):
+        keep = np.arange(64) != p
+        assert np.array_equal(kco[b, keep], kc[b, keep]) and np.array_equal(vco[b, keep], vc[b, keep])
+        assert not np.array_equal(kco[b, p], kc[b, p])
+
+
+def test_position_zero_ignores_query_and_key():
+    """At position 0 the softmax has one entry (weight 1), so the output is
+    x + W_O . repeat(v): W_Q and W_K drop out exactly."""
+    x, w, kc, vc, pos, c, s = make_case(3, 8, [0, 0, 0], 2)
+    a, _, _ = run_oracle(x, w, kc, vc, pos, c, s)
+    w2 = dict(w, wq=w["wq"] * 3.0 + 1.0, wk=-w["wk"])
+    b, _, _ = run_oracle(x, w2, kc, vc, pos, c, s)
+    assert np.array_equal(a, b)
+    # and the cache contents past row 0 do not matter
+    _, _, _ = run_oracle(x, w, kc * 0 + 7, vc * 0 - 3, pos, c, s)
+    d2, _, _ = run_oracle(x, w, kc * 0 + 7, vc * 0 - 3, pos, c, s)
+    assert np.array_equal(a, d2)
+
+
+def test_rope_table_identity_at_position_zero():
+    c, s = orc.rope_tables(16, HD, 10000.0)
+    assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
+    # angle of pair 0 is the position itself
+    assert np.allclose(c[:, 0], np.cos(np.arange(16)), atol=1e-6)
+
+
+# ---------------------------------------------------------------- GPU
+def run_device(x, w, kc, vc, pos, c, s, nh=NH, nkv=NKV, hd=HD):
+    B, d = x.shape
+    max_seq = kc.shape[1]
+    at = mh.Attn(d, nh, nkv, hd, max_seq)
+    try:
+        at.load(w["wq"], w["wk"], w["wv"], w["wo"], w["rms"])
+        at.set_rope(c, s)
+        dx, dk, dv = (mh.DeviceArray.from_host(np.ascontiguousarray(a)) for a in (x, kc, vc))
+        dp = mh.DeviceArray.from_host(np.ascontiguousarray(pos, np.int32))
+        at.decode_dev(dx.ptr, B, dp.ptr, dk.ptr, dv.ptr, 1e-5)
+        mh.synchronize()
+        return dx.to_host(), dk.to_host(), dv.to_host()
+    finally:
+        at.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(128, 8, 2, 16, 600), (512, 8, 2, 64, 1100)],
+                         ids=["small", "config4"])
+def test_attn_decode_device(shape):
+    d, nh, nkv, hd, max_seq = shape
+    pos = [0, 1, 2, 255, 256, 257, 511, 512, max_seq - 1, 100, 300, 37]
+    x, w, kc, vc, pos, c, s = make_case(len(pos), max_seq, pos, 5, d, nh, nkv, hd)
+    xg, kg, vg = run_device(x, w, kc, vc, pos, c, s, nh, nkv, hd)
+    xo, ko, vo = run_oracle(x, w, kc, vc, pos, c, s, nh, nkv, hd)
+    rel = orc.rel_l2(xg, xo)
+    mabs = float(np.abs(xg - xo).max())
+    print(f"[gpu-test] attention {shape}: rel-L2 {rel:.3e} max-abs {mabs:.3e}", flush=True)
+    assert rel <= 1e-5 and mabs <= 1e-4
+    for b, p in enumerate(pos):
+        keep = np.arange(max_seq) != p
+        assert np.array_equal(kg[b, keep], kc[b, keep]) and np.array_equal(vg[b, keep], vc[b, keep])
+        assert orc.rel_l2(kg[b, p], ko[b, p]) < 1e-5 and orc.rel_l2(vg[b, p], vo[b, p]) < 1e-5
+
+
+@pytest.mark.gpu
+def test_attn_decode_position_out_of_range():
+    """A position outside [0, max_seq) leaves that sequence untouched."""
+    x, w, kc, vc, _, c, s = make_case(3, 64, [0, 0, 0], 6)
+    pos = np.array([5, 64, -1], np.int32)
+    xg, kg, vg = run_device(x, w, kc, vc, pos, c, s)
+    for b in (1, 2):
+        assert np.array_equal(xg[b], x[b])
+        assert np.array_equal(kg[b], kc[b]) and np.array_equal(vg[b], vc[b])
+    xo, _, _ = run_oracle(x[:1], w, kc[:1], vc[:1], pos[:1], c, s)
+    assert orc.rel_l2(xg[:1], xo) < 1e-5
