@@ -10,6 +10,9 @@ Also measured in the same run:
   * decode: 64 sequences x 1 token through 8 MoE layers of d=512, d_ff=2048,
     E=16, top-2 (8 layers' weights, 1.6 GB, so the 256 MB last-level cache
     cannot hold them), reported as MoE decode tokens/s and HBM GB/s;
+  * decode_step: the whole block stack of that decode step (GQA attention
+    over a 1024-position KV cache, then the MoE FFN sublayer, per block) with
+    the residual stream on the device;
   * cpu_baseline: the CPU oracle (a restatement of the reference's
     moe_forward, bit-identical routing) on a bounded token sample of the same
     prefill workload, on this host's cores.
@@ -151,6 +154,93 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
     return res
 
 
+def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=2, F=2048,
+                E=16, k=2, eps=1e-5):
+    """The whole block stack of one KV-cache decode step, device resident:
+    per block x += Attn(rms_norm(x)) at position ctx over caches holding ctx
+    earlier positions (src/inference.c:252-308), then x += MoE(rms_norm(x))
+    (:311-343).  Caches, weights and x are synthetic N(0, 1) / N(0, 0.02)."""
+    hd = d // nh
+    kd, max_seq = nkv * hd, ctx + 1
+    rng = np.random.default_rng(7)
+    i = np.arange(hd // 2, dtype=np.float64)
+    ang = np.arange(max_seq)[:, None] / 10000.0 ** (2 * i / hd)[None, :]
+    cos_t, sin_t = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    attn, layers, caches = [], [], []
+    rms = mh.DeviceArray.from_host(np.ones(d, np.float32))
+    for li in range(n_layers):
+        a = mh.Attn(d, nh, nkv, hd, max_seq)
+        w = lambda r, c: (0.02 * rng.standard_normal((r, c))).astype(np.float32)
+        a.load(w(d, nh * hd), w(d, kd), w(d, kd), w(nh * hd, d), np.ones(d, np.float32))
+        a.set_rope(cos_t, sin_t)
+        attn.append(a)
+        L = mh.Layer(d, F, E, k)
+        L.fill_synthetic(100 + li, 0.02, 0.02)
+        layers.append(L)
+        kc, vc = mh.DeviceArray((B, max_seq, kd)), mh.DeviceArray((B, max_seq, kd))
+        mh.fill_normal_dev(kc.ptr, kc.nbytes // 4, 300 + li, 0, 0.0, 1.0)
+        mh.fill_normal_dev(vc.ptr, vc.nbytes // 4, 300 + li, 1, 0.0, 1.0)
+        caches.append((kc, vc))
+    x = mh.DeviceArray((B, d))
+    pos = mh.DeviceArray.from_host(np.full(B, ctx, np.int32))
+    mh.synchronize()
+
+    def attn_only():
+        for li in range(n_layers):
+            attn[li].decode_dev(x.ptr, B, pos.ptr, caches[li][0].ptr, caches[li][1].ptr, eps)
+
+    def step():
+        for li in range(n_layers):
+            attn[li].decode_dev(x.ptr, B, pos.ptr, caches[li][0].ptr, caches[li][1].ptr, eps)
+            layers[li].ffn_sublayer_dev(x.ptr, rms.ptr, eps, B)
+
+    def timed(fn):
+        # Steps issued back to back on the library stream, device time between
+        # two events on it; the residual updates are small enough that x stays
+        # near N(0, 1) over the run.
+        for _ in range(max(warmup, 1)):
+            fn()
+        mh.synchronize()
+        mh.timer_start()
+        for _ in range(steps):
+            fn()
+        return mh.timer_stop() / steps
+
+    mh.fill_normal_dev(x.ptr, B * d, 99, 2, 0.0, 1.0)
+    step_ms = timed(step)
+    attn_ms = timed(attn_only)
+    # The attention's other launch arrangement (informational).
+    mh.set_attn_path(0 if mh.attn_path() else 1)
+    attn_alt_ms = timed(attn_only)
+    mh.set_attn_path(0 if mh.attn_path() else 1)
+    # The same step replayed from a captured HIP graph (informational).
+    with mh.Graph() as graph:
+        step()
+    graph.launch()
+    mh.synchronize()
+    mh.timer_start()
+    for _ in range(steps):
+        graph.launch()
+    graph_ms = mh.timer_stop() / steps
+    graph.close()
+    # Algorithmic bytes of one block's attention: K and V rows 0..ctx of each
+    # sequence read once (the new row written once), plus W_Q, W_K, W_V, W_O.
+    kv_bytes = 4.0 * 2 * B * (ctx + 1) * kd
+    w_bytes = 4.0 * (2 * d * nh * hd + 2 * d * kd)
+    attn_layer = attn_ms / n_layers
+    res = dict(layers=n_layers, B=B, ctx=ctx, d=d, nh=nh, nkv=nkv, hd=hd, F=F, E=E, k=k,
+               ms_per_step=step_ms, tokens_per_s=B / (step_ms * 1e-3),
+               graph_ms_per_step=graph_ms, graph_tokens_per_s=B / (graph_ms * 1e-3),
+               attn_ms_per_layer=attn_layer,
+               attn_path="one launch" if mh.attn_path() else "launches",
+               attn_other_path_ms_per_layer=attn_alt_ms / n_layers,
+               attn_gbs=(kv_bytes + w_bytes) / (attn_layer * 1e-3) / 1e9,
+               moe_ms_per_layer=(step_ms - attn_ms) / n_layers)
+    for o in attn + layers:
+        o.close()
+    return res
+
+
 def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, budget_s=15.0):
     """Oracle moe_forward on the first tokens of the prefill workload, all
     host cores, until ~budget_s of CPU work; tokens/s extrapolates linearly
@@ -185,7 +275,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "decode_step", "copy"], default=None,
                     help="run one section only (for profiling); prints its JSON to stderr")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -208,15 +298,20 @@ def main():
     if args.only == "decode":
         log("decode", json.dumps(decode(mh, args.steps, args.warmup)))
         return
+    if args.only == "decode_step":
+        log("decode_step", json.dumps(decode_step(mh, args.steps, args.warmup)))
+        return
     pre, st = prefill(mh, args.steps, args.warmup)
     if args.only == "prefill":
         log("prefill", json.dumps(pre))
         return
     log("prefill", json.dumps(pre))
-    dec = None
+    dec = stp = None
     if not args.no_decode:
         dec = decode(mh, args.steps, args.warmup)
         log("decode", json.dumps(dec))
+        stp = decode_step(mh, args.steps, args.warmup)
+        log("decode_step", json.dumps(stp))
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(mh, st)
@@ -266,6 +361,16 @@ def main():
             "experts_gbs": dec["experts_gbs"],
             # (per-phase HIP events add a few microseconds to each phase)
             "phase_ms_per_layer": dec["phase_ms"],
+        }
+    if stp:
+        line["decode_step"] = {
+            "workload": "64 seqs x 1 token at context 1024, 8 blocks of GQA 8/2 attention "
+                        "(hd 64) + MoE E=16 top-2, d=512 d_ff=2048, device-resident x",
+            "tokens_per_s": stp["tokens_per_s"], "ms_per_step": stp["ms_per_step"],
+            "graph_ms_per_step": stp["graph_ms_per_step"],
+            "attn_ms_per_layer": stp["attn_ms_per_layer"], "attn_gbs": stp["attn_gbs"],
+            "attn_hbm_frac": stp["attn_gbs"] / PEAK_HBM_GBS,
+            "moe_ms_per_layer": stp["moe_ms_per_layer"],
         }
     print(json.dumps(line), flush=True)
 

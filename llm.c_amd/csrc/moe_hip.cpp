@@ -101,11 +101,11 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, stage,
-        counters, xn, rmsw, aq, ao, apart;
+        counters, xn, rmsw, aq, ao, apart, agpart, ass, acnt;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
                          &tile_expert, &perm, &h, &ys, &stage, &counters, &xn, &rmsw,
-                         &aq, &ao, &apart};
+                         &aq, &ao, &apart, &agpart, &ass, &acnt};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -344,6 +344,19 @@ int moe_hip_layer_load(MoeHipLayer *L, const MoEWeights *w) {
 // ---------------------------------------------------------------------------
 // Attention of the decode step (src/inference.c:252-308): weights in the
 // reference layout, the block's rms_attn scale and the RoPE tables.
+// Decode attention as one launch where the head shape allows (1), or as
+// separate launches (0, the default: measured faster at the 64-sequence,
+// 1024-context decode step, where the one launch cannot keep every chunk
+// resident while the projections run).
+static int g_attn_fused = 0;
+
+int moe_hip_set_attn_path(int fused) {
+    g_attn_fused = fused ? 1 : 0;
+    return MOE_HIP_OK;
+}
+
+int moe_hip_get_attn_path(void) { return g_attn_fused; }
+
 struct MoeHipAttn {
     int d = 0, nh = 0, nkv = 0, hd = 0, max_seq = 0;
     float *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
@@ -413,21 +426,39 @@ int moe_hip_attn_decode_dev(MoeHipAttn *a, float *x, int B, const int *pos, floa
     if (B == 0) return MOE_HIP_OK;
     TRY(ensure_init());
     const int qd = a->nh * a->hd, kd = a->nkv * a->hd;
-    TRY(g_ws.xn.reserve(sizeof(float) * (size_t)B * a->d));
     TRY(g_ws.aq.reserve(sizeof(float) * (size_t)B * qd));
     TRY(g_ws.ao.reserve(sizeof(float) * (size_t)B * qd));
     TRY(g_ws.apart.reserve(sizeof(float) * moe::attn_part_floats(B, a->nh, a->hd, a->max_seq)));
+    TRY(g_ws.agpart.reserve(sizeof(float) * moe::attn_gpart_floats(B, a->d, qd, kd)));
+    TRY(g_ws.ass.reserve(sizeof(float) * moe::attn_sspart_floats(B, a->d)));
+    // Tile and merge counters, then the one-launch sublayer's three: zero
+    // when allocated, reset by the last workgroup of each launch that uses them.
+    const moe::AttnCounters nc = moe::attn_counters(B, a->d, qd, kd, a->nkv);
+    const size_t cnt_bytes =
+        sizeof(int) * (size_t)(moe::attn_sync_ints() + nc.qkv + nc.wo + nc.merge);
+    if (g_ws.acnt.bytes < cnt_bytes) {
+        TRY(g_ws.acnt.reserve(cnt_bytes));
+        HIP_TRY(hipMemsetAsync(g_ws.acnt.p, 0, g_ws.acnt.bytes, g_stream));
+        HIP_TRY(hipStreamSynchronize(g_stream));
+    }
+    TRY(ensure_counters());
+    const bool fused = g_attn_fused && moe::attn_fused_supported(a->hd, a->nh, a->nkv);
     hipStream_t s = pick_stream(stream);
-    HIP_TRY(moe::launch_rms_norm(x, a->rms, eps, B, a->d, g_ws.xn.as<float>(), s));
     moe::AttnArgs aa{};
-    aa.xn = g_ws.xn.as<float>(); aa.x = x;
+    aa.x = x; aa.rms_w = a->rms; aa.eps = eps;
     aa.wq = a->wq; aa.wk = a->wk; aa.wv = a->wv; aa.wo = a->wo;
     aa.cos_t = a->cos_t; aa.sin_t = a->sin_t; aa.kc = k_cache; aa.vc = v_cache; aa.pos = pos;
     aa.q = g_ws.aq.as<float>(); aa.o = g_ws.ao.as<float>(); aa.part = g_ws.apart.as<float>();
+    aa.gpart = g_ws.agpart.as<float>(); aa.sspart = g_ws.ass.as<float>();
+    aa.sync = g_ws.acnt.as<int>();   // (first: 128-byte aligned flag lines)
+    aa.cnt_qkv = aa.sync + moe::attn_sync_ints(); aa.cnt_wo = aa.cnt_qkv + nc.qkv;
+    aa.cnt_merge = aa.cnt_wo + nc.wo;
+    aa.err = g_ws.counters.as<int>() + kLayerErr;
+    aa.nqkv_tiles = nc.qkv;
     aa.B = B; aa.d = a->d; aa.nh = a->nh; aa.nkv = a->nkv; aa.hd = a->hd; aa.qd = qd; aa.kd = kd;
     aa.max_seq = a->max_seq;
     aa.scale = 1.0f / sqrtf((float)a->hd);
-    HIP_TRY(moe::launch_attn_decode(aa, s));
+    HIP_TRY(moe::launch_attn_decode(aa, fused, s));
     return MOE_HIP_OK;
 }
 

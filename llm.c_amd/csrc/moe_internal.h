@@ -131,20 +131,39 @@ hipError_t launch_unpack_down(const float *src, float *wd, int F, int d,
                               hipStream_t s);
 // The attention half of a decode step for B sequences (attention.hip).
 struct AttnArgs {
-    const float *xn;        // [B x d] normalised rows (rms_norm of x)
-    float *x;               // [B x d] residual stream, += the attention output
+    float *x;               // [B x d] residual stream: x += Attn(rms_norm(x))
+    const float *rms_w;     // [d] rms_attn
+    float eps;
     const float *wq, *wk, *wv, *wo;   // reference layout: [d x qd], [d x kd] x2, [qd x d]
     const float *cos_t, *sin_t;       // RoPE tables [max_seq x hd/2]
     float *kc, *vc;         // caches [B][max_seq][kd]
     const int *pos;         // [B] position of each sequence's new token
     float *q;               // [B x qd] workspace
     float *o;               // [B x qd] workspace (merged head outputs)
-    float *part;            // attn_part_floats(...) workspace
+    float *part;            // attn_part_floats(...) workspace: chunk partials
+    float *gpart;           // attn_gpart_floats(...) workspace: projection slices
+    float *sspart;          // attn_sspart_floats(...) workspace: slice sums of x^2
+    int *cnt_qkv, *cnt_wo, *cnt_merge;   // attn_counters(...) device ints, zero between launches
+    // One-launch sublayer: attn_sync_ints() device ints, zero between
+    // launches (counts and readiness flags); err raised if a bounded wait
+    // gave up; nqkv_tiles = the QKV tile count.
+    int *sync;
+    int *err;
+    int nqkv_tiles;
     int B, d, nh, nkv, hd, qd, kd, max_seq;
     float scale;            // 1 / sqrt(hd)
 };
+struct AttnCounters {
+    int qkv, wo, merge;
+};
 size_t attn_part_floats(int B, int nh, int hd, int max_seq);
-hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s);
+size_t attn_gpart_floats(int B, int d, int qd, int kd);
+size_t attn_sspart_floats(int B, int d);
+AttnCounters attn_counters(int B, int d, int qd, int kd, int nkv);
+int attn_sync_ints();
+// Head shapes for which the one-launch sublayer exists.
+bool attn_fused_supported(int hd, int nh, int nkv);
+hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s);
 
 // rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,

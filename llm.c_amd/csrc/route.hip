@@ -419,15 +419,44 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float *src, float 
 // ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)), the scalar tail as FMAs, and
 // inv_rms = 1 / sqrt(fma(ss, 1/cols, eps)) correctly rounded (the reference
 // build estimates it with RSQRTSS and one Newton-Raphson step).
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const float *w, float eps,
-                                                       int rows, int cols, float rcp_cols,
-                                                       float *y) {
+// NB > 0: cols == 16 * NB; sixteen lanes per row, lane l holding the
+// reference accumulator lane l (columns 16b + l) in registers, all its loads
+// in flight at once; four rows per 64-thread workgroup.  The lanes are then
+// folded in the same association: v_l = acc_l + acc_(l+8), s_i = v_i +
+// v_(i+4), ((s_0 + s_1) + (s_2 + s_3)).  NB == 0: any cols, four lanes per
+// row as described above, loads unrolled eight column blocks at a time.
+template <int NB>
+__global__ __launch_bounds__(NB > 0 ? 64 : 256) void rms_norm_kernel(
+    const float *x, const float *w, float eps, int rows, int cols, float rcp_cols, float *y) {
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (NB > 0) {
+        const int l = threadIdx.x & 15;
+        const int row = blockIdx.x * 4 + (threadIdx.x >> 4);
+        const bool live = row < rows;
+        const float *xr = x + (size_t)(live ? row : 0) * cols;
+        float v[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) v[b] = xr[16 * b + l];
+        float acc = 0.0f;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc = fmaf(v[b], v[b], acc);
+        acc = acc + __shfl_down(acc, 8, 16);
+        acc = acc + __shfl_down(acc, 4, 16);
+        acc = acc + __shfl_down(acc, 1, 16);
+        acc = acc + __shfl_down(acc, 2, 16);
+        const float inv = __shfl(1.0f / sqrtf(fmaf(acc, rcp_cols, eps)), 0, 16);
+        if (!live) return;
+        float *yr = y + (size_t)row * cols;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) yr[16 * b + l] = (v[b] * inv) * w[16 * b + l];
+        return;
+    }
     const int q = threadIdx.x & 3;
     const int row = blockIdx.x * 64 + (threadIdx.x >> 2);
     const bool live = row < rows;
     const float *xr = x + (size_t)(live ? row : 0) * cols;
-    float a[4] = {0.f, 0.f, 0.f, 0.f};
     const int nb = cols / 16;
+#pragma unroll 8
     for (int b = 0; b < nb; ++b)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -455,6 +484,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *x, const flo
     const float inv = __shfl(1.0f / sqrtf(fmaf(ss, rcp_cols, eps)), 0, 4);
     if (!live) return;
     float *yr = y + (size_t)row * cols;
+#pragma unroll 4
     for (int c = 4 * q; c < cols; c += 16)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -479,8 +509,15 @@ hipError_t launch_transpose(const float *src, float *dst, int rows, int cols, hi
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,
                            float *y, hipStream_t s) {
     if (rows <= 0 || cols <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(256), 0, s, x, w,
-                       eps, rows, cols, 1.0f / (float)cols, y);
+    const float rc = 1.0f / (float)cols;
+    const dim3 g4((unsigned)((rows + 3) / 4)), g64((unsigned)((rows + 63) / 64));
+    switch (cols) {
+    case 128:  hipLaunchKernelGGL(rms_norm_kernel<8>, g4, dim3(64), 0, s, x, w, eps, rows, cols, rc, y); break;
+    case 256:  hipLaunchKernelGGL(rms_norm_kernel<16>, g4, dim3(64), 0, s, x, w, eps, rows, cols, rc, y); break;
+    case 512:  hipLaunchKernelGGL(rms_norm_kernel<32>, g4, dim3(64), 0, s, x, w, eps, rows, cols, rc, y); break;
+    case 1024: hipLaunchKernelGGL(rms_norm_kernel<64>, g4, dim3(64), 0, s, x, w, eps, rows, cols, rc, y); break;
+    default:   hipLaunchKernelGGL(rms_norm_kernel<0>, g64, dim3(256), 0, s, x, w, eps, rows, cols, rc, y);
+    }
     return hipGetLastError();
 }
 

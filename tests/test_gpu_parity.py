@@ -301,7 +301,7 @@ def test_decode_batch_c4():
 
 
 # --------------------------------------------------------------------- rms_norm + FFN sublayer
-@pytest.mark.parametrize("cols", [128, 256, 512, 2048, 24, 8, 100, 7])
+@pytest.mark.parametrize("cols", [128, 256, 512, 1024, 2048, 24, 8, 100, 7, 16, 48])
 def test_rms_norm_device_bitexact(cols):
     """Device rms_norm against the oracle, bit for bit: the reference's
     accumulator lanes and fold, fused multiply-adds, a correctly rounded
