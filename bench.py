@@ -156,10 +156,11 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
 
 def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=2, F=2048,
                 E=16, k=2, eps=1e-5):
-    """The whole block stack of one KV-cache decode step, device resident:
-    per block x += Attn(rms_norm(x)) at position ctx over caches holding ctx
-    earlier positions (src/inference.c:252-308), then x += MoE(rms_norm(x))
-    (:311-343).  Caches, weights and x are synthetic N(0, 1) / N(0, 0.02)."""
+    """The whole block stack of one KV-cache decode step, device resident,
+    one moe_hip_decode_block_dev per block: x += Attn(rms_norm(x)) at
+    position ctx over caches holding ctx earlier positions
+    (src/inference.c:252-308), then x += MoE(rms_norm(x)) (:311-343).
+    Caches, weights and x are synthetic N(0, 1) / N(0, 0.02)."""
     hd = d // nh
     kd, max_seq = nkv * hd, ctx + 1
     rng = np.random.default_rng(7)
@@ -191,8 +192,8 @@ def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=
 
     def step():
         for li in range(n_layers):
-            attn[li].decode_dev(x.ptr, B, pos.ptr, caches[li][0].ptr, caches[li][1].ptr, eps)
-            layers[li].ffn_sublayer_dev(x.ptr, rms.ptr, eps, B)
+            attn[li].decode_block_dev(layers[li], rms.ptr, x.ptr, B, pos.ptr, caches[li][0].ptr,
+                                      caches[li][1].ptr, eps)
 
     def timed(fn):
         # Steps issued back to back on the library stream, device time between

@@ -243,6 +243,21 @@ int moe_hip_attn_set_rope(MoeHipAttn *attn, const float *cos_table, const float 
 int moe_hip_attn_decode_dev(MoeHipAttn *attn, float *x, int B, const int *pos, float *k_cache,
                             float *v_cache, float eps, void *stream);
 
+/* One decoder block of the KV-cache decode step for B sequences
+ * (src/inference.c:245-345), on device rows x [B x d] in place:
+ * x += Attn(rms_norm(x; rms_attn)) as moe_hip_attn_decode_dev, then
+ * x += MoE(rms_norm(x; rms_ffn, eps)) as moe_hip_ffn_sublayer_dev with the
+ * layer (same d_model).  The FFN half applies to every row (a pos[b] out
+ * of range skips only the attention half).  rms_ffn: device [d]; x_norm
+ * [B x d] receives the FFN's normalised rows, bit-identical to
+ * moe_hip_rms_norm_dev of the updated x (NULL: library workspace); ids
+ * [B x top_k] the expert ids (may be NULL).  The MoE router normalises
+ * the rows itself as its first step (a separate rms_norm launch where it
+ * cannot). */
+int moe_hip_decode_block_dev(MoeHipAttn *attn, MoeHipLayer *layer, const float *rms_ffn, float *x,
+                             int B, const int *pos, float *k_cache, float *v_cache, float eps,
+                             float *x_norm, int *ids, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Checkpoints: the MoE blocks of a file written by model_save
  * (src/transformer.c:573-616, read back by model_load :624-700) straight into
@@ -287,6 +302,7 @@ int moe_hip_set_router_path(int mode);
  * same values.  get returns the current setting. */
 int moe_hip_set_attn_path(int fused);
 int moe_hip_get_attn_path(void);
+
 
 /* Waits for the library stream and reports whether a bounded device-side
  * wait of the one-launch decode layer or decode attention gave up since the

@@ -334,6 +334,142 @@ __device__ void proj_tile(const AttnArgs &a, int tx, int ty, int z, int ntx, int
     if (FUSED && QKV) signal(a.sync, a.nqkv_tiles, a.sync + kSyncQkvFlags);   // q, k, v are out
 }
 
+// Projection tiles without a split reduction: one 1024-thread workgroup per
+// 16 x 16 output tile (tile column blockIdx.x, row blockIdx.y).  The X rows
+// and W columns of a 512-long reduction chunk are staged in LDS: thread t
+// loads float4 t % 128 of X rows t / 128 and 8 + t / 128, and float4s t and
+// t + 1024 of the W block.  Wave w takes chunk rows 32w .. 32w + 31, lane
+// (rr, cq) = (lane / 4, lane % 4) row rr and columns 4cq .. 4cq + 3; the
+// sixteen waves' sums are added through LDS in wave order.  QKV: row r's
+// sum of x^2 is each thread's k-ordered share, summed over its wave and
+// then over the row's two waves; the epilogue (1/rms, RoPE, q and the cache
+// rows) as in proj_tile.  WO: x += the products.  One global round trip.
+constexpr int kPT = 16, kPK = 512;
+struct Proj16Smem {
+    union {
+        struct {
+            float4 xs[kPT][kPK / 4 + 1];
+            float4 ws[kPK][kPT / 4];
+        };
+        float4 red[16][kPT][kPT / 4];
+    };
+    float ssw[2][16];
+};
+
+template <bool QKV>
+__global__ __launch_bounds__(1024) void proj16_kernel(AttnArgs a) {
+    __shared__ Proj16Smem sm;
+    const int M = QKV ? a.d : a.qd, N = QKV ? a.qd + 2 * a.kd : a.d;
+    const float *X = QKV ? a.x : a.o;
+    const int r0 = blockIdx.y * kPT, c0 = blockIdx.x * kPT;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+    // Epilogue threads (tid < 64: row tid / 4, columns 4 (tid % 4) ..) fetch
+    // what they need besides the products up front.
+    const int orow = r0 + (tid >> 2), ocol = c0 + 4 * (tid & 3);
+    const bool owned = tid < 64 && orow < a.B && ocol < N;
+    const int p = owned ? a.pos[orow] : -1;
+    const bool live = owned && p >= 0 && p < a.max_seq;
+    const int col = ocol < a.qd ? ocol : ocol < a.qd + a.kd ? ocol - a.qd : ocol - a.qd - a.kd;
+    const bool rope = QKV && live && ocol < a.qd + a.kd;
+    float4 cs = zero, xo = zero;
+    if (rope) {
+        const int half = a.hd / 2, i0 = (col % a.hd) / 2;
+        const float *cr = a.cos_t + (size_t)p * half + i0, *sr = a.sin_t + (size_t)p * half + i0;
+        cs = make_float4(cr[0], sr[0], cr[1], sr[1]);
+    }
+    if (!QKV && live) xo = *reinterpret_cast<const float4 *>(a.x + (size_t)orow * a.d + ocol);
+
+    const int rr = lane >> 2, cq = lane & 3;
+    const int xq = tid % (kPK / 4), xr0 = tid / (kPK / 4);   // X float4 and first row
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ss[2] = {0.0f, 0.0f};
+    for (int k0 = 0; k0 < M; k0 += kPK) {
+        const int k = k0 + 4 * xq;
+        float4 xv[2], wv[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = r0 + xr0 + 8 * i;
+            xv[i] = row < a.B && k < M ? *reinterpret_cast<const float4 *>(X + (size_t)row * M + k)
+                                       : zero;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 1024 * i, kk = k0 + idx / (kPT / 4), cc = c0 + 4 * (idx % (kPT / 4));
+            const float *src = nullptr;
+            if (kk < M && cc < N) {
+                if (!QKV)                    src = a.wo + (size_t)kk * a.d + cc;
+                else if (cc < a.qd)          src = a.wq + (size_t)kk * a.qd + cc;
+                else if (cc < a.qd + a.kd)   src = a.wk + (size_t)kk * a.kd + (cc - a.qd);
+                else                         src = a.wv + (size_t)kk * a.kd + (cc - a.qd - a.kd);
+            }
+            wv[i] = src ? *reinterpret_cast<const float4 *>(src) : zero;
+        }
+        float4 wr = zero;
+        if (QKV && k < M) wr = *reinterpret_cast<const float4 *>(a.rms_w + k);
+        if (k0 > 0) __syncthreads();   // the previous chunk's products are done
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float4 v = xv[i];
+            if (QKV) {
+                ss[i] = fmaf(v.x, v.x, ss[i]); ss[i] = fmaf(v.y, v.y, ss[i]);
+                ss[i] = fmaf(v.z, v.z, ss[i]); ss[i] = fmaf(v.w, v.w, ss[i]);
+                v = make_float4(v.x * wr.x, v.y * wr.y, v.z * wr.z, v.w * wr.w);
+            }
+            sm.xs[xr0 + 8 * i][xq] = v;
+            const int idx = tid + 1024 * i;
+            sm.ws[idx / (kPT / 4)][idx % (kPT / 4)] = wv[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int kq = wave * 8 + s;
+            const float4 xa = sm.xs[rr][kq];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 wb = sm.ws[4 * kq + j][cq];
+                const float xj = comp(xa, j);
+                acc[0] = fmaf(xj, wb.x, acc[0]);
+                acc[1] = fmaf(xj, wb.y, acc[1]);
+                acc[2] = fmaf(xj, wb.z, acc[2]);
+                acc[3] = fmaf(xj, wb.w, acc[3]);
+            }
+        }
+    }
+    if (QKV) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            for (int off = 32; off >= 1; off >>= 1) ss[i] += __shfl_xor(ss[i], off);
+        if (lane == 0) {
+            sm.ssw[0][wave] = ss[0];   // row wave / 2
+            sm.ssw[1][wave] = ss[1];   // row 8 + wave / 2
+        }
+    }
+    __syncthreads();   // (red overlays xs and ws)
+    sm.red[wave][rr][cq] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    __syncthreads();
+    if (!live) return;
+    float4 y = zero;
+    for (int w = 0; w < 16; ++w) y = add4(y, sm.red[w][tid >> 2][tid & 3]);
+    if (!QKV) {
+        *reinterpret_cast<float4 *>(a.x + (size_t)orow * a.d + ocol) = add4(xo, y);
+        return;
+    }
+    const int r = tid >> 2, h = r >> 3, rw = 2 * (r & 7);
+    const float sq = sm.ssw[h][rw] + sm.ssw[h][rw + 1];
+    const float inv = 1.0f / sqrtf(sq / (float)M + a.eps);
+    y = make_float4(y.x * inv, y.y * inv, y.z * inv, y.w * inv);
+    if (rope) {
+        rope_pair(y.x, y.y, cs.x, cs.y);
+        rope_pair(y.z, y.w, cs.z, cs.w);
+    }
+    float *dst = ocol < a.qd ? a.q + (size_t)orow * a.qd
+                             : (ocol < a.qd + a.kd ? a.kc : a.vc) +
+                                   ((size_t)orow * a.max_seq + p) * a.kd;
+    *reinterpret_cast<float4 *>(dst + col) = y;
+}
+
 // Merged output of one head at dimension dim from its chunk partials at
 // float index ph + c * (hd + 2) = (m_c, l_c, o_c[hd]), c < nc:
 // o = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c with M = max_c m_c,
@@ -774,9 +910,8 @@ hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s) {
         if (!ok) return hipErrorInvalidValue;
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(proj_tile_kernel<true>,
-                       dim3((unsigned)tiles(N), (unsigned)tiles(a.B), (unsigned)slices(a.d)),
-                       dim3(256), 0, s, a);
+    auto t16 = [](int n) { return (unsigned)((n + kPT - 1) / kPT); };
+    hipLaunchKernelGGL(proj16_kernel<true>, dim3(t16(N), t16(a.B)), dim3(1024), 0, s, a);
     const bool fast = with_fast_shape(a.hd, gqa, [&](auto hd, auto g) {
         hipLaunchKernelGGL((attn_chunk_fast_kernel<decltype(hd)::value, decltype(g)::value>),
                            dim3((unsigned)nc), dim3(256), 0, s, a);
@@ -786,9 +921,7 @@ hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s) {
         hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((a.B * a.qd + 255) / 256)),
                            dim3(256), 0, s, a);
     }
-    hipLaunchKernelGGL(proj_tile_kernel<false>,
-                       dim3((unsigned)tiles(a.d), (unsigned)tiles(a.B), (unsigned)slices(a.qd)),
-                       dim3(256), 0, s, a);
+    hipLaunchKernelGGL(proj16_kernel<false>, dim3(t16(a.d), t16(a.B)), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 

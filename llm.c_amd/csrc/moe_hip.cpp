@@ -127,6 +127,13 @@ int ensure_counters() {
     return MOE_HIP_OK;
 }
 
+// Norm: with x_raw set, the rows to route (x, written here) are first
+// rms_norm(x_raw; rms_w, eps), by the router where it can.
+struct Norm {
+    const float *x_raw = nullptr, *rms_w = nullptr;
+    float eps = 0.0f;
+};
+
 // Residency cache for the drop-in entry points.
 struct Resident {
     MoeHipLayer *layer = nullptr;
@@ -341,6 +348,9 @@ int moe_hip_layer_load(MoeHipLayer *L, const MoEWeights *w) {
     return MOE_HIP_OK;
 }
 
+static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
+                        int accumulate, void *stream, Norm nm);
+
 // ---------------------------------------------------------------------------
 // Attention of the decode step (src/inference.c:252-308): weights in the
 // reference layout, the block's rms_attn scale and the RoPE tables.
@@ -356,6 +366,7 @@ int moe_hip_set_attn_path(int fused) {
 }
 
 int moe_hip_get_attn_path(void) { return g_attn_fused; }
+
 
 struct MoeHipAttn {
     int d = 0, nh = 0, nkv = 0, hd = 0, max_seq = 0;
@@ -419,8 +430,9 @@ int moe_hip_attn_set_rope(MoeHipAttn *a, const float *cos_table, const float *si
     return MOE_HIP_OK;
 }
 
-int moe_hip_attn_decode_dev(MoeHipAttn *a, float *x, int B, const int *pos, float *k_cache,
-                            float *v_cache, float eps, void *stream) {
+// The attention sublayer.
+static int attn_decode(MoeHipAttn *a, float *x, int B, const int *pos, float *k_cache,
+                       float *v_cache, float eps, void *stream) {
     if (!a || B < 0 || (B > 0 && (!x || !pos || !k_cache || !v_cache)))
         return set_err(MOE_HIP_ERR_ARG, "bad attention arguments");
     if (B == 0) return MOE_HIP_OK;
@@ -460,6 +472,30 @@ int moe_hip_attn_decode_dev(MoeHipAttn *a, float *x, int B, const int *pos, floa
     aa.scale = 1.0f / sqrtf((float)a->hd);
     HIP_TRY(moe::launch_attn_decode(aa, fused, s));
     return MOE_HIP_OK;
+}
+
+int moe_hip_attn_decode_dev(MoeHipAttn *a, float *x, int B, const int *pos, float *k_cache,
+                            float *v_cache, float eps, void *stream) {
+    return attn_decode(a, x, B, pos, k_cache, v_cache, eps, stream);
+}
+
+int moe_hip_decode_block_dev(MoeHipAttn *a, MoeHipLayer *L, const float *rms_ffn, float *x, int B,
+                             const int *pos, float *k_cache, float *v_cache, float eps,
+                             float *x_norm, int *ids, void *stream) {
+    if (!a || !L || !rms_ffn || a->d != L->d)
+        return set_err(MOE_HIP_ERR_ARG, "block: attention and MoE layer must share d_model");
+    if (B < 0) return set_err(MOE_HIP_ERR_ARG, "bad block arguments");
+    if (B == 0) return MOE_HIP_OK;
+    TRY(ensure_init());
+    float *xn = x_norm;
+    if (!xn) {
+        TRY(g_ws.xn.reserve(sizeof(float) * (size_t)B * L->d));
+        xn = g_ws.xn.as<float>();
+    }
+    TRY(attn_decode(a, x, B, pos, k_cache, v_cache, eps, stream));
+    Norm nm;
+    nm.x_raw = x; nm.rms_w = rms_ffn; nm.eps = eps;
+    return forward_impl(L, xn, B, x, nullptr, ids, 1, stream, nm);
 }
 
 // ---------------------------------------------------------------------------
@@ -668,10 +704,14 @@ int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream
 
 static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
                       int *counts, int *offsets, int *tile_off, int *perm, hipStream_t s,
-                      bool dispatch = true) {
+                      bool dispatch = true, Norm nm = Norm{}) {
     TRY(ensure_counters());
     moe::RouteArgs ra{x, L->wr, L->bias, T, L->d, L->E, L->k, probs, ids, gw};
     ra.no_dispatch = dispatch ? 0 : 1;
+    if (nm.x_raw) {
+        ra.x_raw = nm.x_raw; ra.rms_w = nm.rms_w; ra.rms_eps = nm.eps;
+        ra.rms_rcp = 1.0f / (float)L->d; ra.xn_out = const_cast<float *>(x);
+    }
     if (g_rpath != 1) {
         ra.wrT = L->wrT;
         ra.wr_nonfinite = L->wr_nonfinite;
@@ -709,6 +749,13 @@ int moe_hip_route_dev(MoeHipLayer *L, const float *x, int T, float *probs, int *
 
 int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
                         int accumulate, void *stream) {
+    return forward_impl(L, x, T, out, probs, ids, accumulate, stream, Norm{});
+}
+
+// x: the rows to route and multiply; with nm.x_raw set they are written
+// first, as rms_norm(nm.x_raw) (then x must be writable device memory).
+static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
+                        int accumulate, void *stream, Norm nm) {
     if (!L || T < 0 || (T > 0 && (!x || !out))) return set_err(MOE_HIP_ERR_ARG, "bad forward arguments");
     if (T == 0) return MOE_HIP_OK;
     const int d = L->d, F = L->F, E = L->E, k = L->k;
@@ -749,9 +796,13 @@ int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float
     const size_t fused_bytes = sizeof(float) * (size_t)fused_splits * n * d;
     const bool fused = use_decode && g_path != 3 && fused_bytes <= moe::kFusedPartialBytes;
     const bool one_launch = fused && one_launch_ok;
+    if (nm.x_raw && one_launch) {   // (its router blocks do not normalise)
+        HIP_TRY(moe::launch_rms_norm(nm.x_raw, nm.rms_w, nm.eps, T, d, const_cast<float *>(x), s));
+        nm = Norm{};
+    }
     if (!one_launch)
         TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm,
-                       s, !use_decode));
+                       s, !use_decode, nm));
     int ksplit = 1;
     if (use_decode) {
         // Fused gate/up + split-K down while its partials stay small, else
@@ -945,8 +996,9 @@ int moe_hip_ffn_sublayer_dev(MoeHipLayer *L, float *x, const float *rms_w, float
         TRY(g_ws.xn.reserve(sizeof(float) * (size_t)T * L->d));
         xn = g_ws.xn.as<float>();
     }
-    HIP_TRY(moe::launch_rms_norm(x, rms_w, eps, T, L->d, xn, pick_stream(stream)));
-    return moe_hip_forward_dev(L, xn, T, x, probs, ids, 1, stream);
+    Norm nm;
+    nm.x_raw = x; nm.rms_w = rms_w; nm.eps = eps;
+    return forward_impl(L, xn, T, x, probs, ids, 1, stream, nm);
 }
 
 int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,

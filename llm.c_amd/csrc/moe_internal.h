@@ -26,6 +26,12 @@ struct RouteArgs {
     const float *wrT;    // [E x d], transpose of wr
     int wr_nonfinite;    // wr holds an inf or NaN: apply the zero-skip per step
     int no_dispatch;     // routing only (the decode kernels find their own slots)
+    // Optional: the rows are rms_norm(x_raw; rms_w, rms_eps) (rms_rcp =
+    // 1/d), computed first into xn_out (== x) by the router itself.
+    const float *x_raw = nullptr;
+    const float *rms_w = nullptr;
+    float rms_eps = 0.0f, rms_rcp = 0.0f;
+    float *xn_out = nullptr;
 };
 
 // Up to this many 16-token row blocks the row-block router's last workgroup

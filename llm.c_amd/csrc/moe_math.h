@@ -83,6 +83,59 @@ __device__ inline float glibc_expf(float x) {
 // the hardware exp2 and reciprocal (about 1 ulp each).  The expert outputs
 // are held to a tolerance, not bits (the compiled reference itself divides
 // with an rcpps estimate here), so the fast forms cost nothing in parity.
+// rms_norm (src/matrix.c:666-711) of one row of cols = 16 * nb floats by the
+// 16 lanes of a lane group (lane l = the reference's accumulator lane l:
+// columns 16b + l, b ascending, fused multiply-adds), folded as
+// v_l = acc_l + acc_(l+8), s_i = v_i + v_(i+4), ((s_0 + s_1) + (s_2 + s_3)),
+// then y = (x * inv) * w with inv = 1 / sqrt(fma(ss, rcp_cols, eps))
+// correctly rounded.  ld(i) returns x[i] of the row; every lane of the group
+// calls this (a dead row passes any valid row and store = false).  ys: an
+// optional second copy of the row (e.g. in LDS), written even when !store,
+// flushed to zero if FTZ.
+template <class LD>
+__device__ inline void rms_row16(const LD &ld, const float *w, int nb, float eps, float rcp_cols,
+                                 float *y, bool store, float *ys = nullptr, bool ftz = false) {
+    const int l = threadIdx.x & 15;
+    constexpr int kHeld = 32;   // rows up to 512 wide stay in registers
+    float v[kHeld], wv[kHeld];
+    float acc = 0.0f;
+    if (nb <= kHeld) {
+#pragma unroll
+        for (int b = 0; b < kHeld; ++b) v[b] = ld(16 * (b < nb ? b : 0) + l);
+#pragma unroll
+        for (int b = 0; b < kHeld; ++b) wv[b] = w[16 * (b < nb ? b : 0) + l];
+#pragma unroll
+        for (int b = 0; b < kHeld; ++b)
+            if (b < nb) acc = fmaf(v[b], v[b], acc);
+    } else {
+        for (int b0 = 0; b0 < nb; b0 += 8) {
+            float u8[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) u8[u] = ld(16 * (b0 + u < nb ? b0 + u : 0) + l);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (b0 + u < nb) acc = fmaf(u8[u], u8[u], acc);
+        }
+    }
+    acc = acc + __shfl_down(acc, 8, 16);
+    acc = acc + __shfl_down(acc, 4, 16);
+    acc = acc + __shfl_down(acc, 1, 16);
+    acc = acc + __shfl_down(acc, 2, 16);
+    const float inv = __shfl(1.0f / sqrtf(fmaf(acc, rcp_cols, eps)), 0, 16);
+    if (!store && !ys) return;
+    auto put = [&](int i, float o) {
+        if (store) y[i] = o;
+        if (ys) ys[i] = ftz ? ftz_f(o) : o;
+    };
+    if (nb <= kHeld) {
+#pragma unroll
+        for (int b = 0; b < kHeld; ++b)
+            if (b < nb) put(16 * b + l, (v[b] * inv) * wv[b]);
+    } else {
+        for (int b = 0; b < nb; ++b) put(16 * b + l, (ld(16 * b + l) * inv) * w[16 * b + l]);
+    }
+}
+
 __device__ inline float swiglu_fast(float g, float u) {
     const float e = __builtin_amdgcn_exp2f(-g * 1.44269504f);
     const float sig = __builtin_amdgcn_rcpf(1.0f + e);

@@ -599,6 +599,14 @@ hipError_t launch_rows_router(const RouteArgs &a, const DispatchArgs &da, hipStr
 // sorts them.
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
+    if (a.rms_w && !(a.wrT && a.d % 16 == 0)) {
+        // Only the row-block router normalises its rows itself.
+        hipError_t e = launch_rms_norm(a.x_raw, a.rms_w, a.rms_eps, a.T, a.d, a.xn_out, s);
+        if (e != hipSuccess) return e;
+        RouteArgs b = a;
+        b.rms_w = nullptr;
+        return launch_route_dispatch(b, da, s);
+    }
     if (a.no_dispatch)
         return a.wrT ? launch_rows_router<false>(a, da, s) : launch_router<false>(a, da, s);
     if (a.wrT) {

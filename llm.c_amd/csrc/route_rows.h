@@ -225,9 +225,10 @@ __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *l
 
     float4 rx[XL];
     float rw[RE][WV], wc[RE][WV];
-    auto gload = [&](int k0) {
+    auto gload = [&](int k0, bool with_x = true) {
 #pragma unroll
         for (int i = 0; i < XL; ++i) {
+            if (!with_x) break;
             const int q = min(tid + NT * i, XQ - 1);
             const int rr = q / (KC / 4), c4 = q % (KC / 4);
             const int t = min(t0 + rr, T - 1);
@@ -238,9 +239,10 @@ __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *l
 #pragma unroll
             for (int s4 = 0; s4 < WV; ++s4) rw[j][s4] = wrow[j][k0 + 16 * s4];
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](int buf, bool with_x = true) {
 #pragma unroll
         for (int i = 0; i < XL; ++i) {
+            if (!with_x) break;
             const int q = tid + NT * i;
             if (XQ % NT == 0 || q < XQ) {
                 const int rr = q / (KC / 4), c4 = q % (KC / 4);
@@ -255,12 +257,29 @@ __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *l
             for (int s4 = 0; s4 < WV; ++s4) wc[j][s4] = rw[j][s4];
     };
 
+    const int nchunk = d / KC;
+    // With a.rms_w the block's rows are first normalised from x_raw (sixteen
+    // lanes per row, the reference's accumulator order) into a.x; in one
+    // chunk (d == KC) straight into the LDS rows as well, else read back.
+    const bool pre = a.rms_w && nchunk == 1;
+    if (pre) gload(0, false);   // (router rows in flight during the normalisation)
+    if (a.rms_w) {
+        for (int rr = tid >> 4; rr < 16; rr += NT / 16) {
+            const int t = min(t0 + rr, T - 1);
+            const float *xr = a.x_raw + (size_t)t * d;
+            rms_row16([&](int i) { return xr[i]; }, a.rms_w, d / 16, a.rms_eps, a.rms_rcp,
+                      a.xn_out + (size_t)t * d, t0 + rr < T, pre ? &xs[0][rr][0] : nullptr, SKIP);
+        }
+        if (!pre) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the rows are stored
+            __syncthreads();
+        }
+    }
     float acc[RE];
 #pragma unroll
     for (int j = 0; j < RE; ++j) acc[j] = 0.0f;
-    const int nchunk = d / KC;
-    gload(0);
-    sstore(0);
+    if (!pre) gload(0);
+    sstore(0, !pre);
     __syncthreads();
     if (COHERENT && loaded && tid == 0)
         __hip_atomic_fetch_add(loaded, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

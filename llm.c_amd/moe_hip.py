@@ -78,6 +78,8 @@ SIGNATURES = {
     "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
     "moe_hip_set_router_path": (C.c_int, [C.c_int]),
     "moe_hip_set_attn_path": (C.c_int, [C.c_int]),
+    "moe_hip_decode_block_dev": (C.c_int, [_P, _P, _P, _P, C.c_int, _P, _P, _P, C.c_float, _P,
+                                           _P, _P]),
     "moe_hip_get_attn_path": (C.c_int, []),
     "moe_hip_device_check": (C.c_int, []),
     "moe_hip_timer_start": (C.c_int, []),
@@ -253,6 +255,14 @@ class Attn:
     def decode_dev(self, x_ptr, B, pos_ptr, k_cache_ptr, v_cache_ptr, eps, stream=None):
         check(lib().moe_hip_attn_decode_dev(self.h, x_ptr, B, pos_ptr, k_cache_ptr, v_cache_ptr,
                                             eps, stream))
+
+    def decode_block_dev(self, layer, rms_ffn_ptr, x_ptr, B, pos_ptr, k_cache_ptr, v_cache_ptr,
+                         eps, x_norm_ptr=None, ids_ptr=None, stream=None):
+        """One decoder block: x += Attn(rms_norm(x)), then x += MoE(rms_norm(x))
+        with the MoE layer `layer` (moe_hip_decode_block_dev)."""
+        check(lib().moe_hip_decode_block_dev(self.h, layer.h, rms_ffn_ptr, x_ptr, B, pos_ptr,
+                                             k_cache_ptr, v_cache_ptr, eps, x_norm_ptr, ids_ptr,
+                                             stream))
 
     def close(self):
         if self.h:

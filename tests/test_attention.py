@@ -171,3 +171,51 @@ def test_attn_decode_position_out_of_range(fused):
         assert np.array_equal(kg[b], kc[b]) and np.array_equal(vg[b], vc[b])
     xo, _, _ = run_oracle(x[:1], w, kc[:1], vc[:1], pos[:1], c, s)
     assert orc.rel_l2(xg[:1], xo) < 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fused", [1, 0], ids=["one-launch", "launches"])
+def test_decode_block_device(fused):
+    """moe_hip_decode_block_dev: x += Attn(rms_norm(x)), then x += MoE(
+    rms_norm(x; rms_ffn)).  The FFN's normalised rows (made by the MoE
+    router's first step) are bit-identical to rms_norm of the attention
+    output, routing on them is bit-exact, and x is within the layer
+    tolerance of that output plus the oracle's MoE."""
+    from conftest import CONFIGS
+    from test_gpu_parity import assert_close, bits, host_layer
+    c = CONFIGS["c4"]
+    d, F, E, k = c["d"], c["F"], c["E"], c["k"]
+    nh, nkv, hd, max_seq, B = 8, 2, d // 8, 300, 40
+    pos = np.random.default_rng(12).integers(0, max_seq, B).astype(np.int32)
+    pos[3] = max_seq          # out of range: attention skipped, FFN still applied
+    x, w, kc, vc, pos, cs, sn = make_case(B, max_seq, pos, 12, d, nh, nkv, hd)
+    rms_ffn = (1.0 + 0.1 * np.random.default_rng(13).standard_normal(d)).astype(np.float32)
+    x_attn, _, _ = run_device(x, w, kc, vc, pos, cs, sn, nh, nkv, hd, fused)
+
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(11, c["std_router"], c["std_expert"])
+    hw = host_layer(d, F, E, k, 11, c["std_router"], c["std_expert"])
+    at = mh.Attn(d, nh, nkv, hd, max_seq)
+    prev = mh.attn_path()
+    mh.set_attn_path(fused)
+    try:
+        at.load(w["wq"], w["wk"], w["wv"], w["wo"], w["rms"])
+        at.set_rope(cs, sn)
+        dx, dk, dv = (mh.DeviceArray.from_host(np.ascontiguousarray(a)) for a in (x, kc, vc))
+        dp = mh.DeviceArray.from_host(pos)
+        dw = mh.DeviceArray.from_host(rms_ffn)
+        dxn = mh.DeviceArray((B, d))
+        dids = mh.DeviceArray((B, k), np.int32)
+        print(f"[gpu-test] decode block fused={fused} B={B}", flush=True)
+        at.decode_block_dev(layer, dw.ptr, dx.ptr, B, dp.ptr, dk.ptr, dv.ptr, 1e-5, dxn.ptr,
+                            dids.ptr)
+        mh.device_check()
+        xn_ref = orc.rms_norm(x_attn, rms_ffn, 1e-5)
+        assert np.array_equal(bits(dxn.to_host()), bits(xn_ref))
+        o_ref, _, i_ref = orc.moe_forward(xn_ref, hw, nthreads=16)
+        assert np.array_equal(dids.to_host(), i_ref)
+        assert_close(dx.to_host(), x_attn + o_ref, "decode block")
+    finally:
+        mh.set_attn_path(prev)
+        at.close()
+        layer.close()
