@@ -15,6 +15,12 @@ small .npz fixtures next to this script:
   golden_moe.npz       layer outputs of token samples at configs 2-5
   golden_rms.npz       rms_norm (src/matrix.c:666-711) rows at the configs'
                        widths and at widths with 8-column and scalar tails
+  golden_attn.npz      the decode step's attention sublayer, x after
+                       inference_step (src/inference.c:231-363) of a one-block
+                       MoE model (whose decode FFN is the identity) and the
+                       cache rows it writes, at several head shapes and
+                       positions (oracle/_ref/libref_attn.so, run by
+                       oracle/ref_attn_harness.c)
 
 The reference MoE has no router bias (src/transformer.c:299-300).  Config 5
 is run through the reference's own moe_forward with x extended by a column of
@@ -22,7 +28,7 @@ ones and W_router by the bias row: the FMA chain's last term is then 1*b[e],
 i.e. logits + b rounded once — the mat_mul_add form the library implements.
 
 Run (where the reference sources are present): python tests/golden/make_golden.py
-(`... make_golden.py rms` writes golden_rms.npz only)
+(`... make_golden.py rms` / `... attn` write golden_rms.npz / golden_attn.npz only)
 """
 import ctypes as C
 import hashlib
@@ -240,9 +246,66 @@ def main_rms():
     np.savez_compressed(os.path.join(HERE, "golden_rms.npz"), **rs)
 
 
+# (d, nh, nkv, hd, max_seq, positions): GQA 4, the decode config's heads
+# (d 512, hd 64), 8 query heads on one kv head, and one query head per kv head.
+ATTN_CASES = (
+    (128, 8, 2, 16, 40, (0, 1, 17, 39)),
+    (512, 8, 2, 64, 160, (0, 5, 127, 128, 159)),
+    (256, 8, 1, 32, 70, (0, 33, 69)),
+    (64, 4, 4, 16, 24, (0, 2, 23)),
+)
+
+
+def attn_inputs(i):
+    """Inputs of attention case i: x N(0, 3^2) rows (one per position), W_Q,
+    W_K, W_V N(0, 1/d), W_O N(0, 1/qd), rms_attn N(1, 0.1), caches N(0, 1);
+    RoPE tables from orc.rope_tables(max_seq, hd, 10000)."""
+    d, nh, nkv, hd, ms, pos = ATTN_CASES[i]
+    qd, kd, sd = nh * hd, nkv * hd, 900 + 10 * i
+    f = lambda shape, st, std, mean=0.0: orc.synth(shape, sd, st, std, mean=mean)
+    w = dict(wq=f((d, qd), 1, d ** -0.5), wk=f((d, kd), 2, d ** -0.5), wv=f((d, kd), 3, d ** -0.5),
+             wo=f((qd, d), 4, qd ** -0.5), rms=f((d,), 5, 0.1, mean=1.0))
+    x = f((len(pos), d), 6, 3.0)
+    kc, vc = f((ms, kd), 7, 1.0), f((ms, kd), 8, 1.0)
+    cos_t, sin_t = orc.rope_tables(ms, hd, 10000.0)
+    return x, w, kc, vc, np.asarray(pos, np.int32), cos_t, sin_t
+
+
+def main_attn():
+    lib_path = os.path.join(ROOT, "oracle", "_ref", "libref_attn.so")
+    if not os.path.exists(lib_path):
+        sys.exit("oracle/_ref/libref_attn.so missing: run `make -C oracle ref` first")
+    orc.orc().orc_set_ftz_daz(1)
+    ref = C.CDLL(lib_path)
+    P, I, F = C.c_void_p, C.c_int, C.c_float
+    ref.ref_attn_step.argtypes = [I, I, I, I, I, F] + [P] * 9 + [I, P]
+    ref.ref_attn_step.restype = I
+    gs = {}
+    for i, (d, nh, nkv, hd, ms, pos) in enumerate(ATTN_CASES):
+        x, w, kc, vc, pos, cos_t, sin_t = attn_inputs(i)
+        outs, krows, vrows = [], [], []
+        for j, p in enumerate(pos):
+            xo, k2, v2 = x[j].copy(), kc.copy(), vc.copy()
+            ptr = lambda a: a.ctypes.data
+            rc = ref.ref_attn_step(d, nh, nkv, hd, ms, F(1e-5), ptr(w["wq"]), ptr(w["wk"]),
+                                   ptr(w["wv"]), ptr(w["wo"]), ptr(w["rms"]), ptr(cos_t),
+                                   ptr(sin_t), ptr(k2), ptr(v2), int(p), ptr(xo))
+            assert rc == 0
+            keep = np.arange(ms) != p
+            assert np.array_equal(k2[keep], kc[keep]) and np.array_equal(v2[keep], vc[keep])
+            outs.append(xo); krows.append(k2[p]); vrows.append(v2[p])
+        gs[f"x_{i}"], gs[f"k_{i}"], gs[f"v_{i}"] = np.stack(outs), np.stack(krows), np.stack(vrows)
+        gs[f"sha_x_{i}"], gs[f"sha_kc_{i}"], gs[f"sha_wq_{i}"] = sha(x), sha(kc), sha(w["wq"])
+        print("attention case", i, "done")
+    np.savez_compressed(os.path.join(HERE, "golden_attn.npz"), **gs)
+
+
 if __name__ == "__main__":
     if sys.argv[1:] == ["rms"]:
         main_rms()
+    elif sys.argv[1:] == ["attn"]:
+        main_attn()
     else:
         main()
         main_rms()
+        main_attn()

@@ -1,11 +1,11 @@
 """The attention half of the KV-cache decode step (src/inference.c:252-308).
 
-CPU: the oracle restatement (orc_attn_decode) pinned by an fp64 textbook
-evaluation and by closed forms (position 0 attends only the new token, so
-W_Q and W_K drop out; RoPE at position 0 is the identity).  The compiled
-reference cannot pin it: its attention.c does not build here (an unguarded
-cblas call), so the restatement follows the source, with parity to the
-reference's build unpinned beyond these checks.
+CPU: the oracle restatement (orc_attn_decode) pinned against the compiled
+reference's own decode step (golden_attn.npz: inference_step of
+src/inference.c, built from source, on a one-block MoE model whose decode
+FFN is the identity), by an fp64 textbook evaluation and by closed forms
+(position 0 attends only the new token, so W_Q and W_K drop out; RoPE at
+position 0 is the identity).
 GPU: moe_hip_attn_decode_dev against the oracle within the layer tolerance
 (chunked softmax and V sums reorder the reference's sequential ones)."""
 import numpy as np
@@ -13,6 +13,10 @@ import pytest
 
 import moe_hip as mh
 import orc
+
+import os, sys  # noqa: E401
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import make_golden as mg  # noqa: E402  (input builders only; the reference is not run)
 
 D, NH, NKV, HD = 128, 8, 2, 16
 
@@ -63,6 +67,27 @@ def textbook(x, w, kc, vc, pos, cos_t, sin_t, nh=NH, nkv=NKV, hd=HD):
             ho[h] = (e / e.sum()) @ V[: p + 1, kv * hd:(kv + 1) * hd]
         out[b] = x[b] + ho.reshape(-1) @ w["wo"]
     return out
+
+
+@pytest.mark.parametrize("case", range(len(mg.ATTN_CASES)))
+def test_oracle_vs_reference_decode_step(case):
+    """The oracle against the compiled reference's inference_step, position
+    by position: x within 2e-6 relative (the reference's -ffast-math build
+    reassociates rmsnorm_vec's sum and vectorises expf), the k and v rows it
+    appends within 1e-6."""
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "golden_attn.npz"))
+    d, nh, nkv, hd, ms, _ = mg.ATTN_CASES[case]
+    x, w, kc, vc, pos, cos_t, sin_t = mg.attn_inputs(case)
+    B = len(pos)
+    kcb = np.ascontiguousarray(np.broadcast_to(kc, (B,) + kc.shape))
+    vcb = np.ascontiguousarray(np.broadcast_to(vc, (B,) + vc.shape))
+    xo, ko, vo = run_oracle(x, w, kcb, vcb, pos, cos_t, sin_t, nh, nkv, hd)
+    assert orc.rel_l2(xo, g[f"x_{case}"]) < 2e-6
+    assert float(np.abs(xo - g[f"x_{case}"]).max()) < 2e-5
+    for b, p in enumerate(pos):
+        assert orc.rel_l2(ko[b, p], g[f"k_{case}"][b]) < 1e-6
+        assert orc.rel_l2(vo[b, p], g[f"v_{case}"][b]) < 1e-6
 
 
 def test_oracle_vs_fp64_textbook():
@@ -219,3 +244,26 @@ def test_decode_block_device(fused):
         mh.set_attn_path(prev)
         at.close()
         layer.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", range(len(mg.ATTN_CASES)))
+def test_attn_decode_device_vs_reference(case):
+    """The device sublayer on the golden inputs against the compiled
+    reference's inference_step outputs (golden_attn.npz), within the layer
+    tolerance."""
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "golden_attn.npz"))
+    d, nh, nkv, hd, ms, _ = mg.ATTN_CASES[case]
+    x, w, kc, vc, pos, cos_t, sin_t = mg.attn_inputs(case)
+    B = len(pos)
+    kcb = np.ascontiguousarray(np.broadcast_to(kc, (B,) + kc.shape))
+    vcb = np.ascontiguousarray(np.broadcast_to(vc, (B,) + vc.shape))
+    print(f"[gpu-test] attention vs reference case {case}", flush=True)
+    xg, kg, vg = run_device(x, w, kcb, vcb, pos, cos_t, sin_t, nh, nkv, hd)
+    rel, mabs = orc.rel_l2(xg, g[f"x_{case}"]), float(np.abs(xg - g[f"x_{case}"]).max())
+    print(f"[gpu-test]   rel-L2 {rel:.3e} max-abs {mabs:.3e}", flush=True)
+    assert rel <= 1e-5 and mabs <= 1e-4
+    for b, p in enumerate(pos):
+        assert orc.rel_l2(kg[b, p], g[f"k_{case}"][b]) < 1e-5
+        assert orc.rel_l2(vg[b, p], g[f"v_{case}"][b]) < 1e-5
