@@ -10,6 +10,8 @@ Also measured in the same run:
   * decode: 64 sequences x 1 token through 8 MoE layers of d=512, d_ff=2048,
     E=16, top-2 (8 layers' weights, 1.6 GB, so the 256 MB last-level cache
     cannot hold them), reported as MoE decode tokens/s and HBM GB/s;
+  * prefill_batch8x512: the T=4096 (batch 8 x seq 512) layer, d=256,
+    d_ff=1024, E=8, top-2, timed the same way;
   * decode_step: the whole block stack of that decode step (GQA attention
     over a 1024-position KV cache, then the MoE FFN sublayer, per block) with
     the residual stream on the device;
@@ -83,6 +85,27 @@ def prefill(mh, steps, warmup, T=16384, d=2048, F=8192, E=64, k=4, seed=5):
                bias=bias is not None)
     state = dict(layer=layer, x=x, bias=bias, ids=ids.to_host(), seed=seed)
     return res, state
+
+
+def prefill_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2):
+    """The batch-8 x seq-512 prefill layer (d=256, d_ff=1024, E=8, top-2;
+    router weights N(0, 0.1), experts N(0, 0.02)), timed like the headline."""
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(2, 0.1, 0.02)
+    x = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(x.ptr, T * d, 2, 0, 0.0, 1.0)
+    out = mh.DeviceArray((T, d))
+    for _ in range(max(warmup, 1)):
+        layer.forward_dev(x.ptr, T, out.ptr)
+    mh.synchronize()
+    mh.timer_start()
+    for _ in range(steps):
+        layer.forward_dev(x.ptr, T, out.ptr)
+    ms = mh.timer_stop() / steps
+    layer.close()
+    flops = 6.0 * T * k * d * F + 2.0 * T * d * E
+    return dict(T=T, d=d, F=F, E=E, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3),
+                mfma_frac=flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
 
 
 def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
@@ -276,7 +299,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "decode_step", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "prefill_small", "decode", "decode_step", "copy"], default=None,
                     help="run one section only (for profiling); prints its JSON to stderr")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -299,6 +322,9 @@ def main():
     if args.only == "decode":
         log("decode", json.dumps(decode(mh, args.steps, args.warmup)))
         return
+    if args.only == "prefill_small":
+        log("prefill_small", json.dumps(prefill_small(mh, args.steps, args.warmup)))
+        return
     if args.only == "decode_step":
         log("decode_step", json.dumps(decode_step(mh, args.steps, args.warmup)))
         return
@@ -307,6 +333,8 @@ def main():
         log("prefill", json.dumps(pre))
         return
     log("prefill", json.dumps(pre))
+    small = prefill_small(mh, args.steps, args.warmup)
+    log("prefill_small", json.dumps(small))
     dec = stp = None
     if not args.no_decode:
         dec = decode(mh, args.steps, args.warmup)
@@ -352,6 +380,10 @@ def main():
         "expert_load_max_over_mean": pre["counts_max_over_mean"],
         "cpu_baseline": cpu,
     }
+    line["prefill_batch8x512"] = {
+        "workload": "moe prefill layer T=4096 (8 x 512) d=256 d_ff=1024 E=8 top-2",
+        "tokens_per_s": small["tokens_per_s"], "ms_per_step": small["ms"],
+        "layer_mfma_frac": small["mfma_frac"]}
     if dec:
         line["decode"] = {
             "workload": "64 seqs x 1 token, 8 MoE layers d=512 d_ff=2048 E=16 top-2",

@@ -48,8 +48,10 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     float *Bs = smem + 2 * BM * LDK;           // [2][BN][LDK]
 
     const int ntiles = a.N / BN;
-    const int nt = blockIdx.x % ntiles;
-    const int mtg = blockIdx.x / ntiles;
+    const int per_split = a.max_mtiles * ntiles;
+    const int ks = blockIdx.x / per_split;       // reduction split (down projection)
+    const int nt = (blockIdx.x % per_split) % ntiles;
+    const int mtg = (blockIdx.x % per_split) / ntiles;
     const int total = a.tile_off[a.E];
     if (mtg >= total) return;
     const int e = a.tile_expert[mtg];
@@ -123,13 +125,14 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.0f;
 
-    const int nk = K / KT;
-    gload(0);
+    const int nk = K / KT / a.ksplit;   // K steps of this split
+    const int kb = ks * nk * KT;
+    gload(kb);
     sstore(0);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * KT);
+        if (kt + 1 < nk) gload(kb + (kt + 1) * KT);
         const float *as = As + buf * BM * LDK + (wm * 64 + li) * LDK + 16 * lh;
         const float *bs = Bs + buf * BN * LDK + (wn * 64 + li) * LDK + 16 * lh;
         if (nmb == 2) {
@@ -182,6 +185,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                     a.c[(size_t)(row0 + row) * a.ldc + f] = swiglu_fast(acc[m][0][r], acc[m][1][r]);
             }
     } else {
+        float *c = a.c + (size_t)ks * a.split_stride;
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                     size_t dst = (size_t)a.perm[row0 + row] * a.ldc;
 #pragma unroll
                     for (int n = 0; n < 2; ++n)
-                        a.c[dst + nt * BN + wn * 64 + n * 32 + li] = acc[m][n][r];
+                        c[dst + nt * BN + wn * 64 + n * 32 + li] = acc[m][n][r];
                 }
             }
     }
@@ -210,14 +214,16 @@ hipError_t launch_grouped(const GemmArgs &a, hipStream_t s) {
         attr_set = true;
     }
     const int ntiles = a.N / BN;
-    dim3 grid((unsigned)(a.max_mtiles * ntiles));
+    dim3 grid((unsigned)(a.max_mtiles * ntiles * a.ksplit));
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE, WN>), grid, dim3(128 * WN), lds, s, a);
     return hipGetLastError();
 }
 
 template <int MODE>
 hipError_t launch_mode(const GemmArgs &a, hipStream_t s) {
-    switch (gemm_block_n(a.N)) {
+    const GemmPlan pl = gemm_plan(a.N, a.K, a.max_mtiles, MODE == 1);
+    if (a.ksplit != (MODE == 1 ? pl.ksplit : 1)) return hipErrorInvalidValue;
+    switch (pl.bn) {
         case 256: return launch_grouped<MODE, 4>(a, s);
         case 128: return launch_grouped<MODE, 2>(a, s);
         case 64:  return launch_grouped<MODE, 1>(a, s);
@@ -360,11 +366,19 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(float *dst, size_t n, 
 
 }  // namespace
 
-int gemm_block_n(int N) {
-    if (N % 256 == 0) return 256;
-    if (N % 128 == 0) return 128;
-    if (N % 64 == 0) return 64;
-    return 0;
+GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split) {
+    constexpr int kTarget = 512;   // workgroups: two per CU
+    GemmPlan p{0, 1};
+    if (N % 256 == 0) p.bn = 256;
+    else if (N % 128 == 0) p.bn = 128;
+    else if (N % 64 == 0) p.bn = 64;
+    else return p;
+    while (p.bn > 64 && (size_t)max_mtiles * (N / p.bn) < kTarget) p.bn /= 2;
+    if (allow_split)
+        while (p.ksplit < 8 && (size_t)max_mtiles * (N / p.bn) * p.ksplit < kTarget &&
+               K % (2 * p.ksplit * KT) == 0 && K / (2 * p.ksplit) >= 128)
+            p.ksplit *= 2;
+    return p;
 }
 
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) { return launch_mode<0>(a, s); }

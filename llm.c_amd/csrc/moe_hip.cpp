@@ -860,6 +860,12 @@ static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
         moe::GemmArgs dn{g_ws.h.as<float>(), perm, k, L->wdT, g_ws.ys.as<float>(), offsets, tile_off,
                          tile_e, E, F, d, d, max_mtiles};
+        // Small grids split the down projection's reduction; the combine adds
+        // the splits in order.
+        dn.ksplit = ksplit = moe::gemm_plan(d, F, max_mtiles, true).ksplit;
+        dn.split_stride = n * (size_t)d;
+        if (ksplit > 1) TRY(g_ws.ys.reserve(sizeof(float) * (size_t)ksplit * n * d));
+        dn.c = g_ws.ys.as<float>();
         HIP_TRY(moe::launch_gemm_down(dn, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
     }

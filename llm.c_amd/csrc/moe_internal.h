@@ -71,6 +71,10 @@ struct GemmArgs {
     int N;               // packed output columns (2F for gate/up, d for down)
     int ldc;             // row stride of c (F for gate/up, d for down)
     int max_mtiles;      // grid bound on m-tiles
+    // Down projection only: the reduction split ksplit ways (gemm_plan),
+    // split s writing its partial to c + s * split_stride.
+    int ksplit = 1;
+    size_t split_stride = 0;
 };
 
 struct CombineArgs {
@@ -183,7 +187,12 @@ hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed,
                               uint64_t stream_id, float mean, float std,
                               hipStream_t s);
 
-// Number of n-tiles / block width the gate-up and down launches use.
-int gemm_block_n(int N);
+// Tile width (64, 128 or 256 columns) and reduction split of a grouped GEMM
+// launch: the widest tile dividing N that still gives ~512 workgroups, then
+// (down projection) the split of K that gets there.
+struct GemmPlan {
+    int bn, ksplit;
+};
+GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split);
 
 }  // namespace moe
