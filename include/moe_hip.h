@@ -190,6 +190,24 @@ int moe_hip_forward_dev(MoeHipLayer *layer, const float *x, int T, float *out,
 int moe_hip_rms_norm_dev(const float *x, const float *w, float eps, int rows, int cols,
                          float *y, void *stream);
 
+/* Backward pass of the layer on device rows x [T x d] (no counterpart in
+ * the reference: its block backward, src/transformer.c:975-1013, skips the
+ * FFN/MoE half).  Gradients of L = sum(dout * out) + aux_coef * aux with
+ * out = moe_forward(x) (src/transformer.c:287-366) and the routing held as
+ * that forward decides it (recomputed here, bit-exact), where aux is the
+ * load-balancing loss src/transformer.c:280-282 describes:
+ * aux = n_experts * sum_e f_e * P_e, f_e = (assignments to e) / (T * top_k)
+ * (a count: no gradient), P_e = mean over tokens of probs[t][e].
+ * Outputs, device, in the weights' layout: dx [T x d], dw_router [d x E],
+ * dw_gate, dw_up [n_experts][d x ffn_hidden], dw_down [n_experts][ffn_hidden
+ * x d]; accumulate != 0 adds to them.  aux_loss (device float, may be NULL)
+ * receives aux.  A router bias, if set, enters the forward but gets no
+ * gradient here.  Deterministic; fp32 with fixed summation orders. */
+int moe_hip_backward_dev(MoeHipLayer *layer, const float *x, int T, const float *dout,
+                         float aux_coef, float *dx, float *dw_router, float *dw_gate,
+                         float *dw_up, float *dw_down, float *aux_loss, int accumulate,
+                         void *stream);
+
 /* The MoE block's FFN sublayer on a device-resident residual stream x
  * [T x d], in place: x += MoE(rms_norm(x; rms_w, eps)) (src/transformer.c:
  * 760-767 with the residual add of :767; also the decode form of

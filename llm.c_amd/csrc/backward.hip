@@ -1,0 +1,382 @@
+// backward.hip — backward pass of the MoE layer and its load-balancing loss.
+//
+// The reference has neither: its block backward (src/transformer.c:975-1013)
+// skips the FFN/MoE half, and the auxiliary loss exists only as the comment
+// aux = n_experts * sum_e f_e * P_e (src/transformer.c:280-282).  Here, for
+// the layer of src/transformer.c:287-366 with the routing held as the
+// forward decided it, the gradients of L = sum(dout * out) + aux_coef * aux
+// (f_e = assignments to e / (T k), a count; P_e = mean_t probs[t][e]):
+//
+//   recompute  G, U = x W_g, x W_u (rows in dispatch order), H = silu(G) U,
+//              Y = H W_d
+//   slots      dgw = <Y, dout[t]>, dY = gw dout[t]
+//   experts    dH = dY W_d^T, dG = dH U silu'(G), dU = dH silu(G),
+//              dXr = dG W_g^T + dU W_u^T; dW_d = H^T dY, dW_g = X^T dG,
+//              dW_u = X^T dU over each expert's rows
+//   router     gw = p_sel / S: dp_sel = (dgw - <dgw, gw>) / S; dp += aux_coef
+//              E f / T; dlogits = p (dp - <dp, p>); dW_r = X^T dlogits
+//   dx         = sum over the token's slots of dXr + dlogits W_r^T
+//
+// Two fp32 tiled GEMMs do the products: rows_gemm over the dispatch tile
+// schedule (one expert per 128-row tile), reduce_gemm with the reduction
+// over an expert's rows.  Every sum runs in a fixed order (deterministic).
+#include "moe_internal.h"
+#include "moe_math.h"
+
+namespace moe {
+namespace {
+
+constexpr int kRM = 128, kRN = 64, kRK = 16;   // rows_gemm tile
+constexpr int kQM = 64, kQN = 64, kQR = 16;    // reduce_gemm tile
+
+// C[pos][n] (+)= sum_kk A(pos, kk) B_e(kk, n) for the rows pos of each
+// 128-row tile (expert e).  A(pos, kk) = a[arow * lda + kk] with arow =
+// perm[pos] / topk (GATHER) or pos; B_e(kk, n) = b[e * b_e + kk * ldb + n]
+// or, BT, b[e * b_e + n * ldb + kk].  Thread (tr, tc) = (tid / 16, tid % 16)
+// owns rows 8tr .. 8tr + 7 and columns 4tc .. 4tc + 3; K slices of 16 in LDS.
+struct RowsGemm {
+    const float *a;
+    int lda;
+    const int *perm;
+    int topk;
+    const float *b;
+    size_t b_e;
+    int ldb;
+    float *c;
+    int ldc;
+    const int *offsets, *tile_off, *tile_expert;
+    int E, K, N, max_mtiles, accumulate;
+};
+
+template <bool GATHER, bool BT>
+__global__ __launch_bounds__(256) void rows_gemm_kernel(RowsGemm g) {
+    __shared__ __align__(16) float As[kRK][kRM + 4];
+    __shared__ __align__(16) float Bs[kRK][kRN + 4];
+    const int ntn = (g.N + kRN - 1) / kRN;
+    const int nt = blockIdx.x % ntn, mtg = blockIdx.x / ntn;
+    if (mtg >= g.tile_off[g.E]) return;
+    const int e = g.tile_expert[mtg];
+    const int row0 = g.offsets[e] + (mtg - g.tile_off[e]) * kRM;
+    const int rows = min(kRM, g.offsets[e + 1] - row0);
+    const int n0 = nt * kRN;
+    const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    const float *arow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = min((tid >> 2) + 64 * i, rows - 1);
+        const size_t src = GATHER ? (size_t)(g.perm[row0 + r] / g.topk) : (size_t)(row0 + r);
+        arow[i] = g.a + src * g.lda + 4 * (tid & 3);
+    }
+    const float *bb = g.b + (size_t)e * g.b_e;
+    float acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+
+    for (int k0 = 0; k0 < g.K; k0 += kRK) {
+        float4 av[2], bv;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) av[i] = *reinterpret_cast<const float4 *>(arow[i] + k0);
+        int bk, bn;
+        if (!BT) {   // 16 k rows x 16 column quads
+            bk = tid >> 4;
+            bn = 4 * (tid & 15);
+            bv = n0 + bn < g.N
+                     ? *reinterpret_cast<const float4 *>(bb + (size_t)(k0 + bk) * g.ldb + n0 + bn)
+                     : zero;
+        } else {     // 64 columns x 4 k quads
+            bn = tid >> 2;
+            bk = 4 * (tid & 3);
+            bv = n0 + bn < g.N
+                     ? *reinterpret_cast<const float4 *>(bb + (size_t)(n0 + bn) * g.ldb + k0 + bk)
+                     : zero;
+        }
+        __syncthreads();   // the previous slice is consumed
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = (tid >> 2) + 64 * i, kq = 4 * (tid & 3);
+            As[kq][r] = av[i].x;
+            As[kq + 1][r] = av[i].y;
+            As[kq + 2][r] = av[i].z;
+            As[kq + 3][r] = av[i].w;
+        }
+        if (!BT) {
+            *reinterpret_cast<float4 *>(&Bs[bk][bn]) = bv;
+        } else {
+            Bs[bk][bn] = bv.x;
+            Bs[bk + 1][bn] = bv.y;
+            Bs[bk + 2][bn] = bv.z;
+            Bs[bk + 3][bn] = bv.w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kRK; ++kk) {
+            const float4 a0 = *reinterpret_cast<const float4 *>(&As[kk][8 * tr]);
+            const float4 a1 = *reinterpret_cast<const float4 *>(&As[kk][8 * tr + 4]);
+            const float4 b4 = *reinterpret_cast<const float4 *>(&Bs[kk][4 * tc]);
+            const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+    }
+    const int n = n0 + 4 * tc;
+    if (n >= g.N) return;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 8 * tr + i;
+        if (r >= rows) break;
+        float4 *cp = reinterpret_cast<float4 *>(g.c + (size_t)(row0 + r) * g.ldc + n);
+        float4 v = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+        if (g.accumulate) {
+            const float4 o = *cp;
+            v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+        }
+        *cp = v;
+    }
+}
+
+// C_e[m][n] (+)= sum over the rows pos of group e (offsets[e] ..
+// offsets[e + 1], or 0 .. nrows without offsets) of A(pos, m) B(pos, n),
+// A(pos, m) = a[arow * lda + m] (arow = perm[pos] / topk with GATHER),
+// B(pos, n) = b[pos * ldb + n].  Thread (tm, tn) = (tid / 16, tid % 16)
+// owns rows 4tm .. and columns 4tn .. of the 64 x 64 tile (blockIdx.y,
+// blockIdx.x) of group blockIdx.z; rows in slices of 16 through LDS.
+struct ReduceGemm {
+    const float *a;
+    int lda;
+    const int *perm;
+    int topk;
+    const float *b;
+    int ldb;
+    float *c;
+    size_t c_e;
+    int ldc;
+    const int *offsets;
+    int nrows, M, N, accumulate;
+};
+
+template <bool GATHER>
+__global__ __launch_bounds__(256) void reduce_gemm_kernel(ReduceGemm g) {
+    __shared__ __align__(16) float As[kQR][kQM + 4];
+    __shared__ __align__(16) float Bs[kQR][kQN + 4];
+    const int e = blockIdx.z, m0 = blockIdx.y * kQM, n0 = blockIdx.x * kQN;
+    const int r0 = g.offsets ? g.offsets[e] : 0, r1 = g.offsets ? g.offsets[e + 1] : g.nrows;
+    const int tid = threadIdx.x, tm = tid >> 4, tn = tid & 15;
+    const int lr = tid >> 4, lq = 4 * (tid & 15);   // load row and column quad
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    for (int r = r0; r < r1; r += kQR) {
+        const int row = r + lr;
+        const bool in = row < r1;
+        float av[4], bv[4];
+        const size_t arow = in ? (GATHER ? (size_t)(g.perm[row] / g.topk) : (size_t)row) : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            av[j] = in && m0 + lq + j < g.M ? g.a[arow * g.lda + m0 + lq + j] : 0.f;
+            bv[j] = in && n0 + lq + j < g.N ? g.b[(size_t)row * g.ldb + n0 + lq + j] : 0.f;
+        }
+        __syncthreads();
+        *reinterpret_cast<float4 *>(&As[lr][lq]) = make_float4(av[0], av[1], av[2], av[3]);
+        *reinterpret_cast<float4 *>(&Bs[lr][lq]) = make_float4(bv[0], bv[1], bv[2], bv[3]);
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < kQR; ++rr) {
+            const float4 a4 = *reinterpret_cast<const float4 *>(&As[rr][4 * tm]);
+            const float4 b4 = *reinterpret_cast<const float4 *>(&Bs[rr][4 * tn]);
+            const float a[4] = {a4.x, a4.y, a4.z, a4.w}, b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+    }
+    float *ce = g.c + (size_t)e * g.c_e;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 4 * tm + i;
+        if (m >= g.M) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 4 * tn + j;
+            if (n >= g.N) break;
+            float *cp = ce + (size_t)m * g.ldc + n;
+            *cp = g.accumulate ? *cp + acc[i][j] : acc[i][j];
+        }
+    }
+}
+
+// H = silu(G) * U, the forward's SwiGLU.
+__global__ __launch_bounds__(256) void act_kernel(const float *G, const float *U, float *H,
+                                                  size_t n) {
+    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        H[i] = swiglu_fast(G[i], U[i]);
+}
+
+// In place: G <- dG = dH U silu'(G), U <- dU = dH silu(G).
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(float *G, float *U, const float *dH,
+                                                         size_t n) {
+    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        const float g = G[i], u = U[i], dh = dH[i];
+        const float s = 1.0f / (1.0f + expf(-g));
+        G[i] = dh * u * fmaf(g * s, 1.0f - s, s);
+        U[i] = dh * g * s;
+    }
+}
+
+// One wave per dispatch position pos (slot a = perm[pos], token t = a / k):
+// dgw[a] = <Y[pos], dout[t]> (lane-strided partial sums, then a butterfly),
+// dY[pos] = gw[a] dout[t], inv[a] = pos.
+__global__ __launch_bounds__(256) void slot_kernel(const float *Y, const float *dout,
+                                                   const float *gw, const int *perm, int k, int d,
+                                                   int n, float *dgw, float *dY, int *inv) {
+    const int pos = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (pos >= n) return;
+    const int a = perm[pos], t = a / k;
+    const float w = gw[a];
+    const float *y = Y + (size_t)pos * d, *go = dout + (size_t)t * d;
+    float *dy = dY + (size_t)pos * d;
+    float s = 0.f;
+    for (int c = lane; c < d; c += 64) {
+        const float v = go[c];
+        s = fmaf(y[c], v, s);
+        dy[c] = w * v;
+    }
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) {
+        dgw[a] = s;
+        inv[a] = pos;
+    }
+}
+
+// One thread per token: dlogits [T x E] from dgw through the gate
+// renormalisation, the aux term and the softmax.
+__global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, const int *ids,
+                                                         const float *gw, const float *dgw,
+                                                         const int *counts, int T, int E, int k,
+                                                         float aux_coef, float *dlogits) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= T) return;
+    const float *p = probs + (size_t)t * E;
+    const int *id = ids + (size_t)t * k;
+    float S = 0.f, c = 0.f;
+    for (int s = 0; s < k; ++s) {
+        S += p[id[s]];
+        c = fmaf(dgw[(size_t)t * k + s], gw[(size_t)t * k + s], c);
+    }
+    const float aux_scale = aux_coef * (float)E / ((float)T * (float)T * (float)k);
+    auto dp = [&](int e) {
+        float v = aux_scale * (float)counts[e];
+        for (int s = 0; s < k; ++s)
+            if (id[s] == e) v += (dgw[(size_t)t * k + s] - c) / S;
+        return v;
+    };
+    float dot = 0.f;
+    for (int e = 0; e < E; ++e) dot = fmaf(dp(e), p[e], dot);
+    for (int e = 0; e < E; ++e) dlogits[(size_t)t * E + e] = p[e] * (dp(e) - dot);
+}
+
+// dx[t][c] = sum over slots (in order) of dXr[inv[t k + s]][c], plus
+// sum_e dlogits[t][e] wr[c][e].
+__global__ __launch_bounds__(256) void dx_kernel(const float *dXr, const int *inv,
+                                                 const float *dlogits, const float *wr, int T,
+                                                 int d, int E, int k, int accumulate, float *dx) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)T * d) return;
+    const int t = (int)(i / d), c = (int)(i % d);
+    float v = 0.f;
+    for (int s = 0; s < k; ++s) v += dXr[(size_t)inv[(size_t)t * k + s] * d + c];
+    float r = 0.f;
+    for (int e = 0; e < E; ++e) r = fmaf(dlogits[(size_t)t * E + e], wr[(size_t)c * E + e], r);
+    v += r;
+    dx[i] = accumulate ? dx[i] + v : v;
+}
+
+// aux = E * sum_e (counts[e] / (T k)) * (sum_t probs[t][e] / T), one
+// workgroup: per expert a strided sum and a fixed tree.
+__global__ __launch_bounds__(256) void aux_kernel(const float *probs, const int *counts, int T,
+                                                  int E, int k, float *aux) {
+    __shared__ float red[256];
+    float total = 0.f;
+    for (int e = 0; e < E; ++e) {
+        float s = 0.f;
+        for (int t = threadIdx.x; t < T; t += 256) s += probs[(size_t)t * E + e];
+        red[threadIdx.x] = s;
+        __syncthreads();
+        for (int w = 128; w >= 1; w >>= 1) {
+            if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+            __syncthreads();
+        }
+        total = fmaf((float)counts[e] / ((float)T * (float)k), red[0] / (float)T, total);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *aux = (float)E * total;
+}
+
+unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 16384); }
+
+}  // namespace
+
+hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
+    const int d = b.d, F = b.F, E = b.E, k = b.k, T = b.T;
+    const size_t n = (size_t)T * k;
+    if (T <= 0) return hipSuccess;
+    if (d % 16 || F % 16) return hipErrorInvalidValue;
+    auto rows = [&](auto gather, auto bt, const float *A, int lda, const float *B, size_t b_e,
+                    int ldb, float *C, int K, int N, int accumulate) {
+        RowsGemm g{A, lda, b.perm, k, B, b_e, ldb, C, N, b.offsets, b.tile_off, b.tile_expert,
+                   E, K, N, b.max_mtiles, accumulate};
+        const unsigned grid = (unsigned)(b.max_mtiles * ((N + kRN - 1) / kRN));
+        hipLaunchKernelGGL((rows_gemm_kernel<decltype(gather)::value, decltype(bt)::value>),
+                           dim3(grid), dim3(256), 0, s, g);
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    // Recompute: G, U (gathered x rows), H, Y.
+    rows(T_{}, F_{}, b.x, d, b.wg, (size_t)d * F, F, b.G, d, F, 0);
+    rows(T_{}, F_{}, b.x, d, b.wu, (size_t)d * F, F, b.U, d, F, 0);
+    hipLaunchKernelGGL(act_kernel, dim3(blocks_for(n * F)), dim3(256), 0, s, b.G, b.U, b.H,
+                       n * F);
+    rows(F_{}, F_{}, b.H, F, b.wd, (size_t)F * d, d, b.Y, F, d, 0);
+    // Slots: dgw, dY, the slot -> position map.
+    hipLaunchKernelGGL(slot_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, b.Y, b.dout,
+                       b.gw, b.perm, k, d, (int)n, b.dgw, b.dY, b.inv);
+    // Experts: dH, dG and dU (in place over G, U), dXr (over Y).
+    rows(F_{}, T_{}, b.dY, d, b.wd, (size_t)F * d, d, b.dH, d, F, 0);
+    hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(blocks_for(n * F)), dim3(256), 0, s, b.G, b.U,
+                       b.dH, n * F);
+    rows(F_{}, T_{}, b.G, F, b.wg, (size_t)d * F, F, b.Y, F, d, 0);
+    rows(F_{}, T_{}, b.U, F, b.wu, (size_t)d * F, F, b.Y, F, d, 1);
+    // Router and dx.
+    hipLaunchKernelGGL(router_bwd_kernel, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s,
+                       b.probs, b.ids, b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
+    hipLaunchKernelGGL(dx_kernel, dim3(blocks_for((size_t)T * d)), dim3(256), 0, s, b.Y, b.inv,
+                       b.dlogits, b.wr, T, d, E, k, b.accumulate, b.dx);
+    // Weight gradients over each expert's rows; the router's over all tokens.
+    auto reduce = [&](auto gather, const float *A, int lda, const float *B, int ldb, float *C,
+                      size_t c_e, int M, int N, const int *offsets, int nrows, int groups) {
+        ReduceGemm g{A, lda, b.perm, k, B, ldb, C, c_e, N, offsets, nrows, M, N, b.accumulate};
+        dim3 grid((unsigned)((N + kQN - 1) / kQN), (unsigned)((M + kQM - 1) / kQM),
+                  (unsigned)groups);
+        hipLaunchKernelGGL((reduce_gemm_kernel<decltype(gather)::value>), grid, dim3(256), 0, s,
+                           g);
+    };
+    reduce(F_{}, b.H, F, b.dY, d, b.dwd, (size_t)F * d, F, d, b.offsets, 0, E);
+    reduce(T_{}, b.x, d, b.G, F, b.dwg, (size_t)d * F, d, F, b.offsets, 0, E);
+    reduce(T_{}, b.x, d, b.U, F, b.dwu, (size_t)d * F, d, F, b.offsets, 0, E);
+    reduce(F_{}, b.x, d, b.dlogits, E, b.dwr, 0, d, E, nullptr, T, 1);
+    if (b.aux)
+        hipLaunchKernelGGL(aux_kernel, dim3(1), dim3(256), 0, s, b.probs, b.counts, T, E, k,
+                           b.aux);
+    return hipGetLastError();
+}
+
+}  // namespace moe

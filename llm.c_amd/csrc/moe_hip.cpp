@@ -101,11 +101,11 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, stage,
-        counters, xn, rmsw, aq, ao, apart, agpart, ass, acnt;
+        counters, xn, rmsw, aq, ao, apart, agpart, ass, acnt, bw, bwork;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
                          &tile_expert, &perm, &h, &ys, &stage, &counters, &xn, &rmsw,
-                         &aq, &ao, &apart, &agpart, &ass, &acnt};
+                         &aq, &ao, &apart, &agpart, &ass, &acnt, &bw, &bwork};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -988,6 +988,62 @@ int moe_hip_rms_norm_dev(const float *x, const float *w, float eps, int rows, in
     if (rows == 0) return MOE_HIP_OK;
     TRY(ensure_init());
     HIP_TRY(moe::launch_rms_norm(x, w, eps, rows, cols, y, pick_stream(stream)));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dout, float aux_coef,
+                         float *dx, float *dw_router, float *dw_gate, float *dw_up, float *dw_down,
+                         float *aux_loss, int accumulate, void *stream) {
+    if (!L || T < 0 || (T > 0 && (!x || !dout || !dx || !dw_router || !dw_gate || !dw_up || !dw_down)))
+        return set_err(MOE_HIP_ERR_ARG, "bad backward arguments");
+    if (T == 0) return MOE_HIP_OK;
+    TRY(ensure_init());
+    const int d = L->d, F = L->F, E = L->E, k = L->k;
+    const size_t n = (size_t)T * k;
+    if (n * (size_t)(F > d ? F : d) > (size_t)0x7fffffff)
+        return set_err(MOE_HIP_ERR_UNSUPPORTED, "T*k*max(F,d) exceeds 32-bit indexing");
+    hipStream_t s = pick_stream(stream);
+    // The forward's routing and dispatch (bit-exact with moe_forward).
+    TRY(g_ws.probs.reserve(sizeof(float) * (size_t)T * E));
+    TRY(g_ws.ids.reserve(sizeof(int) * n));
+    TRY(g_ws.gw.reserve(sizeof(float) * n));
+    TRY(g_ws.counts.reserve(sizeof(int) * E));
+    TRY(g_ws.offsets.reserve(sizeof(int) * (E + 1)));
+    TRY(g_ws.tile_off.reserve(sizeof(int) * (E + 1)));
+    TRY(g_ws.perm.reserve(sizeof(int) * n));
+    TRY(route_impl(L, x, T, g_ws.probs.as<float>(), g_ws.ids.as<int>(), g_ws.gw.as<float>(),
+                   g_ws.counts.as<int>(), g_ws.offsets.as<int>(), g_ws.tile_off.as<int>(),
+                   g_ws.perm.as<int>(), s, true));
+    // Weights in the reference layout: wg, wu [E][d x F], wd [E][F x d].
+    const size_t dF = (size_t)d * F;
+    TRY(g_ws.bw.reserve(sizeof(float) * 3 * E * dF));
+    float *wg = g_ws.bw.as<float>(), *wu = wg + E * dF, *wd = wu + E * dF;
+    for (int e = 0; e < E; ++e) {
+        HIP_TRY(moe::launch_unpack_gateup(L->wgu + (size_t)e * 2 * dF, wg + e * dF, wu + e * dF, d,
+                                          F, s));
+        HIP_TRY(moe::launch_unpack_down(L->wdT + (size_t)e * dF, wd + e * dF, F, d, s));
+    }
+    // Workspace: G, U, H, dH [n x F]; Y, dY [n x d]; dgw, inv [n]; dlogits [T x E].
+    const size_t nF = n * F, nd = n * d;
+    TRY(g_ws.bwork.reserve(sizeof(float) * (4 * nF + 2 * nd + 2 * n + (size_t)T * E)));
+    float *G = g_ws.bwork.as<float>(), *U = G + nF, *H = U + nF, *dH = H + nF;
+    float *Y = dH + nF, *dY = Y + nd, *dgw = dY + nd;
+    int *inv = reinterpret_cast<int *>(dgw + n);
+    float *dlogits = reinterpret_cast<float *>(inv + n);
+    moe::BackwardArgs b{};
+    b.x = x; b.dout = dout; b.wr = L->wr; b.wg = wg; b.wu = wu; b.wd = wd;
+    b.probs = g_ws.probs.as<float>(); b.gw = g_ws.gw.as<float>();
+    b.ids = g_ws.ids.as<int>(); b.counts = g_ws.counts.as<int>();
+    b.offsets = g_ws.offsets.as<int>(); b.tile_off = g_ws.tile_off.as<int>();
+    b.tile_expert = g_ws.tile_expert.as<int>(); b.perm = g_ws.perm.as<int>();
+    b.T = T; b.d = d; b.F = F; b.E = E; b.k = k;
+    b.max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
+    b.aux_coef = aux_coef;
+    b.G = G; b.U = U; b.H = H; b.dH = dH; b.Y = Y; b.dY = dY; b.dgw = dgw; b.dlogits = dlogits;
+    b.inv = inv;
+    b.dx = dx; b.dwr = dw_router; b.dwg = dw_gate; b.dwu = dw_up; b.dwd = dw_down;
+    b.aux = aux_loss; b.accumulate = accumulate ? 1 : 0;
+    HIP_TRY(moe::launch_moe_backward(b, s));
     return MOE_HIP_OK;
 }
 

@@ -175,6 +175,26 @@ int attn_sync_ints();
 bool attn_fused_supported(int hd, int nh, int nkv);
 hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s);
 
+// Backward pass of the layer (backward.hip) with the routing of a forward
+// already run (probs, ids, gw, counts, offsets, tile schedule, perm).
+// Weights in the reference layout: wr [d x E], wg, wu [E][d x F], wd [E][F x d].
+// Workspace: G, U, H, dH [n x F], Y, dY [n x d] (n = T k), dgw [n], inv [n],
+// dlogits [T x E].  Outputs (accumulate: added to): dx [T x d], dwr,
+// dwg, dwu, dwd (layouts of the weights); aux (optional) = the loss value.
+struct BackwardArgs {
+    const float *x, *dout;
+    const float *wr, *wg, *wu, *wd;
+    const float *probs, *gw;
+    const int *ids, *counts, *offsets, *tile_off, *tile_expert, *perm;
+    int T, d, F, E, k, max_mtiles;
+    float aux_coef;
+    float *G, *U, *H, *dH, *Y, *dY, *dgw, *dlogits;
+    int *inv;
+    float *dx, *dwr, *dwg, *dwu, *dwd, *aux;
+    int accumulate;
+};
+hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s);
+
 // rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,
                            float *y, hipStream_t s);

@@ -78,6 +78,8 @@ SIGNATURES = {
     "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
     "moe_hip_set_router_path": (C.c_int, [C.c_int]),
     "moe_hip_set_attn_path": (C.c_int, [C.c_int]),
+    "moe_hip_backward_dev": (C.c_int, [_P, _P, C.c_int, _P, C.c_float, _P, _P, _P, _P, _P, _P,
+                                       C.c_int, _P]),
     "moe_hip_decode_block_dev": (C.c_int, [_P, _P, _P, _P, C.c_int, _P, _P, _P, C.c_float, _P,
                                            _P, _P]),
     "moe_hip_get_attn_path": (C.c_int, []),
@@ -227,6 +229,12 @@ class Layer:
         """x += MoE(rms_norm(x)) in place on device rows x [T x d]."""
         check(lib().moe_hip_ffn_sublayer_dev(self.h, x_ptr, rms_w_ptr, eps, T, x_norm_ptr,
                                              probs_ptr, ids_ptr, stream))
+
+    def backward_dev(self, x_ptr, T, dout_ptr, aux_coef, dx_ptr, dwr_ptr, dwg_ptr, dwu_ptr,
+                     dwd_ptr, aux_ptr=None, accumulate=0, stream=None):
+        """Gradients of sum(dout * out) + aux_coef * aux (moe_hip_backward_dev)."""
+        check(lib().moe_hip_backward_dev(self.h, x_ptr, T, dout_ptr, aux_coef, dx_ptr, dwr_ptr,
+                                         dwg_ptr, dwu_ptr, dwd_ptr, aux_ptr, accumulate, stream))
 
     def route_dev(self, x_ptr, T, probs=None, ids=None, gw=None, counts=None, offsets=None,
                   perm=None, stream=None):

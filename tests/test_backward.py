@@ -1,0 +1,127 @@
+"""Backward pass of the MoE layer and its load-balancing loss
+(moe_hip_backward_dev).  The reference has no backward for this layer and no
+code for the loss its comment defines (src/transformer.c:280-282), so there
+is no golden: the fp64 restatement oracle/moe_backward.py is pinned by
+central finite differences of its own fp64 forward (every gradient, with and
+without the loss), by closed forms (uniform routing: aux = 1 and the loss
+adds nothing to the router gradient; softmax gradients sum to zero per
+token), and the device is checked against it within the layer tolerance,
+with the routing the fp32 forward (bit-exact with the reference) decides."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import moe_hip as mh
+import orc
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                                "oracle"))
+import moe_backward as mb  # noqa: E402
+
+
+def small_case(seed, T=6, d=8, F=5, E=4, k=2):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, d))
+    wr = rng.standard_normal((d, E)) * 0.5
+    wg = rng.standard_normal((E, d, F)) * 0.3
+    wu = rng.standard_normal((E, d, F)) * 0.3
+    wd = rng.standard_normal((E, F, d)) * 0.3
+    _, p = mb.moe_forward64(x, wr, wg, wu, wd, np.zeros((T, k), int))
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :k]
+    dout = rng.standard_normal((T, d))
+    return x, wr, wg, wu, wd, ids, dout
+
+
+@pytest.mark.parametrize("seed,aux_coef,k", [(0, 0.0, 2), (1, 0.7, 2), (2, 1.5, 1), (3, 0.3, 3)])
+def test_oracle_vs_finite_differences(seed, aux_coef, k):
+    x, wr, wg, wu, wd, ids, dout = small_case(seed, k=k)
+    E = wr.shape[1]
+    g = mb.moe_backward64(x, wr, wg, wu, wd, ids, dout, aux_coef)
+
+    def loss(args):
+        out, p = mb.moe_forward64(*args, ids)
+        return float(np.sum(dout * out)) + aux_coef * mb.aux_loss64(p, ids, E)[0]
+
+    rng = np.random.default_rng(100 + seed)
+    base = [x, wr, wg, wu, wd]
+    eps = 1e-6
+    for i, name in enumerate(("dx", "dwr", "dwg", "dwu", "dwd")):
+        for _ in range(6):
+            idx = tuple(int(rng.integers(0, n)) for n in base[i].shape)
+            plus = [a.copy() for a in base]
+            minus = [a.copy() for a in base]
+            plus[i][idx] += eps
+            minus[i][idx] -= eps
+            fd = (loss(plus) - loss(minus)) / (2 * eps)
+            assert abs(fd - g[name][idx]) <= 1e-7 + 1e-6 * abs(fd), (name, idx, fd, g[name][idx])
+
+
+def test_oracle_closed_forms():
+    """Uniform router (W_r = 0, every p = 1/E) and round-robin ids: f_e =
+    1/E, so aux = 1 exactly and its gradient on the logits vanishes; the
+    logit gradient of any case sums to zero per token."""
+    T, d, F, E, k = 8, 6, 4, 4, 1
+    x, _, wg, wu, wd, _, dout = small_case(7, T, d, F, E, k)
+    ids = (np.arange(T) % E)[:, None]
+    g = mb.moe_backward64(x, np.zeros((d, E)), wg, wu, wd, ids, np.zeros_like(dout), 2.0)
+    assert abs(g["aux"] - 1.0) < 1e-15
+    assert np.abs(g["dlogits"]).max() < 1e-15
+    x, wr, wg, wu, wd, ids, dout = small_case(8)
+    g = mb.moe_backward64(x, wr, wg, wu, wd, ids, dout, 0.5)
+    assert np.abs(g["dlogits"].sum(axis=1)).max() < 1e-12
+
+
+# ---------------------------------------------------------------- GPU
+def run_device_backward(d, F, E, k, T, seed, aux_coef, accumulate_twice=False):
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(seed, 0.1, 0.05)
+    wr, ex = orc.synth_layer_host(d, F, E, k, seed, 0.1, 0.05)
+    x = orc.synth((T, d), seed, 77, 1.0)
+    dout = orc.synth((T, d), seed, 78, 1.0)
+    dxd, dod = mh.DeviceArray.from_host(x), mh.DeviceArray.from_host(dout)
+    outs = dict(dx=mh.DeviceArray((T, d)), dwr=mh.DeviceArray((d, E)),
+                dwg=mh.DeviceArray((E, d, F)), dwu=mh.DeviceArray((E, d, F)),
+                dwd=mh.DeviceArray((E, F, d)))
+    aux = mh.DeviceArray((1,))
+    args = [outs[n].ptr for n in ("dx", "dwr", "dwg", "dwu", "dwd")]
+    layer.backward_dev(dxd.ptr, T, dod.ptr, aux_coef, *args, aux.ptr)
+    if accumulate_twice:
+        layer.backward_dev(dxd.ptr, T, dod.ptr, aux_coef, *args, aux.ptr, accumulate=1)
+    mh.synchronize()
+    res = {n: a.to_host() for n, a in outs.items()}
+    res["aux"] = float(aux.to_host()[0])
+    layer.close()
+    wg = np.stack([ex[e][0] for e in range(E)])
+    wu = np.stack([ex[e][1] for e in range(E)])
+    wd = np.stack([ex[e][2] for e in range(E)])
+    return res, x, dout, wr, wg, wu, wd
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(128, 512, 4, 2, 256), (256, 1024, 8, 2, 384),
+                                   (128, 256, 16, 4, 100)], ids=["c1", "c2-rows", "e16-k4"])
+@pytest.mark.parametrize("aux_coef", [0.0, 0.5])
+def test_backward_device_vs_oracle(shape, aux_coef):
+    d, F, E, k, T = shape
+    print(f"[gpu-test] backward d={d} F={F} E={E} k={k} T={T} aux={aux_coef}", flush=True)
+    res, x, dout, wr, wg, wu, wd = run_device_backward(d, F, E, k, T, 31, aux_coef)
+    hw_ids = orc.route(x, wr, k)[1]   # the fp32 forward's routing (bit-exact on the device)
+    g = mb.moe_backward64(x, wr, wg, wu, wd, hw_ids, dout, aux_coef)
+    for name in ("dx", "dwr", "dwg", "dwu", "dwd"):
+        rel = orc.rel_l2(res[name], g[name])
+        print(f"[gpu-test]   {name}: rel-L2 {rel:.3e}", flush=True)
+        assert rel <= 1e-5, name
+    assert abs(res["aux"] - g["aux"]) <= 1e-5 * max(1.0, abs(g["aux"]))
+
+
+@pytest.mark.gpu
+def test_backward_deterministic_and_accumulates():
+    """Same bits on a repeat; accumulate = 1 adds a second pass exactly."""
+    a, *_ = run_device_backward(128, 256, 4, 2, 200, 5, 0.3)
+    b, *_ = run_device_backward(128, 256, 4, 2, 200, 5, 0.3)
+    c, *_ = run_device_backward(128, 256, 4, 2, 200, 5, 0.3, accumulate_twice=True)
+    for name in ("dx", "dwr", "dwg", "dwu", "dwd"):
+        assert np.array_equal(a[name], b[name]), name
+        assert np.array_equal(c[name], a[name] + a[name]), name
