@@ -12,6 +12,8 @@ Also measured in the same run:
     cannot hold them), reported as MoE decode tokens/s and HBM GB/s;
   * prefill_batch8x512: the T=4096 (batch 8 x seq 512) layer, d=256,
     d_ff=1024, E=8, top-2, timed the same way;
+  * backward_batch8x512: the same layer's backward pass (every gradient and
+    the load-balancing loss);
   * decode_step: the whole block stack of that decode step (GQA attention
     over a 1024-position KV cache, then the MoE FFN sublayer, per block) with
     the residual stream on the device;
@@ -106,6 +108,32 @@ def prefill_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2):
     flops = 6.0 * T * k * d * F + 2.0 * T * d * E
     return dict(T=T, d=d, F=F, E=E, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3),
                 mfma_frac=flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
+
+
+def backward_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2, aux_coef=0.01):
+    """moe_hip_backward_dev on the batch-8 x seq-512 layer: the routing and
+    expert products recomputed, then every gradient and the aux loss.
+    Flops: 18 T k d F (G, U, Y, dH, dX and the three weight gradients)."""
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(2, 0.1, 0.02)
+    x = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(x.ptr, T * d, 2, 0, 0.0, 1.0)
+    dout = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(dout.ptr, T * d, 2, 1, 0.0, 1.0)
+    bufs = [mh.DeviceArray(sh) for sh in ((T, d), (d, E), (E, d, F), (E, d, F), (E, F, d))]
+    aux = mh.DeviceArray((1,))
+    run = lambda: layer.backward_dev(x.ptr, T, dout.ptr, aux_coef, *[b.ptr for b in bufs], aux.ptr)
+    for _ in range(max(warmup, 1)):
+        run()
+    mh.synchronize()
+    mh.timer_start()
+    for _ in range(steps):
+        run()
+    ms = mh.timer_stop() / steps
+    layer.close()
+    tflops = 18.0 * T * k * d * F / (ms * 1e-3) / 1e12
+    return dict(T=T, d=d, F=F, E=E, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3), tflops=tflops,
+                mfma_frac=tflops / PEAK_FP32_MFMA_TFLOPS)
 
 
 def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
@@ -299,7 +327,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "prefill_small", "decode", "decode_step", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "prefill_small", "backward", "decode", "decode_step", "copy"], default=None,
                     help="run one section only (for profiling); prints its JSON to stderr")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -325,6 +353,9 @@ def main():
     if args.only == "prefill_small":
         log("prefill_small", json.dumps(prefill_small(mh, args.steps, args.warmup)))
         return
+    if args.only == "backward":
+        log("backward", json.dumps(backward_small(mh, args.steps, args.warmup)))
+        return
     if args.only == "decode_step":
         log("decode_step", json.dumps(decode_step(mh, args.steps, args.warmup)))
         return
@@ -335,6 +366,8 @@ def main():
     log("prefill", json.dumps(pre))
     small = prefill_small(mh, args.steps, args.warmup)
     log("prefill_small", json.dumps(small))
+    bwd = backward_small(mh, args.steps, args.warmup)
+    log("backward", json.dumps(bwd))
     dec = stp = None
     if not args.no_decode:
         dec = decode(mh, args.steps, args.warmup)
@@ -384,6 +417,11 @@ def main():
         "workload": "moe prefill layer T=4096 (8 x 512) d=256 d_ff=1024 E=8 top-2",
         "tokens_per_s": small["tokens_per_s"], "ms_per_step": small["ms"],
         "layer_mfma_frac": small["mfma_frac"]}
+    line["backward_batch8x512"] = {
+        "workload": "moe layer backward + aux loss, T=4096 d=256 d_ff=1024 E=8 top-2 "
+                    "(routing and expert products recomputed)",
+        "ms_per_step": bwd["ms"], "tokens_per_s": bwd["tokens_per_s"],
+        "tflops": bwd["tflops"], "fp32_peak_frac": bwd["mfma_frac"]}
     if dec:
         line["decode"] = {
             "workload": "64 seqs x 1 token, 8 MoE layers d=512 d_ff=2048 E=16 top-2",

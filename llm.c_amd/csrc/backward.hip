@@ -28,6 +28,7 @@ namespace {
 
 constexpr int kRM = 128, kRN = 64, kRK = 16;   // rows_gemm tile
 constexpr int kQM = 64, kQN = 64, kQR = 16;    // reduce_gemm tile
+constexpr int kRouterChunk = 256;              // token rows per router-gradient partial
 
 // C[pos][n] (+)= sum_kk A(pos, kk) B_e(kk, n) for the rows pos of each
 // 128-row tile (expert e).  A(pos, kk) = a[arow * lda + kk] with arow =
@@ -158,15 +159,18 @@ struct ReduceGemm {
     size_t c_e;
     int ldc;
     const int *offsets;
-    int nrows, M, N, accumulate;
+    int nrows, chunk, M, N, accumulate, vec_a, vec_b;
 };
 
 template <bool GATHER>
 __global__ __launch_bounds__(256) void reduce_gemm_kernel(ReduceGemm g) {
     __shared__ __align__(16) float As[kQR][kQM + 4];
     __shared__ __align__(16) float Bs[kQR][kQN + 4];
+    // Groups: the experts' row ranges, or (no offsets) chunks of nrows rows
+    // of `chunk` each, whose partials go to C + z * c_e.
     const int e = blockIdx.z, m0 = blockIdx.y * kQM, n0 = blockIdx.x * kQN;
-    const int r0 = g.offsets ? g.offsets[e] : 0, r1 = g.offsets ? g.offsets[e + 1] : g.nrows;
+    const int r0 = g.offsets ? g.offsets[e] : e * g.chunk;
+    const int r1 = g.offsets ? g.offsets[e + 1] : min(g.nrows, (e + 1) * g.chunk);
     const int tid = threadIdx.x, tm = tid >> 4, tn = tid & 15;
     const int lr = tid >> 4, lq = 4 * (tid & 15);   // load row and column quad
     float acc[4][4];
@@ -179,10 +183,21 @@ __global__ __launch_bounds__(256) void reduce_gemm_kernel(ReduceGemm g) {
         const bool in = row < r1;
         float av[4], bv[4];
         const size_t arow = in ? (GATHER ? (size_t)(g.perm[row] / g.topk) : (size_t)row) : 0;
+        if (g.vec_a && in && m0 + lq < g.M) {   // (M, lda multiples of 4)
+            const float4 v = *reinterpret_cast<const float4 *>(g.a + arow * g.lda + m0 + lq);
+            av[0] = v.x; av[1] = v.y; av[2] = v.z; av[3] = v.w;
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            av[j] = in && m0 + lq + j < g.M ? g.a[arow * g.lda + m0 + lq + j] : 0.f;
-            bv[j] = in && n0 + lq + j < g.N ? g.b[(size_t)row * g.ldb + n0 + lq + j] : 0.f;
+            for (int j = 0; j < 4; ++j)
+                av[j] = in && m0 + lq + j < g.M ? g.a[arow * g.lda + m0 + lq + j] : 0.f;
+        }
+        if (g.vec_b && in && n0 + lq < g.N) {   // (N, ldb multiples of 4)
+            const float4 v = *reinterpret_cast<const float4 *>(g.b + (size_t)row * g.ldb + n0 + lq);
+            bv[0] = v.x; bv[1] = v.y; bv[2] = v.z; bv[3] = v.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                bv[j] = in && n0 + lq + j < g.N ? g.b[(size_t)row * g.ldb + n0 + lq + j] : 0.f;
         }
         __syncthreads();
         *reinterpret_cast<float4 *>(&As[lr][lq]) = make_float4(av[0], av[1], av[2], av[3]);
@@ -211,6 +226,16 @@ __global__ __launch_bounds__(256) void reduce_gemm_kernel(ReduceGemm g) {
             float *cp = ce + (size_t)m * g.ldc + n;
             *cp = g.accumulate ? *cp + acc[i][j] : acc[i][j];
         }
+    }
+}
+
+// C (+)= sum over z (in order) of P[z] for nz partials of n floats.
+__global__ __launch_bounds__(256) void sum_partials_kernel(const float *P, int nz, size_t n,
+                                                           int accumulate, float *C) {
+    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        float v = 0.f;
+        for (int z = 0; z < nz; ++z) v += P[(size_t)z * n + i];
+        C[i] = accumulate ? C[i] + v : v;
     }
 }
 
@@ -362,17 +387,27 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
                        b.dlogits, b.wr, T, d, E, k, b.accumulate, b.dx);
     // Weight gradients over each expert's rows; the router's over all tokens.
     auto reduce = [&](auto gather, const float *A, int lda, const float *B, int ldb, float *C,
-                      size_t c_e, int M, int N, const int *offsets, int nrows, int groups) {
-        ReduceGemm g{A, lda, b.perm, k, B, ldb, C, c_e, N, offsets, nrows, M, N, b.accumulate};
+                      size_t c_e, int M, int N, const int *offsets, int nrows, int chunk,
+                      int groups, int accumulate) {
+        ReduceGemm g{A, lda, b.perm, k, B, ldb, C, c_e, N, offsets, nrows, chunk, M, N,
+                     accumulate, M % 4 == 0 && lda % 4 == 0, N % 4 == 0 && ldb % 4 == 0};
         dim3 grid((unsigned)((N + kQN - 1) / kQN), (unsigned)((M + kQM - 1) / kQM),
                   (unsigned)groups);
         hipLaunchKernelGGL((reduce_gemm_kernel<decltype(gather)::value>), grid, dim3(256), 0, s,
                            g);
     };
-    reduce(F_{}, b.H, F, b.dY, d, b.dwd, (size_t)F * d, F, d, b.offsets, 0, E);
-    reduce(T_{}, b.x, d, b.G, F, b.dwg, (size_t)d * F, d, F, b.offsets, 0, E);
-    reduce(T_{}, b.x, d, b.U, F, b.dwu, (size_t)d * F, d, F, b.offsets, 0, E);
-    reduce(F_{}, b.x, d, b.dlogits, E, b.dwr, 0, d, E, nullptr, T, 1);
+    reduce(F_{}, b.H, F, b.dY, d, b.dwd, (size_t)F * d, F, d, b.offsets, 0, 0, E, b.accumulate);
+    reduce(T_{}, b.x, d, b.G, F, b.dwg, (size_t)d * F, d, F, b.offsets, 0, 0, E, b.accumulate);
+    reduce(T_{}, b.x, d, b.U, F, b.dwu, (size_t)d * F, d, F, b.offsets, 0, 0, E, b.accumulate);
+    // The router's over all tokens, in chunks of kRouterChunk rows whose
+    // partials (in dH, free by now) are then added in chunk order.
+    // (at most n F / (d E) partials fit in dH)
+    const size_t fit = std::max<size_t>(1, n * F / ((size_t)d * E));
+    const int chunk = (int)std::max<size_t>(kRouterChunk, (T + fit - 1) / fit);
+    const int nz = (T + chunk - 1) / chunk;
+    reduce(F_{}, b.x, d, b.dlogits, E, b.dH, (size_t)d * E, d, E, nullptr, T, chunk, nz, 0);
+    hipLaunchKernelGGL(sum_partials_kernel, dim3(blocks_for((size_t)d * E)), dim3(256), 0, s,
+                       b.dH, nz, (size_t)d * E, b.accumulate, b.dwr);
     if (b.aux)
         hipLaunchKernelGGL(aux_kernel, dim3(1), dim3(256), 0, s, b.probs, b.counts, T, E, k,
                            b.aux);

@@ -329,10 +329,14 @@ __global__ __launch_bounds__(256) void combine_groups_kernel(CombineArgs a) {
 // Packs source matrix src [K x N] (reference layout) into the unit layout
 // (unpack != 0: the inverse).  Source column c goes to packed row
 // c (mode 0, down), 64*(c/32) + c%32 (mode 1, gate) or that + 32 (mode 2,
-// up).  One workgroup moves a 32 x 32 block = 4 units through LDS.
+// up).  One workgroup moves a 32 x 32 block = 4 units through LDS; grid z
+// runs over experts whose matrices are src_e and dst_e floats apart.
 __global__ __launch_bounds__(256) void pack_kernel(float *src, float *dst, int K, int N,
-                                                    int mode, int unpack) {
+                                                    int mode, int unpack, size_t src_e = 0,
+                                                    size_t dst_e = 0) {
     __shared__ float tile[32][33];
+    src += blockIdx.z * src_e;
+    dst += blockIdx.z * dst_e;
     const int c0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
     const int row0 = mode == 0 ? c0 : 64 * (c0 >> 5) + (mode == 2 ? 32 : 0);
@@ -425,6 +429,19 @@ hipError_t launch_unpack_gateup(const float *src, float *wg, float *wu, int d, i
     dim3 grid(F / 32, d / 32);
     hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, wg, const_cast<float *>(src), d, F, 1, 1);
     hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, s, wu, const_cast<float *>(src), d, F, 2, 1);
+    return hipGetLastError();
+}
+
+hipError_t launch_unpack_experts(const float *wgu, const float *wdT, float *wg, float *wu,
+                                 float *wd, int E, int d, int F, hipStream_t s) {
+    const size_t dF = (size_t)d * F;
+    dim3 ggu(F / 32, d / 32, E), gdn(d / 32, F / 32, E);
+    hipLaunchKernelGGL(pack_kernel, ggu, dim3(256), 0, s, wg, const_cast<float *>(wgu), d, F, 1, 1,
+                       dF, 2 * dF);
+    hipLaunchKernelGGL(pack_kernel, ggu, dim3(256), 0, s, wu, const_cast<float *>(wgu), d, F, 2, 1,
+                       dF, 2 * dF);
+    hipLaunchKernelGGL(pack_kernel, gdn, dim3(256), 0, s, wd, const_cast<float *>(wdT), F, d, 0, 1,
+                       dF, dF);
     return hipGetLastError();
 }
 

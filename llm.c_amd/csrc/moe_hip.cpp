@@ -1018,11 +1018,7 @@ int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dou
     const size_t dF = (size_t)d * F;
     TRY(g_ws.bw.reserve(sizeof(float) * 3 * E * dF));
     float *wg = g_ws.bw.as<float>(), *wu = wg + E * dF, *wd = wu + E * dF;
-    for (int e = 0; e < E; ++e) {
-        HIP_TRY(moe::launch_unpack_gateup(L->wgu + (size_t)e * 2 * dF, wg + e * dF, wu + e * dF, d,
-                                          F, s));
-        HIP_TRY(moe::launch_unpack_down(L->wdT + (size_t)e * dF, wd + e * dF, F, d, s));
-    }
+    HIP_TRY(moe::launch_unpack_experts(L->wgu, L->wdT, wg, wu, wd, E, d, F, s));
     // Workspace: G, U, H, dH [n x F]; Y, dY [n x d]; dgw, inv [n]; dlogits [T x E].
     const size_t nF = n * F, nd = n * d;
     TRY(g_ws.bwork.reserve(sizeof(float) * (4 * nF + 2 * nd + 2 * n + (size_t)T * E)));

@@ -139,6 +139,9 @@ hipError_t launch_unpack_gateup(const float *src, float *wg, float *wu, int d,
                                 int F, hipStream_t s);
 hipError_t launch_unpack_down(const float *src, float *wd, int F, int d,
                               hipStream_t s);
+// All E experts at once: wg, wu [E][d x F], wd [E][F x d].
+hipError_t launch_unpack_experts(const float *wgu, const float *wdT, float *wg, float *wu,
+                                 float *wd, int E, int d, int F, hipStream_t s);
 // The attention half of a decode step for B sequences (attention.hip).
 struct AttnArgs {
     float *x;               // [B x d] residual stream: x += Attn(rms_norm(x))
