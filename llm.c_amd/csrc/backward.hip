@@ -142,6 +142,128 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(RowsGemm g) {
     }
 }
 
+// The same product on the matrix cores (v_mfma_f32_32x32x2f32): a 128 x 64
+// tile per workgroup of two waves, wave w rows 64w .. 64w + 63 and all 64
+// columns (2 x 2 blocks of 32 x 32).  K slices of 32 sit in LDS with K
+// contiguous per row (As) and per column (Bs); lane (li, lh) = (l % 32,
+// l / 32) feeds k = 16 lh + 4q + s of MFMA (q, s), as in the forward's
+// grouped GEMM.  The next slice is loaded into registers while the MFMAs
+// of this one run.
+typedef float fx4 __attribute__((ext_vector_type(4)));
+typedef float fx16 __attribute__((ext_vector_type(16)));
+constexpr int kMK = 32, kMLd = kMK + 4;
+
+template <bool GATHER, bool BT>
+__global__ __launch_bounds__(128) void rows_mfma_kernel(RowsGemm g) {
+    __shared__ __align__(16) float As[kRM][kMLd];
+    __shared__ __align__(16) float Bs[kRN][kMLd];
+    const int ntn = (g.N + kRN - 1) / kRN;
+    const int nt = blockIdx.x % ntn, mtg = blockIdx.x / ntn;
+    if (mtg >= g.tile_off[g.E]) return;
+    const int e = g.tile_expert[mtg];
+    const int row0 = g.offsets[e] + (mtg - g.tile_off[e]) * kRM;
+    const int rows = min(kRM, g.offsets[e + 1] - row0);
+    const int n0 = nt * kRN;
+    const int tid = threadIdx.x, lane = tid & 63, wm = tid >> 6;
+    const int li = lane & 31, lh = lane >> 5;
+    const fx4 zero = {0.f, 0.f, 0.f, 0.f};
+
+    // A: 128 rows x 8 k-quads = 1024 float4s, 8 per thread.
+    const float *asrc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int q = tid + 128 * i, r = min(q >> 3, rows - 1);
+        const size_t src = GATHER ? (size_t)(g.perm[row0 + r] / g.topk) : (size_t)(row0 + r);
+        asrc[i] = g.a + src * g.lda + 4 * (q & 7);
+    }
+    const float *bb = g.b + (size_t)e * g.b_e;
+    fx4 ra[8], rb[4];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const fx4 *>(asrc[i] + k0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 128 * i;
+            if (BT) {   // 64 columns x 8 k-quads
+                const int n = n0 + (q >> 3);
+                rb[i] = n < g.N ? *reinterpret_cast<const fx4 *>(bb + (size_t)n * g.ldb + k0 +
+                                                                   4 * (q & 7))
+                                : zero;
+            } else {    // 32 k rows x 16 column quads
+                const int n = n0 + 4 * (q & 15);
+                rb[i] = n < g.N ? *reinterpret_cast<const fx4 *>(bb + (size_t)(k0 + (q >> 4)) *
+                                                                           g.ldb + n)
+                                : zero;
+            }
+        }
+    };
+    auto sstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = tid + 128 * i;
+            *reinterpret_cast<fx4 *>(&As[q >> 3][4 * (q & 7)]) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = tid + 128 * i;
+            if (BT) {
+                *reinterpret_cast<fx4 *>(&Bs[q >> 3][4 * (q & 7)]) = rb[i];
+            } else {
+                const int k = q >> 4, n = 4 * (q & 15);
+                Bs[n][k] = rb[i][0];
+                Bs[n + 1][k] = rb[i][1];
+                Bs[n + 2][k] = rb[i][2];
+                Bs[n + 3][k] = rb[i][3];
+            }
+        }
+    };
+    fx16 acc[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.f;
+    const int nk = g.K / kMK;
+    gload(0);
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kt > 0) __syncthreads();   // this slice's LDS is free
+        sstore();
+        __syncthreads();
+        if (kt + 1 < nk) gload((kt + 1) * kMK);
+        const float *as = &As[wm * 64 + li][16 * lh];
+        const float *bs = &Bs[li][16 * lh];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const fx4 a0 = *reinterpret_cast<const fx4 *>(as + 4 * q);
+            const fx4 a1 = *reinterpret_cast<const fx4 *>(as + 32 * kMLd + 4 * q);
+            const fx4 b0 = *reinterpret_cast<const fx4 *>(bs + 4 * q);
+            const fx4 b1 = *reinterpret_cast<const fx4 *>(bs + 32 * kMLd + 4 * q);
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s2], b0[s2], acc[0][0], 0, 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s2], b1[s2], acc[0][1], 0, 0, 0);
+                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s2], b0[s2], acc[1][0], 0, 0, 0);
+                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s2], b1[s2], acc[1][1], 0, 0, 0);
+            }
+        }
+    }
+    // Block (m, n), register r: row 8 (r / 4) + 4 lh + r % 4, column li.
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            if (row >= rows) continue;
+            float *cr = g.c + (size_t)(row0 + row) * g.ldc;
+#pragma unroll
+            for (int n = 0; n < 2; ++n) {
+                const int col = n0 + n * 32 + li;
+                if (col < g.N) cr[col] = g.accumulate ? cr[col] + acc[m][n][r] : acc[m][n][r];
+            }
+        }
+}
+
 // C_e[m][n] (+)= sum over the rows pos of group e (offsets[e] ..
 // offsets[e + 1], or 0 .. nrows without offsets) of A(pos, m) B(pos, n),
 // A(pos, m) = a[arow * lda + m] (arow = perm[pos] / topk with GATHER),
@@ -360,8 +482,12 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         RowsGemm g{A, lda, b.perm, k, B, b_e, ldb, C, N, b.offsets, b.tile_off, b.tile_expert,
                    E, K, N, b.max_mtiles, accumulate};
         const unsigned grid = (unsigned)(b.max_mtiles * ((N + kRN - 1) / kRN));
-        hipLaunchKernelGGL((rows_gemm_kernel<decltype(gather)::value, decltype(bt)::value>),
-                           dim3(grid), dim3(256), 0, s, g);
+        if (K % kMK == 0)
+            hipLaunchKernelGGL((rows_mfma_kernel<decltype(gather)::value, decltype(bt)::value>),
+                               dim3(grid), dim3(128), 0, s, g);
+        else
+            hipLaunchKernelGGL((rows_gemm_kernel<decltype(gather)::value, decltype(bt)::value>),
+                               dim3(grid), dim3(256), 0, s, g);
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
