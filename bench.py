@@ -110,6 +110,26 @@ def prefill_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2):
                 mfma_frac=flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
 
 
+def dropin_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2):
+    """The host-pointer drop-in moe_forward (x in host memory, out, probs and
+    ids back to host memory) on the batch-8 x seq-512 layer: the
+    PCIe-inclusive rate.  Weights become device-resident on the first call."""
+    import abi_types
+    rng = np.random.default_rng(4)
+    f = lambda *sh, sd: (sd * rng.standard_normal(sh)).astype(np.float32)
+    hw = abi_types.HostMoE(f(d, E, sd=0.1), f(E, d, F, sd=0.02), f(E, d, F, sd=0.02),
+                           f(E, F, d, sd=0.02), k)
+    x = f(T, d, sd=1.0)
+    for _ in range(max(warmup, 1)):
+        mh.moe_forward(x, hw)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        mh.moe_forward(x, hw)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    pcie_bytes = 4.0 * T * (2 * d + E + k)
+    return dict(T=T, ms=ms, tokens_per_s=T / (ms * 1e-3), pcie_bytes=pcie_bytes)
+
+
 def backward_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2, aux_coef=0.01):
     """moe_hip_backward_dev on the batch-8 x seq-512 layer: the routing and
     expert products recomputed, then every gradient and the aux loss.
@@ -293,17 +313,28 @@ def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=
     return res
 
 
-def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, budget_s=15.0):
-    """Oracle moe_forward on the first tokens of the prefill workload, all
-    host cores, until ~budget_s of CPU work; tokens/s extrapolates linearly
-    (tokens are independent in the reference loop, src/transformer.c:312)."""
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, budget_s=15.0, threads=None):
+    """Oracle moe_forward on the first tokens of the prefill workload, `threads`
+    host threads (all cores by default), until ~budget_s of CPU work;
+    tokens/s extrapolates linearly (tokens are independent in the reference
+    loop, src/transformer.c:312)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     layer, ids = st["layer"], st["ids"]
     wr = layer.get_router()
     xh = st["x"].to_host()
-    threads = os.cpu_count() or 1
-    ex = {}
+    threads = threads or os.cpu_count() or 1
+    ex = st.setdefault("host_experts", {})
     done, secs = 0, 0.0
     chunk = max(threads, 16)
     while secs < budget_s and done < T:
@@ -317,7 +348,31 @@ def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, budget_s=15.0):
         done = rows.stop
     return dict(value=done / secs, unit="tokens/s", cores=threads, kind="port",
                 sample=f"first {done} of {T} tokens of the same prefill layer "
-                       f"({secs:.1f} s of oracle time, {threads} threads)")
+                       f"({secs:.1f} s of oracle time, {threads} threads, {cpu_model()})")
+
+
+def cpu_decode_baseline(mh, T=64, d=512, F=2048, E=16, k=2, n_layers=8):
+    """Oracle moe_forward on the 64 decode rows of one layer (all experts
+    host-resident), all host threads; decode tokens/s = 64 / (8 layers x
+    that time)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import orc
+    L = mh.Layer(d, F, E, k)
+    L.fill_synthetic(100, 0.02, 0.02)
+    ex = {e: L.get_expert(e) for e in range(E)}
+    wr = L.get_router()
+    L.close()
+    x = np.random.default_rng(3).standard_normal((T, d)).astype(np.float32)
+    threads = os.cpu_count() or 1
+    orc.moe_forward_experts(x, wr, ex, d, F, E, k, None, nthreads=threads)
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        orc.moe_forward_experts(x, wr, ex, d, F, E, k, None, nthreads=threads)
+    layer_s = (time.perf_counter() - t0) / reps
+    return dict(value=T / (n_layers * layer_s), unit="tokens/s", cores=threads, kind="port",
+                sample=f"one MoE layer on the 64 decode rows, x{n_layers} layers "
+                       f"({layer_s * 1e3:.1f} ms per layer, {threads} threads, {cpu_model()})")
 
 
 def main():
@@ -368,16 +423,22 @@ def main():
     log("prefill_small", json.dumps(small))
     bwd = backward_small(mh, args.steps, args.warmup)
     log("backward", json.dumps(bwd))
+    dropin = dropin_small(mh, args.steps, args.warmup)
+    log("dropin", json.dumps(dropin))
     dec = stp = None
     if not args.no_decode:
         dec = decode(mh, args.steps, args.warmup)
         log("decode", json.dumps(dec))
         stp = decode_step(mh, args.steps, args.warmup)
         log("decode_step", json.dumps(stp))
-    cpu = None
+    cpu = cpu1 = cpu_dec = None
     if not args.no_cpu:
         cpu = cpu_baseline(mh, st)
         log("cpu", json.dumps(cpu))
+        cpu1 = cpu_baseline(mh, st, budget_s=5.0, threads=1)
+        log("cpu 1 thread", json.dumps(cpu1))
+        cpu_dec = cpu_decode_baseline(mh)
+        log("cpu decode", json.dumps(cpu_dec))
 
     ms = pre["ms"]
     gu_tflops = pre["gateup_tflops"]
@@ -412,11 +473,16 @@ def main():
                                      pre["phase_ms"])),
         "expert_load_max_over_mean": pre["counts_max_over_mean"],
         "cpu_baseline": cpu,
+        "cpu_baseline_1thread": cpu1,
     }
     line["prefill_batch8x512"] = {
         "workload": "moe prefill layer T=4096 (8 x 512) d=256 d_ff=1024 E=8 top-2",
         "tokens_per_s": small["tokens_per_s"], "ms_per_step": small["ms"],
         "layer_mfma_frac": small["mfma_frac"]}
+    line["prefill_batch8x512_host_dropin"] = {
+        "workload": "moe_forward with host x / out / probs / ids (PCIe included), same layer",
+        "tokens_per_s": dropin["tokens_per_s"], "ms_per_step": dropin["ms"],
+        "pcie_bytes_per_call": dropin["pcie_bytes"]}
     line["backward_batch8x512"] = {
         "workload": "moe layer backward + aux loss, T=4096 d=256 d_ff=1024 E=8 top-2 "
                     "(routing and expert products recomputed)",
@@ -432,6 +498,7 @@ def main():
             "experts_gbs": dec["experts_gbs"],
             # (per-phase HIP events add a few microseconds to each phase)
             "phase_ms_per_layer": dec["phase_ms"],
+            "cpu_baseline": cpu_dec,
         }
     if stp:
         line["decode_step"] = {
