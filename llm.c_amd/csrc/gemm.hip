@@ -371,17 +371,31 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(float *dst, size_t n, 
 }  // namespace
 
 GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split) {
-    constexpr int kTarget = 512;   // workgroups: two per CU
+    // Waves in flight for tile width bn (bn / 32 waves per workgroup) and
+    // split ks; aim for ~4 per SIMD.  Wider tiles reuse each loaded tile
+    // across more waves, so they shrink only to 128 columns, and only tiny
+    // grids go to 64; splits (whose partials the combine adds) stop at 4.
+    constexpr size_t kTarget = 1024;
+    auto waves = [&](int bn, int ks) { return (size_t)max_mtiles * (N / bn) * ks * (bn / 32); };
     GemmPlan p{0, 1};
     if (N % 256 == 0) p.bn = 256;
     else if (N % 128 == 0) p.bn = 128;
     else if (N % 64 == 0) p.bn = 64;
     else return p;
-    while (p.bn > 64 && (size_t)max_mtiles * (N / p.bn) < kTarget) p.bn /= 2;
-    if (allow_split)
-        while (p.ksplit < 8 && (size_t)max_mtiles * (N / p.bn) * p.ksplit < kTarget &&
-               K % (2 * p.ksplit * KT) == 0 && K / (2 * p.ksplit) >= 128)
-            p.ksplit *= 2;
+    while (p.bn > 128 && waves(p.bn, 1) < kTarget) p.bn /= 2;
+    auto split = [&](int bn) {
+        int ks = 1;
+        if (allow_split)
+            while (ks < 4 && waves(bn, ks) < kTarget && K % (2 * ks * KT) == 0 &&
+                   K / (2 * ks) >= 128)
+                ks *= 2;
+        return ks;
+    };
+    p.ksplit = split(p.bn);
+    if (p.bn > 64 && waves(p.bn, p.ksplit) < kTarget / 4 && N % 64 == 0) {
+        p.bn = 64;
+        p.ksplit = split(64);
+    }
     return p;
 }
 

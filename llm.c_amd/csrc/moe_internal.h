@@ -211,8 +211,7 @@ hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed,
                               hipStream_t s);
 
 // Tile width (64, 128 or 256 columns) and reduction split of a grouped GEMM
-// launch: the widest tile dividing N that still gives ~512 workgroups, then
-// (down projection) the split of K that gets there.
+// launch, sized for ~1024 waves in flight (gemm.hip).
 struct GemmPlan {
     int bn, ksplit;
 };
