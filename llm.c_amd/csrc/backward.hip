@@ -282,6 +282,9 @@ struct ReduceGemm {
     int ldc;
     const int *offsets;
     int nrows, chunk, M, N, accumulate, vec_a, vec_b;
+    // B read from [G | U] in the packed gate/up column order: column n of
+    // the gate (0) or up (1) half is 64 (n / 32) + n % 32 + 32 b_gu; -1: plain.
+    int b_gu = -1;
 };
 
 template <bool GATHER>
@@ -351,6 +354,77 @@ __global__ __launch_bounds__(256) void reduce_gemm_kernel(ReduceGemm g) {
     }
 }
 
+// The same product on the matrix cores for M, N multiples of 64 and the
+// experts' row ranges: a 64 x 64 tile per workgroup, 4 waves of 32 x 32
+// (v_mfma_f32_32x32x2f32; lane half h feeds rows 2i + h of the slice).  Rows
+// go through LDS in double-buffered slices of 32, the next slice's loads in
+// registers while the current one is multiplied; rows past the range load
+// as zeros.  Row stride 96: the two half-waves' rows fall in disjoint banks.
+constexpr int kMR = 32, kMT = 64, kMLD = 96;
+
+template <bool GATHER>
+__global__ __launch_bounds__(256) void reduce_mfma_kernel(ReduceGemm g) {
+    __shared__ __align__(16) float As[2][kMR][kMLD];
+    __shared__ __align__(16) float Bs[2][kMR][kMLD];
+    const int e = blockIdx.z, m0 = blockIdx.y * kMT, n0 = blockIdx.x * kMT;
+    const int r0 = g.offsets[e], r1 = g.offsets[e + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, li = lane & 31, lh = lane >> 5;
+    const int lr = tid >> 4, lq = 4 * (tid & 15);   // load rows lr, lr + 16; column quad
+    const int bcol = g.b_gu < 0 ? n0 + lq : 64 * ((n0 + lq) >> 5) + ((n0 + lq) & 31) + 32 * g.b_gu;
+    fx4 ra[2], rb[2];
+    auto gload = [&](int r) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = r + lr + 16 * i;
+            if (row < r1) {
+                const size_t arow = GATHER ? (size_t)(g.perm[row] / g.topk) : (size_t)row;
+                ra[i] = *reinterpret_cast<const fx4 *>(g.a + arow * g.lda + m0 + lq);
+                rb[i] = *reinterpret_cast<const fx4 *>(g.b + (size_t)row * g.ldb + bcol);
+            } else {
+                ra[i] = fx4{0.f, 0.f, 0.f, 0.f};
+                rb[i] = fx4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            *reinterpret_cast<fx4 *>(&As[buf][lr + 16 * i][lq]) = ra[i];
+            *reinterpret_cast<fx4 *>(&Bs[buf][lr + 16 * i][lq]) = rb[i];
+        }
+    };
+    fx16 acc;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+    if (r0 < r1) {
+        gload(r0);
+        sstore(0);
+        __syncthreads();
+        int buf = 0;
+        for (int r = r0; r < r1; r += kMR, buf ^= 1) {
+            const bool more = r + kMR < r1;
+            if (more) gload(r + kMR);
+#pragma unroll
+            for (int kk = 0; kk < kMR; kk += 2)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[buf][kk + lh][wm * 32 + li],
+                                                           Bs[buf][kk + lh][wn * 32 + li], acc,
+                                                           0, 0, 0);
+            if (more) sstore(buf ^ 1);
+            __syncthreads();
+        }
+    }
+    // Lane l, register q: row 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32.
+    float *ce = g.c + (size_t)e * g.c_e;
+    const int n = n0 + wn * 32 + li;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int m = m0 + wm * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
+        float *cp = ce + (size_t)m * g.ldc + n;
+        *cp = g.accumulate ? *cp + acc[q] : acc[q];
+    }
+}
+
 // C (+)= sum over z (in order) of P[z] for nz partials of n floats.
 __global__ __launch_bounds__(256) void sum_partials_kernel(const float *P, int nz, size_t n,
                                                            int accumulate, float *C) {
@@ -379,22 +453,36 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(float *G, float *U, con
     }
 }
 
+// Where an expert GEMM left its [T k x d] rows: by dispatch position, or by
+// slot as ns partials ys apart (summed in order).
+struct SlotRows {
+    const float *p;
+    int by_slot, ns;
+    size_t ys;
+    __device__ float at(int pos, int a, int d, int c) const {
+        const float *r = p + (size_t)(by_slot ? a : pos) * d + c;
+        float v = r[0];
+        for (int s = 1; s < ns; ++s) v += r[(size_t)s * ys];
+        return v;
+    }
+};
+
 // One wave per dispatch position pos (slot a = perm[pos], token t = a / k):
-// dgw[a] = <Y[pos], dout[t]> (lane-strided partial sums, then a butterfly),
+// dgw[a] = <Y(a), dout[t]> (lane-strided partial sums, then a butterfly),
 // dY[pos] = gw[a] dout[t], inv[a] = pos.
-__global__ __launch_bounds__(256) void slot_kernel(const float *Y, const float *dout,
+__global__ __launch_bounds__(256) void slot_kernel(SlotRows Y, const float *dout,
                                                    const float *gw, const int *perm, int k, int d,
                                                    int n, float *dgw, float *dY, int *inv) {
     const int pos = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (pos >= n) return;
     const int a = perm[pos], t = a / k;
     const float w = gw[a];
-    const float *y = Y + (size_t)pos * d, *go = dout + (size_t)t * d;
+    const float *go = dout + (size_t)t * d;
     float *dy = dY + (size_t)pos * d;
     float s = 0.f;
     for (int c = lane; c < d; c += 64) {
         const float v = go[c];
-        s = fmaf(y[c], v, s);
+        s = fmaf(Y.at(pos, a, d, c), v, s);
         dy[c] = w * v;
     }
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
@@ -431,52 +519,87 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, con
     for (int e = 0; e < E; ++e) dlogits[(size_t)t * E + e] = p[e] * (dp(e) - dot);
 }
 
-// dx[t][c] = sum over slots (in order) of dXr[inv[t k + s]][c], plus
-// sum_e dlogits[t][e] wr[c][e].
-__global__ __launch_bounds__(256) void dx_kernel(const float *dXr, const int *inv,
-                                                 const float *dlogits, const float *wr, int T,
+// dx[t][c..c+3] = sum over slots (in order) of dXr(t k + s), plus
+// sum_e dlogits[t][e] wr[c][e] (read from wrT [E x d]); one thread per 4
+// columns (d % 4 == 0).
+__global__ __launch_bounds__(256) void dx_kernel(SlotRows dXr, const int *inv,
+                                                 const float *dlogits, const float *wrT, int T,
                                                  int d, int E, int k, int accumulate, float *dx) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (size_t)T * d) return;
-    const int t = (int)(i / d), c = (int)(i % d);
-    float v = 0.f;
-    for (int s = 0; s < k; ++s) v += dXr[(size_t)inv[(size_t)t * k + s] * d + c];
-    float r = 0.f;
-    for (int e = 0; e < E; ++e) r = fmaf(dlogits[(size_t)t * E + e], wr[(size_t)c * E + e], r);
-    v += r;
-    dx[i] = accumulate ? dx[i] + v : v;
+    const int d4 = d / 4;
+    if (i >= (size_t)T * d4) return;
+    const int t = (int)(i / d4), c = 4 * (int)(i % d4);
+    fx4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < k; ++s) {
+        const int a = t * k + s;
+        const float *r = dXr.p + (size_t)(dXr.by_slot ? a : inv[a]) * d + c;
+        fx4 y = *reinterpret_cast<const fx4 *>(r);
+        for (int z = 1; z < dXr.ns; ++z) y += *reinterpret_cast<const fx4 *>(r + (size_t)z * dXr.ys);
+        v += y;
+    }
+    fx4 rr = {0.f, 0.f, 0.f, 0.f};
+    const float *dl = dlogits + (size_t)t * E;
+    for (int e = 0; e < E; ++e) {
+        const float g = dl[e];
+        const fx4 w = *reinterpret_cast<const fx4 *>(wrT + (size_t)e * d + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rr[j] = fmaf(g, w[j], rr[j]);
+    }
+    v += rr;
+    fx4 *o = reinterpret_cast<fx4 *>(dx + (size_t)t * d + c);
+    *o = accumulate ? *o + v : v;
 }
 
-// aux = E * sum_e (counts[e] / (T k)) * (sum_t probs[t][e] / T), one
-// workgroup: per expert a strided sum and a fixed tree.
-__global__ __launch_bounds__(256) void aux_kernel(const float *probs, const int *counts, int T,
-                                                  int E, int k, float *aux) {
+// aux = E * sum_e (counts[e] / (T k)) * (sum_t probs[t][e] / T): workgroup
+// e sums column e (thread-strided sums, then a fixed tree) into colsum[e];
+// aux_final adds the terms in expert order.
+__global__ __launch_bounds__(256) void aux_cols_kernel(const float *probs, int T, int E,
+                                                       float *colsum) {
     __shared__ float red[256];
-    float total = 0.f;
-    for (int e = 0; e < E; ++e) {
-        float s = 0.f;
-        for (int t = threadIdx.x; t < T; t += 256) s += probs[(size_t)t * E + e];
-        red[threadIdx.x] = s;
-        __syncthreads();
-        for (int w = 128; w >= 1; w >>= 1) {
-            if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-            __syncthreads();
-        }
-        total = fmaf((float)counts[e] / ((float)T * (float)k), red[0] / (float)T, total);
+    const int e = blockIdx.x;
+    float s = 0.f;
+    for (int t = threadIdx.x; t < T; t += 256) s += probs[(size_t)t * E + e];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x == 0) *aux = (float)E * total;
+    if (threadIdx.x == 0) colsum[e] = red[0];
+}
+
+__global__ __launch_bounds__(64) void aux_final_kernel(const float *colsum, const int *counts,
+                                                       int T, int E, int k, float *aux) {
+    if (threadIdx.x != 0) return;
+    float total = 0.f;
+    for (int e = 0; e < E; ++e)
+        total = fmaf((float)counts[e] / ((float)T * (float)k), colsum[e] / (float)T, total);
+    *aux = (float)E * total;
 }
 
 unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 16384); }
 
+#define BWD_TRY(x)                               \
+    do {                                         \
+        hipError_t e_ = (x);                     \
+        if (e_ != hipSuccess) return e_;         \
+    } while (0)
+
 }  // namespace
+
+bool backward_engine_ok(int d, int F) { return d % 64 == 0 && F % 64 == 0; }
+
+int backward_slot_splits(int d, int F, int max_mtiles) {
+    if (!backward_engine_ok(d, F)) return 1;
+    return std::max(gemm_plan(d, F, max_mtiles, true).ksplit,
+                    gemm_plan(d, 2 * F, max_mtiles, true).ksplit);
+}
 
 hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
     const int d = b.d, F = b.F, E = b.E, k = b.k, T = b.T;
     const size_t n = (size_t)T * k;
     if (T <= 0) return hipSuccess;
-    if (d % 16 || F % 16) return hipErrorInvalidValue;
+    if (d % 16 || F % 16) return hipErrorInvalidValue;   // (dx_kernel: d % 4)
     auto rows = [&](auto gather, auto bt, const float *A, int lda, const float *B, size_t b_e,
                     int ldb, float *C, int K, int N, int accumulate) {
         RowsGemm g{A, lda, b.perm, k, B, b_e, ldb, C, N, b.offsets, b.tile_off, b.tile_expert,
@@ -491,26 +614,64 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
     };
     using T_ = std::true_type;
     using F_ = std::false_type;
-    // Recompute: G, U (gathered x rows), H, Y.
-    rows(T_{}, F_{}, b.x, d, b.wg, (size_t)d * F, F, b.G, d, F, 0);
-    rows(T_{}, F_{}, b.x, d, b.wu, (size_t)d * F, F, b.U, d, F, 0);
-    hipLaunchKernelGGL(act_kernel, dim3(blocks_for(n * F)), dim3(256), 0, s, b.G, b.U, b.H,
-                       n * F);
-    rows(F_{}, F_{}, b.H, F, b.wd, (size_t)F * d, d, b.Y, F, d, 0);
-    // Slots: dgw, dY, the slot -> position map.
-    hipLaunchKernelGGL(slot_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, b.Y, b.dout,
-                       b.gw, b.perm, k, d, (int)n, b.dgw, b.dY, b.inv);
-    // Experts: dH, dG and dU (in place over G, U), dXr (over Y).
-    rows(F_{}, T_{}, b.dY, d, b.wd, (size_t)F * d, d, b.dH, d, F, 0);
-    hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(blocks_for(n * F)), dim3(256), 0, s, b.G, b.U,
-                       b.dH, n * F);
-    rows(F_{}, T_{}, b.G, F, b.wg, (size_t)d * F, F, b.Y, F, d, 0);
-    rows(F_{}, T_{}, b.U, F, b.wu, (size_t)d * F, F, b.Y, F, d, 1);
+    const size_t nd = n * d;
+    const unsigned slot_grid = (unsigned)((n + 3) / 4);
+    SlotRows dXr{b.Y, 0, 1, 0};
+    if (b.wgu) {
+        // The forward's tile engine on the packed weights and their unit
+        // transposes; G and U adjacent as GU [n x 2F] in packed column order.
+        float *GU = b.G;
+        BWD_TRY(launch_transpose_units(b.wdT, b.wdTT, d, F, E, s));
+        BWD_TRY(launch_transpose_units(b.wgu, b.wguT, 2 * F, d, E, s));
+        GemmArgs g{};
+        g.perm = b.perm; g.topk = k; g.offsets = b.offsets; g.tile_off = b.tile_off;
+        g.tile_expert = b.tile_expert; g.E = E; g.max_mtiles = b.max_mtiles;
+        // Recompute GU and H, then Y by slot (split partials).
+        GemmArgs gu = g;
+        gu.a = b.x; gu.b = b.wgu; gu.c = GU; gu.K = d; gu.N = 2 * F; gu.ldc = 2 * F;
+        gu.c2 = b.H; gu.ldc2 = F;
+        BWD_TRY(launch_gemm_bwd(gu, 2, s));
+        const GemmPlan py = gemm_plan(d, F, b.max_mtiles, true);
+        GemmArgs gy = g;
+        gy.a = b.H; gy.b = b.wdT; gy.c = b.Y; gy.K = F; gy.N = d; gy.ldc = d;
+        gy.ksplit = py.ksplit; gy.split_stride = nd;
+        BWD_TRY(launch_gemm_down(gy, s));
+        hipLaunchKernelGGL(slot_kernel, dim3(slot_grid), dim3(256), 0, s,
+                           SlotRows{b.Y, 1, py.ksplit, nd}, b.dout, b.gw, b.perm, k, d, (int)n,
+                           b.dgw, b.dY, b.inv);
+        // dH -> dG, dU in place over GU; dXr = dGU wgu^T by slot (over Y).
+        GemmArgs gh = g;
+        gh.a = b.dY; gh.b = b.wdTT; gh.c = GU; gh.K = d; gh.N = F; gh.ldc = 2 * F;
+        BWD_TRY(launch_gemm_bwd(gh, 3, s));
+        const GemmPlan px = gemm_plan(d, 2 * F, b.max_mtiles, true);
+        GemmArgs gx = g;
+        gx.a = GU; gx.b = b.wguT; gx.c = b.Y; gx.K = 2 * F; gx.N = d; gx.ldc = d;
+        gx.ksplit = px.ksplit; gx.split_stride = nd;
+        BWD_TRY(launch_gemm_down(gx, s));
+        dXr = SlotRows{b.Y, 1, px.ksplit, nd};
+    } else {
+        // Recompute: G, U (gathered x rows), H, Y.
+        rows(T_{}, F_{}, b.x, d, b.wg, (size_t)d * F, F, b.G, d, F, 0);
+        rows(T_{}, F_{}, b.x, d, b.wu, (size_t)d * F, F, b.U, d, F, 0);
+        hipLaunchKernelGGL(act_kernel, dim3(blocks_for(n * F)), dim3(256), 0, s, b.G, b.U, b.H,
+                           n * F);
+        rows(F_{}, F_{}, b.H, F, b.wd, (size_t)F * d, d, b.Y, F, d, 0);
+        // Slots: dgw, dY, the slot -> position map.
+        hipLaunchKernelGGL(slot_kernel, dim3(slot_grid), dim3(256), 0, s, SlotRows{b.Y, 0, 1, 0},
+                           b.dout, b.gw, b.perm, k, d, (int)n, b.dgw, b.dY, b.inv);
+        // Experts: dH, dG and dU (in place over G, U), dXr (over Y).
+        rows(F_{}, T_{}, b.dY, d, b.wd, (size_t)F * d, d, b.dH, d, F, 0);
+        hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(blocks_for(n * F)), dim3(256), 0, s, b.G,
+                           b.U, b.dH, n * F);
+        rows(F_{}, T_{}, b.G, F, b.wg, (size_t)d * F, F, b.Y, F, d, 0);
+        rows(F_{}, T_{}, b.U, F, b.wu, (size_t)d * F, F, b.Y, F, d, 1);
+    }
     // Router and dx.
     hipLaunchKernelGGL(router_bwd_kernel, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s,
                        b.probs, b.ids, b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
-    hipLaunchKernelGGL(dx_kernel, dim3(blocks_for((size_t)T * d)), dim3(256), 0, s, b.Y, b.inv,
-                       b.dlogits, b.wr, T, d, E, k, b.accumulate, b.dx);
+    hipLaunchKernelGGL(dx_kernel, dim3((unsigned)(((size_t)T * (d / 4) + 255) / 256)), dim3(256),
+                       0, s, dXr, b.inv,
+                       b.dlogits, b.wrT, T, d, E, k, b.accumulate, b.dx);
     // Weight gradients over each expert's rows; the router's over all tokens.
     auto reduce = [&](auto gather, const float *A, int lda, const float *B, int ldb, float *C,
                       size_t c_e, int M, int N, const int *offsets, int nrows, int chunk,
@@ -522,9 +683,26 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         hipLaunchKernelGGL((reduce_gemm_kernel<decltype(gather)::value>), grid, dim3(256), 0, s,
                            g);
     };
-    reduce(F_{}, b.H, F, b.dY, d, b.dwd, (size_t)F * d, F, d, b.offsets, 0, 0, E, b.accumulate);
-    reduce(T_{}, b.x, d, b.G, F, b.dwg, (size_t)d * F, d, F, b.offsets, 0, 0, E, b.accumulate);
-    reduce(T_{}, b.x, d, b.U, F, b.dwu, (size_t)d * F, d, F, b.offsets, 0, 0, E, b.accumulate);
+    if (b.wgu) {
+        auto mfma = [&](auto gather, const float *A, int lda, const float *B, int ldb, int b_gu,
+                        float *C, int M, int N) {
+            ReduceGemm g{A, lda, b.perm, k, B, ldb, C, (size_t)M * N, N, b.offsets, 0, 0, M, N,
+                         b.accumulate, 1, 1, b_gu};
+            hipLaunchKernelGGL((reduce_mfma_kernel<decltype(gather)::value>),
+                               dim3((unsigned)(N / kMT), (unsigned)(M / kMT), (unsigned)E),
+                               dim3(256), 0, s, g);
+        };
+        mfma(F_{}, b.H, F, b.dY, d, -1, b.dwd, F, d);
+        mfma(T_{}, b.x, d, b.G, 2 * F, 0, b.dwg, d, F);
+        mfma(T_{}, b.x, d, b.G, 2 * F, 1, b.dwu, d, F);
+    } else {
+        reduce(F_{}, b.H, F, b.dY, d, b.dwd, (size_t)F * d, F, d, b.offsets, 0, 0, E,
+               b.accumulate);
+        reduce(T_{}, b.x, d, b.G, F, b.dwg, (size_t)d * F, d, F, b.offsets, 0, 0, E,
+               b.accumulate);
+        reduce(T_{}, b.x, d, b.U, F, b.dwu, (size_t)d * F, d, F, b.offsets, 0, 0, E,
+               b.accumulate);
+    }
     // The router's over all tokens, in chunks of kRouterChunk rows whose
     // partials (in dH, free by now) are then added in chunk order.
     // (at most n F / (d E) partials fit in dH)
@@ -534,9 +712,13 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
     reduce(F_{}, b.x, d, b.dlogits, E, b.dH, (size_t)d * E, d, E, nullptr, T, chunk, nz, 0);
     hipLaunchKernelGGL(sum_partials_kernel, dim3(blocks_for((size_t)d * E)), dim3(256), 0, s,
                        b.dH, nz, (size_t)d * E, b.accumulate, b.dwr);
-    if (b.aux)
-        hipLaunchKernelGGL(aux_kernel, dim3(1), dim3(256), 0, s, b.probs, b.counts, T, E, k,
-                           b.aux);
+    // (dlogits, consumed by now, holds the column sums)
+    if (b.aux) {
+        hipLaunchKernelGGL(aux_cols_kernel, dim3((unsigned)E), dim3(256), 0, s, b.probs, T, E,
+                           b.dlogits);
+        hipLaunchKernelGGL(aux_final_kernel, dim3(1), dim3(64), 0, s, b.dlogits, b.counts, T, E,
+                           k, b.aux);
+    }
     return hipGetLastError();
 }
 

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         a_dst[i] = r * LDK + 4 * c4;
         const int rr = min(r, rows - 1);
         size_t src_row;
-        if (MODE == 0) src_row = (size_t)(a.perm[row0 + rr] / a.topk);
+        if (MODE == 0 || MODE == 2) src_row = (size_t)(a.perm[row0 + rr] / a.topk);
         else           src_row = (size_t)(row0 + rr);
         a_src[i] = a.a + src_row * K + 4 * c4;
     }
@@ -183,6 +183,44 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                 int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (row < rows)
                     a.c[(size_t)(row0 + row) * a.ldc + f] = swiglu_fast(acc[m][0][r], acc[m][1][r]);
+            }
+    } else if (MODE == 2) {
+        // Raw gate and up columns (packed order, dispatch-ordered rows) and H.
+        const int f = ((nt * BN + wn * 64) >> 1) + li;
+        const int col = nt * BN + wn * 64 + li;
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row < rows) {
+                    const size_t p = (size_t)(row0 + row);
+                    const float g = acc[m][0][r], u = acc[m][1][r];
+                    a.c[p * a.ldc + col] = g;
+                    a.c[p * a.ldc + col + 32] = u;
+                    a.c2[p * a.ldc2 + f] = swiglu_fast(g, u);
+                }
+            }
+    } else if (MODE == 3) {
+        // acc = dH for features f = nt*BN + wn*64 + 32n + li; the gate and up
+        // values of f sit at packed columns 64(f/32) + f%32 and 32 past it,
+        // and are replaced by dG = dH u silu'(g), dU = dH silu(g).
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row < rows) {
+                    float *gu = a.c + (size_t)(row0 + row) * a.ldc;
+#pragma unroll
+                    for (int n = 0; n < 2; ++n) {
+                        const int col = 2 * (nt * BN + wn * 64) + 64 * n + li;
+                        const float g = gu[col], u = gu[col + 32], dh = acc[m][n][r];
+                        const float sg = 1.0f / (1.0f + expf(-g));
+                        gu[col] = dh * u * fmaf(g * sg, 1.0f - sg, sg);
+                        gu[col + 32] = dh * g * sg;
+                    }
+                }
             }
     } else {
         float *c = a.c + (size_t)ks * a.split_stride;
@@ -361,6 +399,26 @@ __global__ __launch_bounds__(256) void pack_kernel(float *src, float *dst, int K
     }
 }
 
+// dst[e] = the transpose of src[e] in the unit layout: src [E][R rows][C],
+// dst [E][C rows][R].  Four 16 x 16 units per workgroup, 64 threads each;
+// thread q writes destination floats o = 4q..4q+3 of its unit (row 16rb + j,
+// k = 16kb + 4h + s for o = 64h + 4j + s), read from source row
+// 16kb + 4h + s, k = 16rb + j.
+__global__ __launch_bounds__(256) void transpose_units_kernel(const float *src, float *dst, int R,
+                                                              int C) {
+    const int units = (R / 16) * (C / 16);
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= units) return;
+    const int rb = u % (C / 16), kb = u / (C / 16);
+    const size_t base = (size_t)blockIdx.y * R * C;
+    const int q = threadIdx.x & 63, h = q >> 4, j = q & 15;
+    const float *sp = src + base + ((size_t)kb * (C / 16) + rb) * 256 + (j >> 2) * 64 + (j & 3);
+    floatx4 v;
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) v[sl] = sp[(4 * h + sl) * 4];
+    *reinterpret_cast<floatx4 *>(dst + base + ((size_t)rb * (R / 16) + kb) * 256 + 4 * q) = v;
+}
+
 __global__ __launch_bounds__(256) void fill_normal_kernel(float *dst, size_t n, uint64_t seed,
                                                            uint64_t stream_id, float mean,
                                                            float std) {
@@ -401,6 +459,22 @@ GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split) {
 
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) { return launch_mode<0>(a, s); }
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) { return launch_mode<1>(a, s); }
+
+hipError_t launch_gemm_bwd(const GemmArgs &a, int mode, hipStream_t s) {
+    if (a.ksplit != 1) return hipErrorInvalidValue;
+    const GemmPlan pl = gemm_plan(a.N, a.K, a.max_mtiles, false);
+    if (a.K % KT || (mode != 2 && mode != 3)) return hipErrorInvalidValue;
+#define MOE_BWD_CASE(M)                                              \
+    switch (pl.bn) {                                                 \
+        case 256: return launch_grouped<M, 4>(a, s);                 \
+        case 128: return launch_grouped<M, 2>(a, s);                 \
+        case 64:  return launch_grouped<M, 1>(a, s);                 \
+        default:  return hipErrorInvalidValue;                       \
+    }
+    if (mode == 2) { MOE_BWD_CASE(2) }
+    MOE_BWD_CASE(3)
+#undef MOE_BWD_CASE
+}
 
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
     if (a.ksplit > 8 && a.ksplit <= 128) {
@@ -456,6 +530,15 @@ hipError_t launch_unpack_experts(const float *wgu, const float *wdT, float *wg, 
                        dF, 2 * dF);
     hipLaunchKernelGGL(pack_kernel, gdn, dim3(256), 0, s, wd, const_cast<float *>(wdT), F, d, 0, 1,
                        dF, dF);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_units(const float *src, float *dst, int R, int C, int E,
+                                  hipStream_t s) {
+    if (R % 16 || C % 16 || E <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(transpose_units_kernel,
+                       dim3((unsigned)(((R / 16) * (C / 16) + 3) / 4), (unsigned)E),
+                       dim3(256), 0, s, src, dst, R, C);
     return hipGetLastError();
 }
 

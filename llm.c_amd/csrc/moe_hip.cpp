@@ -1014,26 +1014,37 @@ int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dou
     TRY(route_impl(L, x, T, g_ws.probs.as<float>(), g_ws.ids.as<int>(), g_ws.gw.as<float>(),
                    g_ws.counts.as<int>(), g_ws.offsets.as<int>(), g_ws.tile_off.as<int>(),
                    g_ws.perm.as<int>(), s, true));
-    // Weights in the reference layout: wg, wu [E][d x F], wd [E][F x d].
+    // Weights: the packed ones and their unit transposes (tile engine), or
+    // the reference layout wg, wu [E][d x F], wd [E][F x d].
     const size_t dF = (size_t)d * F;
+    const bool engine = moe::backward_engine_ok(d, F);
+    const int max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
     TRY(g_ws.bw.reserve(sizeof(float) * 3 * E * dF));
-    float *wg = g_ws.bw.as<float>(), *wu = wg + E * dF, *wd = wu + E * dF;
-    HIP_TRY(moe::launch_unpack_experts(L->wgu, L->wdT, wg, wu, wd, E, d, F, s));
-    // Workspace: G, U, H, dH [n x F]; Y, dY [n x d]; dgw, inv [n]; dlogits [T x E].
+    float *w0 = g_ws.bw.as<float>(), *w1 = w0 + E * dF, *w2 = w1 + E * dF;
+    if (!engine) HIP_TRY(moe::launch_unpack_experts(L->wgu, L->wdT, w0, w1, w2, E, d, F, s));
+    // Workspace: G, U, H, dH [n x F]; Y [splits][n x d], dY [n x d]; dgw,
+    // inv [n]; dlogits [T x E].
     const size_t nF = n * F, nd = n * d;
-    TRY(g_ws.bwork.reserve(sizeof(float) * (4 * nF + 2 * nd + 2 * n + (size_t)T * E)));
+    const size_t ysplits = (size_t)moe::backward_slot_splits(d, F, max_mtiles);
+    TRY(g_ws.bwork.reserve(sizeof(float) *
+                           (4 * nF + (ysplits + 1) * nd + 2 * n + (size_t)T * E)));
     float *G = g_ws.bwork.as<float>(), *U = G + nF, *H = U + nF, *dH = H + nF;
-    float *Y = dH + nF, *dY = Y + nd, *dgw = dY + nd;
+    float *Y = dH + nF, *dY = Y + ysplits * nd, *dgw = dY + nd;
     int *inv = reinterpret_cast<int *>(dgw + n);
     float *dlogits = reinterpret_cast<float *>(inv + n);
     moe::BackwardArgs b{};
-    b.x = x; b.dout = dout; b.wr = L->wr; b.wg = wg; b.wu = wu; b.wd = wd;
+    b.x = x; b.dout = dout; b.wr = L->wr; b.wrT = L->wrT;
+    if (engine) {
+        b.wgu = L->wgu; b.wdT = L->wdT; b.wguT = w0; b.wdTT = w0 + 2 * E * dF;
+    } else {
+        b.wg = w0; b.wu = w1; b.wd = w2;
+    }
     b.probs = g_ws.probs.as<float>(); b.gw = g_ws.gw.as<float>();
     b.ids = g_ws.ids.as<int>(); b.counts = g_ws.counts.as<int>();
     b.offsets = g_ws.offsets.as<int>(); b.tile_off = g_ws.tile_off.as<int>();
     b.tile_expert = g_ws.tile_expert.as<int>(); b.perm = g_ws.perm.as<int>();
     b.T = T; b.d = d; b.F = F; b.E = E; b.k = k;
-    b.max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
+    b.max_mtiles = max_mtiles;
     b.aux_coef = aux_coef;
     b.G = G; b.U = U; b.H = H; b.dH = dH; b.Y = Y; b.dY = dY; b.dgw = dgw; b.dlogits = dlogits;
     b.inv = inv;

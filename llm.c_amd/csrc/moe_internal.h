@@ -75,6 +75,9 @@ struct GemmArgs {
     // split s writing its partial to c + s * split_stride.
     int ksplit = 1;
     size_t split_stride = 0;
+    // Backward epilogues: mode 2 also writes H = swiglu(G, U) to c2.
+    float *c2 = nullptr;
+    int ldc2 = 0;
 };
 
 struct CombineArgs {
@@ -121,6 +124,16 @@ hipError_t launch_decode_layer(const LayerArgs &a, hipStream_t s);
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s);
+// The backward's tile epilogues (gemm.hip), no reduction split:
+//   mode 2  gate/up rows gathered like the forward: c = [G | U] per 32-feature
+//           group in the packed column order (ldc = 2F), c2 = H (ldc2 = F);
+//   mode 3  a = dY rows, b = the unit transpose of wdT (N = F, K = d): the
+//           tile is dH, turned into dG, dU in place over c = [G | U].
+hipError_t launch_gemm_bwd(const GemmArgs &a, int mode, hipStream_t s);
+// dst[e] = transpose of src[e] in the packed unit layout: src [E][R][C],
+// dst [E][C][R] (R, C multiples of 16).
+hipError_t launch_transpose_units(const float *src, float *dst, int R, int C, int E,
+                                  hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s);
@@ -187,6 +200,13 @@ hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s);
 struct BackwardArgs {
     const float *x, *dout;
     const float *wr, *wg, *wu, *wd;
+    // Set (backward_engine_ok): the packed wgu, wdT and workspace for their
+    // unit transposes [E][d x 2F], [E][F x d]; wg, wu, wd then unused.  G and
+    // U must be adjacent (G + n F == U), Y hold backward_slot_splits(...)
+    // times [n x d].
+    const float *wgu = nullptr, *wdT = nullptr;
+    float *wguT = nullptr, *wdTT = nullptr;
+    const float *wrT = nullptr;   // [E x d], the router transposed (required)
     const float *probs, *gw;
     const int *ids, *counts, *offsets, *tile_off, *tile_expert, *perm;
     int T, d, F, E, k, max_mtiles;
@@ -197,6 +217,10 @@ struct BackwardArgs {
     int accumulate;
 };
 hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s);
+// The backward runs its row products on the grouped tile engine.
+bool backward_engine_ok(int d, int F);
+// Partial products per slot row the engine path leaves in Y (1 otherwise).
+int backward_slot_splits(int d, int F, int max_mtiles);
 
 // rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,

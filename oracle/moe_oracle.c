@@ -2,7 +2,8 @@
  * moe_oracle.c — TEST INFRASTRUCTURE ONLY.
  *
  * A CPU restatement of murderface-cpu/llm.c's mixture-of-experts layer, used
- * by the tests, smoke() and the CPU-baseline leg of bench.py as the checker.
+ * by the tests, smoke() and the CPU-baseline leg of bench.py to check and
+ * time the device results.
  * Nothing in the shipped library links, loads or calls this file.
  *
  * What it restates (reference paths relative to the reference repo root):

@@ -101,9 +101,12 @@ def run_device_backward(d, F, E, k, T, seed, aux_coef, accumulate_twice=False):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape", [(128, 512, 4, 2, 256), (256, 1024, 8, 2, 384),
-                                   (128, 256, 16, 4, 100)], ids=["c1", "c2-rows", "e16-k4"])
+                                   (128, 256, 16, 4, 100), (64, 96, 4, 2, 150)],
+                         ids=["c1", "c2-rows", "e16-k4", "untiled"])
 @pytest.mark.parametrize("aux_coef", [0.0, 0.5])
 def test_backward_device_vs_oracle(shape, aux_coef):
+    """The tile-engine path (d, F multiples of 64; split partials by slot at
+    c2-rows) and the untiled row products (F = 96)."""
     d, F, E, k, T = shape
     print(f"[gpu-test] backward d={d} F={F} E={E} k={k} T={T} aux={aux_coef}", flush=True)
     res, x, dout, wr, wg, wu, wd = run_device_backward(d, F, E, k, T, 31, aux_coef)
