@@ -23,9 +23,17 @@
 // through double-buffered LDS in 32-wide slices; a lane of half h (lane/32)
 // feeds the MFMA's k-row h with the slice's elements 16h..16h+15 in turn, so
 // both operands come from LDS as 128-bit reads of K-contiguous rows.
+// Global loads run two slices ahead in two register sets (the K loop is
+// unrolled by two so a set is a fixed register range).  They are issued
+// unconditionally, past the end re-reading the last slice, so the compiler's
+// count of loads in flight stays exact and each LDS fill waits only for its
+// own loads.  The fill of the next slice is spread over the four quarters of
+// the current slice's MFMAs: issued in one burst, its LDS writes held back
+// every wave's operand reads (measured: 10 % of the gate/up time).
 #include "moe_internal.h"
 #include "moe_math.h"
 #include "synth.h"
+#include <type_traits>
 
 namespace moe {
 namespace {
@@ -99,22 +107,35 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         b_src[i] = B + ((size_t)(nt * (BN / 16) + nbl) * (K / 16) + qbl) * 256 + 4 * l;
     }
 
-    floatx4 ra[A_LD], rb[B_LD];
-    auto gload = [&](int k0) {
+    floatx4 ra[2][A_LD], rb[2][B_LD];
+    auto gload = [&](int k0, int set) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i)
-            ra[i] = *reinterpret_cast<const floatx4 *>(a_src[i] + k0);
+            ra[set][i] = *reinterpret_cast<const floatx4 *>(a_src[i] + k0);
 #pragma unroll
         for (int i = 0; i < B_LD; ++i)
-            rb[i] = *reinterpret_cast<const floatx4 *>(b_src[i] + (size_t)16 * k0);
+            rb[set][i] = *reinterpret_cast<const floatx4 *>(b_src[i] + (size_t)16 * k0);
     };
-    auto sstore = [&](int buf) {
+    // Part q (of 4) of the LDS fill: items [q W / 4, (q + 1) W / 4) of the
+    // W = A_LD + B_LD float4s, so the fill is spread over the K step.
+    auto sstore_part = [&](int buf, int set, int q) {
+        constexpr int W = A_LD + B_LD;
         float *as = As + buf * BM * LDK;
         float *bs = Bs + buf * BN * LDK;
 #pragma unroll
-        for (int i = 0; i < A_LD; ++i) *reinterpret_cast<floatx4 *>(as + a_dst[i]) = ra[i];
+        for (int w = 0; w < W; ++w) {
+            if (w < q * W / 4 || w >= (q + 1) * W / 4) continue;
+            if (w < A_LD) *reinterpret_cast<floatx4 *>(as + a_dst[w]) = ra[set][w];
+            else          *reinterpret_cast<floatx4 *>(bs + b_dst[w - A_LD]) = rb[set][w - A_LD];
+        }
+    };
+    auto sstore = [&](int buf, int set) {
+        float *as = As + buf * BM * LDK;
+        float *bs = Bs + buf * BN * LDK;
 #pragma unroll
-        for (int i = 0; i < B_LD; ++i) *reinterpret_cast<floatx4 *>(bs + b_dst[i]) = rb[i];
+        for (int i = 0; i < A_LD; ++i) *reinterpret_cast<floatx4 *>(as + a_dst[i]) = ra[set][i];
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) *reinterpret_cast<floatx4 *>(bs + b_dst[i]) = rb[set][i];
     };
 
     floatx16 acc[2][2];
@@ -127,12 +148,17 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 
     const int nk = K / KT / a.ksplit;   // K steps of this split
     const int kb = ks * nk * KT;
-    gload(kb);
-    sstore(0);
+    gload(kb, 0);
+    sstore(0, 0);
+    gload(kb + min(1, nk - 1) * KT, 1);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload(kb + (kt + 1) * KT);
+    // K step kt: LDS buffer and register set P = kt % 2 hold slice kt (set P
+    // is then free for slice kt + 2); set P ^ 1 (slice kt + 1) fills buffer
+    // P ^ 1, free since the barrier that ended step kt - 1.
+    auto slice = [&](int kt, auto pset) {
+        constexpr int P = decltype(pset)::value;
+        const int buf = P;
+        gload(kb + min(kt + 2, nk - 1) * KT, P);   // (past the end: the last slice again)
         const float *as = As + buf * BM * LDK + (wm * 64 + li) * LDK + 16 * lh;
         const float *bs = Bs + buf * BN * LDK + (wn * 64 + li) * LDK + 16 * lh;
         if (nmb == 2) {
@@ -149,9 +175,10 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                     acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b0[s], acc[1][0], 0, 0, 0);
                     acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc[1][1], 0, 0, 0);
                 }
-                // The next tile's LDS fill goes in mid-block, while the other
-                // wave of this SIMD keeps the matrix unit busy.
-                if (q == 1 && kt + 1 < nk) sstore(buf ^ 1);
+                // A quarter of the next slice's LDS fill after each quarter
+                // of the MFMAs; the other wave of this SIMD keeps the matrix
+                // unit busy meanwhile.
+                if (kt + 1 < nk) sstore_part(buf ^ 1, P ^ 1, q);
             }
         } else {
             if (nmb == 1) {
@@ -167,9 +194,13 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                     }
                 }
             }
-            if (kt + 1 < nk) sstore(buf ^ 1);
+            if (kt + 1 < nk) sstore(buf ^ 1, P ^ 1);
         }
         __syncthreads();
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        slice(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
     }
 
     // Accumulator layout of a 32x32 block: lane l, register r holds
