@@ -240,6 +240,39 @@ def test_forward_dev_configs(name):
     layer.close()
 
 
+@pytest.mark.parametrize("accumulate", [0, 1])
+def test_forward_large_skewed(accumulate):
+    """A large layer (T k = 32768 routed rows), every token against the
+    oracle.  A skewed router bias gives one expert nearly every token and
+    others a few dozen to a few hundred rows (short last m-tiles);
+    accumulate = 1 adds the layer into out."""
+    T, d, F, E, k = 8192, 256, 512, 8, 4
+    say(f"large skewed layer: T={T} d={d} F={F} E={E} k={k} accumulate={accumulate}")
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(9, 0.1, 0.05)
+    bias = np.array([3.0, 1.5, 0.5, 0.0, -1.0, -2.0, -3.5, -5.0], np.float32)
+    layer.set_bias(bias)
+    hw = host_layer(d, F, E, k, 9, 0.1, 0.05)
+    x = orc.synth((T, d), 9, 0, 1.0)
+    base = orc.synth((T, d), 9, 1, 1.0)
+    dx = mh.DeviceArray.from_host(x)
+    dout = mh.DeviceArray.from_host(base)
+    dprobs = mh.DeviceArray((T, E))
+    dids = mh.DeviceArray((T, k), np.int32)
+    layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr, accumulate=accumulate)
+    mh.synchronize()
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw, bias, nthreads=16)
+    ids = dids.to_host()
+    assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    say(f"large skewed layer: rows per expert {counts.tolist()}")
+    assert counts.min() < 256 and counts.max() > 4 * 256
+    expect = o_ref + base if accumulate else o_ref
+    assert_close(dout.to_host(), expect, "large skewed layer")
+    layer.close()
+
+
 def test_forward_c5_sampled():
     """Config 5 at full size on the device (12.9 GB of experts, Zipf-skewed
     router bias when its fixture exists); routing compared for all tokens,
