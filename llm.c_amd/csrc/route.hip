@@ -84,7 +84,20 @@ __device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], i
     const int chunk = ((n + NW * 64 - 1) / (NW * 64)) * 64;
     const int beg = w * chunk;
     const int end = min(n, beg + chunk);
-    for (int i = beg + lane; i < end; i += 64) atomicAdd(&hist[w][a.ids[i]], 1);
+    // Expert ids in groups of 8 per lane, every load of a group in flight
+    // before its LDS atomics.
+    constexpr int kG = 8;
+    for (int i0 = beg; i0 < end; i0 += 64 * kG) {
+        int v[kG];
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+            const int i = i0 + 64 * u + lane;
+            v[u] = i < end ? a.ids[i] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kG; ++u)
+            if (v[u] >= 0) atomicAdd(&hist[w][v[u]], 1);
+    }
     __syncthreads();
 
     // Wave 0 scans counts and m-tiles over the (at most 128) experts, two
@@ -131,10 +144,21 @@ __device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], i
     int nbits = 0;
     while ((1 << nbits) < E) ++nbits;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int ev[kG];   // the next group of ids, loaded ahead of the ballots
     for (int i0 = beg; i0 < end; i0 += 64) {
+        const int u = ((i0 - beg) >> 6) % kG;
+        if (u == 0)
+#pragma unroll
+            for (int q = 0; q < kG; ++q) {
+                const int iq = i0 + 64 * q + lane;
+                ev[q] = iq < end ? a.ids[iq] : 0;
+            }
         const int i = i0 + lane;
         const bool valid = i < end;
-        const int e = valid ? a.ids[i] : 0;
+        int e = 0;
+#pragma unroll
+        for (int q = 0; q < kG; ++q)
+            if (q == u) e = ev[q];
         uint64_t peers = __ballot(valid);
         for (int b = 0; b < nbits; ++b) {
             uint64_t m = __ballot(valid && ((e >> b) & 1));
