@@ -285,6 +285,10 @@ struct ReduceGemm {
     // B read from [G | U] in the packed gate/up column order: column n of
     // the gate (0) or up (1) half is 64 (n / 32) + n % 32 + 32 b_gu; -1: plain.
     int b_gu = -1;
+    // reduce_mfma_kernel only: N runs over [G | U]'s 2F packed columns and
+    // column n's product goes to c (gate, n % 64 < 32) or c_up (up) at
+    // feature 32 (n / 64) + n % 32.
+    float *c_up = nullptr;
 };
 
 template <bool GATHER>
@@ -415,12 +419,13 @@ __global__ __launch_bounds__(256) void reduce_mfma_kernel(ReduceGemm g) {
         }
     }
     // Lane l, register q: row 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32.
-    float *ce = g.c + (size_t)e * g.c_e;
     const int n = n0 + wn * 32 + li;
+    float *ce = (g.c_up && (n & 32) ? g.c_up : g.c) + (size_t)e * g.c_e;
+    const int col = g.c_up ? 32 * (n >> 6) + (n & 31) : n;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
         const int m = m0 + wm * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
-        float *cp = ce + (size_t)m * g.ldc + n;
+        float *cp = ce + (size_t)m * g.ldc + col;
         *cp = g.accumulate ? *cp + acc[q] : acc[q];
     }
 }
@@ -684,17 +689,17 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
                            g);
     };
     if (b.wgu) {
-        auto mfma = [&](auto gather, const float *A, int lda, const float *B, int ldb, int b_gu,
-                        float *C, int M, int N) {
-            ReduceGemm g{A, lda, b.perm, k, B, ldb, C, (size_t)M * N, N, b.offsets, 0, 0, M, N,
-                         b.accumulate, 1, 1, b_gu};
+        auto mfma = [&](auto gather, const float *A, int lda, const float *B, int ldb, float *C,
+                        float *C_up, int M, int N, int ldc) {
+            ReduceGemm g{A, lda, b.perm, k, B, ldb, C, (size_t)M * ldc, ldc, b.offsets, 0, 0, M,
+                         N, b.accumulate, 1, 1, -1, C_up};
             hipLaunchKernelGGL((reduce_mfma_kernel<decltype(gather)::value>),
                                dim3((unsigned)(N / kMT), (unsigned)(M / kMT), (unsigned)E),
                                dim3(256), 0, s, g);
         };
-        mfma(F_{}, b.H, F, b.dY, d, -1, b.dwd, F, d);
-        mfma(T_{}, b.x, d, b.G, 2 * F, 0, b.dwg, d, F);
-        mfma(T_{}, b.x, d, b.G, 2 * F, 1, b.dwu, d, F);
+        mfma(F_{}, b.H, F, b.dY, d, b.dwd, nullptr, F, d, d);
+        // dW_g and dW_u in one launch over GU's 2F packed columns.
+        mfma(T_{}, b.x, d, b.G, 2 * F, b.dwg, b.dwu, d, 2 * F, F);
     } else {
         reduce(F_{}, b.H, F, b.dY, d, b.dwd, (size_t)F * d, F, d, b.offsets, 0, 0, E,
                b.accumulate);
