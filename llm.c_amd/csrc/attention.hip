@@ -398,8 +398,10 @@ __global__ __launch_bounds__(1024) void proj16_kernel(AttnArgs a) {
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 1024 * i, kk = k0 + idx / (kPT / 4), cc = c0 + 4 * (idx % (kPT / 4));
             const float *src = nullptr;
+            const float *wp = QKV ? a.wqkv_p : a.wo_p;
             if (kk < M && cc < N) {
-                if (!QKV)                    src = a.wo + (size_t)kk * a.d + cc;
+                if (wp)                      src = wp + ((size_t)(cc >> 4) * M + kk) * 16 + (cc & 15);
+                else if (!QKV)               src = a.wo + (size_t)kk * a.d + cc;
                 else if (cc < a.qd)          src = a.wq + (size_t)kk * a.qd + cc;
                 else if (cc < a.qd + a.kd)   src = a.wk + (size_t)kk * a.kd + (cc - a.qd);
                 else                         src = a.wv + (size_t)kk * a.kd + (cc - a.qd - a.kd);
@@ -889,6 +891,27 @@ AttnCounters attn_counters(int B, int d, int qd, int kd, int nkv) {
 
 bool attn_fused_supported(int hd, int nh, int nkv) {
     return nkv > 0 && nh % nkv == 0 && with_fast_shape(hd, nh / nkv, [](auto, auto) {});
+}
+
+namespace {
+__global__ __launch_bounds__(256) void pack_cols16_kernel(const float *src, float *dst, int K,
+                                                          int N, int col0) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;   // float4 of dst
+    if (i >= (size_t)K * N / 4) return;
+    const int t = (int)(i / ((size_t)K * 4)), rem = (int)(i % ((size_t)K * 4));
+    const int k = rem >> 2, c = 16 * t + 4 * (rem & 3);
+    *reinterpret_cast<float4 *>(dst + ((size_t)(col0 / 16 + t) * K + k) * 16 + 4 * (rem & 3)) =
+        *reinterpret_cast<const float4 *>(src + (size_t)k * N + c);
+}
+}  // namespace
+
+hipError_t launch_pack_cols16(const float *src, float *dst, int K, int N, int col0,
+                              hipStream_t s) {
+    if (K <= 0 || N <= 0 || N % 16 || col0 % 16) return hipErrorInvalidValue;
+    const size_t n4 = (size_t)K * N / 4;
+    hipLaunchKernelGGL(pack_cols16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                       src, dst, K, N, col0);
+    return hipGetLastError();
 }
 
 hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s) {

@@ -372,11 +372,14 @@ struct MoeHipAttn {
     int d = 0, nh = 0, nkv = 0, hd = 0, max_seq = 0;
     float *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
     float *rms = nullptr, *cos_t = nullptr, *sin_t = nullptr;
+    // The projections' weights in 16-column tiles (when every width is a
+    // multiple of 16): [wq | wk | wv] and wo, for the projection tiles.
+    float *wqkv_p = nullptr, *wo_p = nullptr;
 };
 
 int moe_hip_attn_destroy(MoeHipAttn *a) {
     if (!a) return MOE_HIP_OK;
-    for (float *p : {a->wq, a->wk, a->wv, a->wo, a->rms, a->cos_t, a->sin_t})
+    for (float *p : {a->wq, a->wk, a->wv, a->wo, a->rms, a->cos_t, a->sin_t, a->wqkv_p, a->wo_p})
         if (p) (void)hipFree(p);
     delete a;
     return MOE_HIP_OK;
@@ -406,6 +409,12 @@ int moe_hip_attn_create(int d_model, int n_heads, int n_kv_heads, int head_dim, 
             moe_hip_attn_destroy(a);
             return set_err(MOE_HIP_ERR_NOMEM, "attention weights");
         }
+    if (qd % 16 == 0 && kd % 16 == 0 && d_model % 16 == 0 &&
+        (hipMalloc(&a->wqkv_p, sizeof(float) * d_model * (qd + 2 * kd)) != hipSuccess ||
+         hipMalloc(&a->wo_p, sizeof(float) * qd * d_model) != hipSuccess)) {
+        moe_hip_attn_destroy(a);
+        return set_err(MOE_HIP_ERR_NOMEM, "attention weights");
+    }
     *out = a;
     return MOE_HIP_OK;
 }
@@ -419,6 +428,14 @@ int moe_hip_attn_load(MoeHipAttn *a, const float *wq, const float *wk, const flo
     HIP_TRY(hipMemcpy(a->wv, wv, sizeof(float) * a->d * kd, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(a->wo, wo, sizeof(float) * qd * a->d, hipMemcpyHostToDevice));
     HIP_TRY(hipMemcpy(a->rms, rms_attn, sizeof(float) * a->d, hipMemcpyHostToDevice));
+    if (a->wqkv_p) {
+        const int d = a->d, q = (int)qd, kv = (int)kd;
+        HIP_TRY(moe::launch_pack_cols16(a->wq, a->wqkv_p, d, q, 0, g_stream));
+        HIP_TRY(moe::launch_pack_cols16(a->wk, a->wqkv_p, d, kv, q, g_stream));
+        HIP_TRY(moe::launch_pack_cols16(a->wv, a->wqkv_p, d, kv, q + kv, g_stream));
+        HIP_TRY(moe::launch_pack_cols16(a->wo, a->wo_p, q, d, 0, g_stream));
+        HIP_TRY(hipStreamSynchronize(g_stream));
+    }
     return MOE_HIP_OK;
 }
 
@@ -459,6 +476,7 @@ static int attn_decode(MoeHipAttn *a, float *x, int B, const int *pos, float *k_
     moe::AttnArgs aa{};
     aa.x = x; aa.rms_w = a->rms; aa.eps = eps;
     aa.wq = a->wq; aa.wk = a->wk; aa.wv = a->wv; aa.wo = a->wo;
+    aa.wqkv_p = a->wqkv_p; aa.wo_p = a->wo_p;
     aa.cos_t = a->cos_t; aa.sin_t = a->sin_t; aa.kc = k_cache; aa.vc = v_cache; aa.pos = pos;
     aa.q = g_ws.aq.as<float>(); aa.o = g_ws.ao.as<float>(); aa.part = g_ws.apart.as<float>();
     aa.gpart = g_ws.agpart.as<float>(); aa.sspart = g_ws.ass.as<float>();

@@ -178,6 +178,10 @@ struct AttnArgs {
     int nqkv_tiles;
     int B, d, nh, nkv, hd, qd, kd, max_seq;
     float scale;            // 1 / sqrt(hd)
+    // Optional copies packed in 16-column tiles ([N/16][K][16], see
+    // launch_pack_cols16): the projection tiles then read one contiguous
+    // block per tile.  wqkv_p holds [wq | wk | wv] (K = d), wo_p wo (K = qd).
+    const float *wqkv_p = nullptr, *wo_p = nullptr;
 };
 struct AttnCounters {
     int qkv, wo, merge;
@@ -190,6 +194,11 @@ int attn_sync_ints();
 // Head shapes for which the one-launch sublayer exists.
 bool attn_fused_supported(int hd, int nh, int nkv);
 hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s);
+// Columns col0 .. col0 + N of a K-row matrix packed in 16-column tiles:
+// dst[((col0 + c) / 16) K 16 + k 16 + c % 16] = src[k N + c] (col0, N
+// multiples of 16).
+hipError_t launch_pack_cols16(const float *src, float *dst, int K, int N, int col0,
+                              hipStream_t s);
 
 // Backward pass of the layer (backward.hip) with the routing of a forward
 // already run (probs, ids, gw, counts, offsets, tile schedule, perm).

@@ -116,6 +116,10 @@ def attn_decode(x, rms_w, eps, wq, wk, wv, wo, cos_t, sin_t, kc, vc, pos, nh, nk
     vc = np.array(vc, np.float32, copy=True, order="C")
     pos = np.ascontiguousarray(pos, np.int32)
     B, d = x.shape
+    # The restatement, like inference_step, needs pos < max_seq (it writes
+    # cache row pos and scores 0 .. pos); refuse rather than overrun.
+    if pos.shape != (B,) or kc.shape[0] != B or (pos < 0).any() or (pos >= kc.shape[1]).any():
+        raise ValueError("attn_decode: every position must lie in [0, max_seq)")
     ar = [np.ascontiguousarray(a, np.float32) for a in (rms_w, wq, wk, wv, wo, cos_t, sin_t)]
     orc().orc_attn_decode(fptr(x), B, d, nh, nkv, hd, fptr(ar[0]), eps, fptr(ar[1]), fptr(ar[2]),
                           fptr(ar[3]), fptr(ar[4]), fptr(ar[5]), fptr(ar[6]), fptr(kc), fptr(vc),

@@ -147,8 +147,9 @@ def run_device(x, w, kc, vc, pos, c, s, nh=NH, nkv=NKV, hd=HD, fused=1):
 @pytest.mark.gpu
 @pytest.mark.parametrize("fused", [1, 0], ids=["one-launch", "launches"])
 @pytest.mark.parametrize("shape", [(128, 8, 2, 16, 600), (512, 8, 2, 64, 1100),
-                                   (256, 8, 1, 32, 300), (64, 4, 4, 16, 300)],
-                         ids=["small", "config4", "g8", "mha-generic"])
+                                   (256, 8, 1, 32, 300), (64, 4, 4, 16, 300),
+                                   (64, 2, 1, 8, 300)],
+                         ids=["small", "config4", "g8", "mha-generic", "hd8-unpacked"])
 def test_attn_decode_device(shape, fused):
     """Outputs within the layer tolerance of the oracle; the new k, v rows
     within it too, every other cache row bit-for-bit unchanged.  mha-generic
