@@ -282,9 +282,6 @@ struct ReduceGemm {
     int ldc;
     const int *offsets;
     int nrows, chunk, M, N, accumulate, vec_a, vec_b;
-    // B read from [G | U] in the packed gate/up column order: column n of
-    // the gate (0) or up (1) half is 64 (n / 32) + n % 32 + 32 b_gu; -1: plain.
-    int b_gu = -1;
     // reduce_mfma_kernel only: N runs over [G | U]'s 2F packed columns and
     // column n's product goes to c (gate, n % 64 < 32) or c_up (up) at
     // feature 32 (n / 64) + n % 32.
@@ -375,7 +372,7 @@ __global__ __launch_bounds__(256) void reduce_mfma_kernel(ReduceGemm g) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, li = lane & 31, lh = lane >> 5;
     const int lr = tid >> 4, lq = 4 * (tid & 15);   // load rows lr, lr + 16; column quad
-    const int bcol = g.b_gu < 0 ? n0 + lq : 64 * ((n0 + lq) >> 5) + ((n0 + lq) & 31) + 32 * g.b_gu;
+    const int bcol = n0 + lq;
     fx4 ra[2], rb[2];
     auto gload = [&](int r) {
 #pragma unroll
@@ -692,7 +689,7 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         auto mfma = [&](auto gather, const float *A, int lda, const float *B, int ldb, float *C,
                         float *C_up, int M, int N, int ldc) {
             ReduceGemm g{A, lda, b.perm, k, B, ldb, C, (size_t)M * ldc, ldc, b.offsets, 0, 0, M,
-                         N, b.accumulate, 1, 1, -1, C_up};
+                         N, b.accumulate, 1, 1, C_up};
             hipLaunchKernelGGL((reduce_mfma_kernel<decltype(gather)::value>),
                                dim3((unsigned)(N / kMT), (unsigned)(M / kMT), (unsigned)E),
                                dim3(256), 0, s, g);
