@@ -22,14 +22,20 @@
 // A wave issues v_mfma_f32_32x32x2f32 on 2 x 2 sub-tiles.  K is staged
 // through double-buffered LDS in 32-wide slices; a lane of half h (lane/32)
 // feeds the MFMA's k-row h with the slice's elements 16h..16h+15 in turn, so
-// both operands come from LDS as 128-bit reads of K-contiguous rows.
-// Global loads run two slices ahead in two register sets (the K loop is
-// unrolled by two so a set is a fixed register range).  They are issued
-// unconditionally, past the end re-reading the last slice, so the compiler's
-// count of loads in flight stays exact and each LDS fill waits only for its
-// own loads.  The fill of the next slice is spread over the four quarters of
-// the current slice's MFMAs: issued in one burst, its LDS writes held back
-// every wave's operand reads (measured: 10 % of the gate/up time).
+// both operands come from LDS as 128-bit reads.
+// B (two thirds of each slice at 256 columns) goes global -> LDS by DMA
+// (global_load_lds_dwordx4): each packed 1 KB unit is copied whole, keeping
+// the unit layout in LDS, one slice ahead; no registers or LDS store
+// instructions carry it.  A (rows gathered through perm) goes through
+// registers into padded K-contiguous LDS rows: its loads run two slices
+// ahead in two register sets (the K loop is unrolled by two so a set is a
+// fixed register range), issued unconditionally (past the end re-reading the
+// last slice) so the compiler's count of loads in flight stays exact, and
+// its LDS fill is spread over the four quarters of the current slice's
+// MFMAs.  Issued in one burst, the whole tile's LDS fill held back every
+// wave's operand reads (10 % of the gate/up time); B by DMA saves another 2 %.
+// The DMA is waited for explicitly (vmcnt) before the barrier that ends the
+// slice: s_barrier orders LDS accesses, not loads in flight.
 #include "moe_internal.h"
 #include "moe_math.h"
 #include "synth.h"
@@ -44,6 +50,15 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int BM = kGemmBM;   // 128
 constexpr int KT = 32;
 constexpr int LDK = KT + 4;   // padded LDS row (144 B): conflict-free b128 reads
+
+// One wave instruction of LDS DMA: lane i's 16 bytes at g go to lds + 16 i
+// bytes (lds wave-uniform).  (Kept out of the kernel body: a device-only
+// builtin written directly in a __global__ template suppresses its host stub.)
+__device__ __forceinline__ void gemm_dma16(const float *g, float *lds) {
+    __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+// s_waitcnt limiting only the vector-memory count (expcnt, lgkmcnt at max).
+#define GEMM_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | 0x0F70)
 
 template <int MODE, int WN>
 __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
@@ -95,47 +110,44 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         else           src_row = (size_t)(row0 + rr);
         a_src[i] = a.a + src_row * K + 4 * c4;
     }
-    // B tile = (BN/16) x 2 units; 64 consecutive threads load one unit.
-    const float *b_src[B_LD];
-    int b_dst[B_LD];
+    // B tile = (BN/16) x 2 units, copied whole by LDS DMA: wave w the units
+    // w * BUW .. in the packed unit layout (unit u at u * 256 floats).
+    constexpr int BUW = (BN / 16 * 2) / (2 * WN);
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
+    const float *b_src[BUW];
 #pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
-        int g = tid + NT * i;
-        int u = g >> 6, l = g & 63;
-        int nbl = u >> 1, qbl = u & 1;
-        b_dst[i] = (nbl * 16 + (l & 15)) * LDK + qbl * 16 + (l >> 4) * 4;
-        b_src[i] = B + ((size_t)(nt * (BN / 16) + nbl) * (K / 16) + qbl) * 256 + 4 * l;
+    for (int i = 0; i < BUW; ++i) {
+        const int u = wu * BUW + i, nbl = u >> 1, qbl = u & 1;
+        b_src[i] = B + ((size_t)(nt * (BN / 16) + nbl) * (K / 16) + qbl) * 256 + 4 * lane;
     }
+    auto bdma = [&](int k0, int buf) {
+        float *bs = Bs + buf * BN * LDK;
+#pragma unroll
+        for (int i = 0; i < BUW; ++i)
+            gemm_dma16(b_src[i] + (size_t)16 * k0, bs + (wu * BUW + i) * 256);
+    };
 
-    floatx4 ra[2][A_LD], rb[2][B_LD];
+    floatx4 ra[2][A_LD];
     auto gload = [&](int k0, int set) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i)
             ra[set][i] = *reinterpret_cast<const floatx4 *>(a_src[i] + k0);
-#pragma unroll
-        for (int i = 0; i < B_LD; ++i)
-            rb[set][i] = *reinterpret_cast<const floatx4 *>(b_src[i] + (size_t)16 * k0);
     };
     // Part q (of 4) of the LDS fill: items [q W / 4, (q + 1) W / 4) of the
     // W = A_LD + B_LD float4s, so the fill is spread over the K step.
     auto sstore_part = [&](int buf, int set, int q) {
-        constexpr int W = A_LD + B_LD;
+        constexpr int W = A_LD;
         float *as = As + buf * BM * LDK;
-        float *bs = Bs + buf * BN * LDK;
 #pragma unroll
         for (int w = 0; w < W; ++w) {
             if (w < q * W / 4 || w >= (q + 1) * W / 4) continue;
-            if (w < A_LD) *reinterpret_cast<floatx4 *>(as + a_dst[w]) = ra[set][w];
-            else          *reinterpret_cast<floatx4 *>(bs + b_dst[w - A_LD]) = rb[set][w - A_LD];
+            *reinterpret_cast<floatx4 *>(as + a_dst[w]) = ra[set][w];
         }
     };
     auto sstore = [&](int buf, int set) {
         float *as = As + buf * BM * LDK;
-        float *bs = Bs + buf * BN * LDK;
 #pragma unroll
         for (int i = 0; i < A_LD; ++i) *reinterpret_cast<floatx4 *>(as + a_dst[i]) = ra[set][i];
-#pragma unroll
-        for (int i = 0; i < B_LD; ++i) *reinterpret_cast<floatx4 *>(bs + b_dst[i]) = rb[set][i];
     };
 
     floatx16 acc[2][2];
@@ -148,9 +160,11 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 
     const int nk = K / KT / a.ksplit;   // K steps of this split
     const int kb = ks * nk * KT;
+    bdma(kb, 0);
     gload(kb, 0);
     sstore(0, 0);
     gload(kb + min(1, nk - 1) * KT, 1);
+    GEMM_WAIT_VMCNT(A_LD);   // (the slice-1 A loads may stay in flight)
     __syncthreads();
     // K step kt: LDS buffer and register set P = kt % 2 hold slice kt (set P
     // is then free for slice kt + 2); set P ^ 1 (slice kt + 1) fills buffer
@@ -158,16 +172,17 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     auto slice = [&](int kt, auto pset) {
         constexpr int P = decltype(pset)::value;
         const int buf = P;
+        if (kt + 1 < nk) bdma(kb + (kt + 1) * KT, buf ^ 1);
         gload(kb + min(kt + 2, nk - 1) * KT, P);   // (past the end: the last slice again)
         const float *as = As + buf * BM * LDK + (wm * 64 + li) * LDK + 16 * lh;
-        const float *bs = Bs + buf * BN * LDK + (wn * 64 + li) * LDK + 16 * lh;
+        const float *bs = Bs + buf * BN * LDK + ((wn * 4 + (li >> 4)) * 2 + lh) * 256 + (li & 15) * 4;
         if (nmb == 2) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
                 floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * LDK + 4 * q);
-                floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 4 * q);
-                floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 32 * LDK + 4 * q);
+                floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 64 * q);
+                floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 4 * 256 + 64 * q);
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
@@ -185,8 +200,8 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
-                    floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 4 * q);
-                    floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 32 * LDK + 4 * q);
+                    floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 64 * q);
+                    floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 4 * 256 + 64 * q);
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
                         acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
@@ -196,6 +211,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
             }
             if (kt + 1 < nk) sstore(buf ^ 1, P ^ 1);
         }
+        GEMM_WAIT_VMCNT(A_LD);
         __syncthreads();
     };
     for (int kt = 0; kt < nk; kt += 2) {
