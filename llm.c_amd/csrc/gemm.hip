@@ -23,19 +23,18 @@
 // through double-buffered LDS in 32-wide slices; a lane of half h (lane/32)
 // feeds the MFMA's k-row h with the slice's elements 16h..16h+15 in turn, so
 // both operands come from LDS as 128-bit reads.
-// B (two thirds of each slice at 256 columns) goes global -> LDS by DMA
-// (global_load_lds_dwordx4): each packed 1 KB unit is copied whole, keeping
-// the unit layout in LDS, one slice ahead; no registers or LDS store
-// instructions carry it.  A (rows gathered through perm) goes through
-// registers into padded K-contiguous LDS rows: its loads run two slices
-// ahead in two register sets (the K loop is unrolled by two so a set is a
-// fixed register range), issued unconditionally (past the end re-reading the
-// last slice) so the compiler's count of loads in flight stays exact, and
-// its LDS fill is spread over the four quarters of the current slice's
-// MFMAs.  Issued in one burst, the whole tile's LDS fill held back every
-// wave's operand reads (10 % of the gate/up time); B by DMA saves another 2 %.
-// The DMA is waited for explicitly (vmcnt) before the barrier that ends the
-// slice: s_barrier orders LDS accesses, not loads in flight.
+// Both operands go global -> LDS by DMA (global_load_lds_dwordx4, one wave
+// instruction = 64 lanes x 16 bytes into 1 KB of LDS), one slice ahead of
+// the MFMAs: no registers or LDS store instructions carry the tiles.
+//   B  the packed 1 KB units are copied whole (unit layout in LDS);
+//   A  a unit is 8 whole gathered rows (128 B each, full cache lines), each
+//      row's eight 16-byte chunks permuted by XOR with row % 8 so the
+//      fragment reads are free of bank conflicts.
+// Measured on the gate/up GEMM of the large layer (ms): register staging
+// with the fill in one burst 35.3, spread over the slice 34.5, B by DMA 33.8,
+// both by DMA 33.1.  The DMA is waited for explicitly (vmcnt) before the
+// barrier that ends the slice: s_barrier orders LDS accesses, not loads in
+// flight.
 #include "moe_internal.h"
 #include "moe_math.h"
 #include "synth.h"
@@ -49,7 +48,6 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = kGemmBM;   // 128
 constexpr int KT = 32;
-constexpr int LDK = KT + 4;   // padded LDS row (144 B): conflict-free b128 reads
 
 // One wave instruction of LDS DMA: lane i's 16 bytes at g go to lds + 16 i
 // bytes (lds wave-uniform).  (Kept out of the kernel body: a device-only
@@ -63,12 +61,11 @@ __device__ __forceinline__ void gemm_dma16(const float *g, float *lds) {
 template <int MODE, int WN>
 __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     constexpr int BN = 64 * WN;
-    constexpr int NT = 128 * WN;
-    constexpr int A_LD = (BM * KT / 4) / NT;   // float4 loads of A per thread
-    constexpr int B_LD = (BN * KT / 4) / NT;   // float4 loads of B per thread
     extern __shared__ __align__(16) float smem[];
-    float *As = smem;                          // [2][BM][LDK]
-    float *Bs = smem + 2 * BM * LDK;           // [2][BN][LDK]
+    // Two buffers each: A as 128 rows of 32 swizzled floats, B as
+    // (BN/16) x 2 packed 1 KB units (BN rows of 32 floats' worth).
+    float *As = smem;
+    float *Bs = smem + 2 * BM * KT;
 
     const int ntiles = a.N / BN;
     const int per_split = a.max_mtiles * ntiles;
@@ -97,19 +94,28 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     // Per-thread global source rows for the A tile.  Rows past the expert's
     // last row reuse its last row: their accumulator rows are never stored,
     // and unconditional loads keep the K loop free of exec-masked branches.
-    const float *a_src[A_LD];
-    int a_dst[A_LD];
+    // A tile = 16 units of 8 whole rows (32 floats = 128 B each), copied by
+    // LDS DMA: lane i of a unit's DMA brings row i / 8's 16-byte chunk
+    // (i % 8) ^ (row % 8), so row r's chunk c sits at r * 32 + 4 (c ^ (r % 8))
+    // floats and the fragment reads below are free of bank conflicts.
+    constexpr int AUW = (BM / 8) / (2 * WN);
+    const int wa = __builtin_amdgcn_readfirstlane(wave);
+    const float *a_src[AUW];
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-        int q = tid + NT * i;
-        int r = q >> 3, c4 = q & 7;
-        a_dst[i] = r * LDK + 4 * c4;
+    for (int i = 0; i < AUW; ++i) {
+        const int r = 8 * (wa * AUW + i) + (lane >> 3);
+        const int c = (lane & 7) ^ (r & 7);
         const int rr = min(r, rows - 1);
         size_t src_row;
         if (MODE == 0 || MODE == 2) src_row = (size_t)(a.perm[row0 + rr] / a.topk);
         else           src_row = (size_t)(row0 + rr);
-        a_src[i] = a.a + src_row * K + 4 * c4;
+        a_src[i] = a.a + src_row * K + 4 * c;
     }
+    auto adma = [&](int k0, int buf) {
+        float *as = As + buf * BM * KT;
+#pragma unroll
+        for (int i = 0; i < AUW; ++i) gemm_dma16(a_src[i] + k0, as + (wa * AUW + i) * 256);
+    };
     // B tile = (BN/16) x 2 units, copied whole by LDS DMA: wave w the units
     // w * BUW .. in the packed unit layout (unit u at u * 256 floats).
     constexpr int BUW = (BN / 16 * 2) / (2 * WN);
@@ -121,33 +127,10 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         b_src[i] = B + ((size_t)(nt * (BN / 16) + nbl) * (K / 16) + qbl) * 256 + 4 * lane;
     }
     auto bdma = [&](int k0, int buf) {
-        float *bs = Bs + buf * BN * LDK;
+        float *bs = Bs + buf * BN * KT;
 #pragma unroll
         for (int i = 0; i < BUW; ++i)
             gemm_dma16(b_src[i] + (size_t)16 * k0, bs + (wu * BUW + i) * 256);
-    };
-
-    floatx4 ra[2][A_LD];
-    auto gload = [&](int k0, int set) {
-#pragma unroll
-        for (int i = 0; i < A_LD; ++i)
-            ra[set][i] = *reinterpret_cast<const floatx4 *>(a_src[i] + k0);
-    };
-    // Part q (of 4) of the LDS fill: items [q W / 4, (q + 1) W / 4) of the
-    // W = A_LD + B_LD float4s, so the fill is spread over the K step.
-    auto sstore_part = [&](int buf, int set, int q) {
-        constexpr int W = A_LD;
-        float *as = As + buf * BM * LDK;
-#pragma unroll
-        for (int w = 0; w < W; ++w) {
-            if (w < q * W / 4 || w >= (q + 1) * W / 4) continue;
-            *reinterpret_cast<floatx4 *>(as + a_dst[w]) = ra[set][w];
-        }
-    };
-    auto sstore = [&](int buf, int set) {
-        float *as = As + buf * BM * LDK;
-#pragma unroll
-        for (int i = 0; i < A_LD; ++i) *reinterpret_cast<floatx4 *>(as + a_dst[i]) = ra[set][i];
     };
 
     floatx16 acc[2][2];
@@ -160,27 +143,30 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 
     const int nk = K / KT / a.ksplit;   // K steps of this split
     const int kb = ks * nk * KT;
+    adma(kb, 0);
     bdma(kb, 0);
-    gload(kb, 0);
-    sstore(0, 0);
-    gload(kb + min(1, nk - 1) * KT, 1);
-    GEMM_WAIT_VMCNT(A_LD);   // (the slice-1 A loads may stay in flight)
+    GEMM_WAIT_VMCNT(0);
     __syncthreads();
-    // K step kt: LDS buffer and register set P = kt % 2 hold slice kt (set P
-    // is then free for slice kt + 2); set P ^ 1 (slice kt + 1) fills buffer
-    // P ^ 1, free since the barrier that ended step kt - 1.
-    auto slice = [&](int kt, auto pset) {
-        constexpr int P = decltype(pset)::value;
-        const int buf = P;
-        if (kt + 1 < nk) bdma(kb + (kt + 1) * KT, buf ^ 1);
-        gload(kb + min(kt + 2, nk - 1) * KT, P);   // (past the end: the last slice again)
-        const float *as = As + buf * BM * LDK + (wm * 64 + li) * LDK + 16 * lh;
-        const float *bs = Bs + buf * BN * LDK + ((wn * 4 + (li >> 4)) * 2 + lh) * 256 + (li & 15) * 4;
+    // Row (li) of this lane's A blocks has r % 8 = li % 8: the 16-byte chunk
+    // 4 lh + q of K step q sits at 4 ((4 lh + q) ^ (li % 8)) floats.
+    int aoff[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) aoff[q] = 4 * ((4 * lh + q) ^ (li & 7));
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        // The next slice into the other buffer (free since the barrier that
+        // ended step kt - 1), in flight while this one is multiplied.
+        if (kt + 1 < nk) {
+            adma(kb + (kt + 1) * KT, buf ^ 1);
+            bdma(kb + (kt + 1) * KT, buf ^ 1);
+        }
+        const float *as = As + buf * BM * KT + (wm * 64 + li) * KT;
+        const float *bs = Bs + buf * BN * KT + ((wn * 4 + (li >> 4)) * 2 + lh) * 256 + (li & 15) * 4;
         if (nmb == 2) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
-                floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * LDK + 4 * q);
+                floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + aoff[q]);
+                floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * 32 + aoff[q]);
                 floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 64 * q);
                 floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 4 * 256 + 64 * q);
 #pragma unroll
@@ -190,33 +176,22 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                     acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b0[s], acc[1][0], 0, 0, 0);
                     acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc[1][1], 0, 0, 0);
                 }
-                // A quarter of the next slice's LDS fill after each quarter
-                // of the MFMAs; the other wave of this SIMD keeps the matrix
-                // unit busy meanwhile.
-                if (kt + 1 < nk) sstore_part(buf ^ 1, P ^ 1, q);
             }
-        } else {
-            if (nmb == 1) {
+        } else if (nmb == 1) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 4 * q);
-                    floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 64 * q);
-                    floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 4 * 256 + 64 * q);
+            for (int q = 0; q < 4; ++q) {
+                floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + aoff[q]);
+                floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 64 * q);
+                floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 4 * 256 + 64 * q);
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
-                        acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b1[s], acc[0][1], 0, 0, 0);
-                    }
+                for (int s = 0; s < 4; ++s) {
+                    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[0][0], 0, 0, 0);
+                    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b1[s], acc[0][1], 0, 0, 0);
                 }
             }
-            if (kt + 1 < nk) sstore(buf ^ 1, P ^ 1);
         }
-        GEMM_WAIT_VMCNT(A_LD);
+        GEMM_WAIT_VMCNT(0);   // the next slice has landed
         __syncthreads();
-    };
-    for (int kt = 0; kt < nk; kt += 2) {
-        slice(kt, std::integral_constant<int, 0>{});
-        if (kt + 1 < nk) slice(kt + 1, std::integral_constant<int, 1>{});
     }
 
     // Accumulator layout of a 32x32 block: lane l, register r holds
@@ -289,7 +264,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 template <int MODE, int WN>
 hipError_t launch_grouped(const GemmArgs &a, hipStream_t s) {
     constexpr int BN = 64 * WN;
-    const size_t lds = (size_t)(2 * BM + 2 * BN) * LDK * sizeof(float);
+    const size_t lds = (size_t)(2 * BM + 2 * BN) * KT * sizeof(float);
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t err = hipFuncSetAttribute(
