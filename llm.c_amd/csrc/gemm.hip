@@ -91,19 +91,18 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     const int nmb = max(0, min(2, (rows - wm * 64 + 31) / 32));
     const int li = lane & 31, lh = lane >> 5;
 
-    // Per-thread global source rows for the A tile.  Rows past the expert's
-    // last row reuse its last row: their accumulator rows are never stored,
-    // and unconditional loads keep the K loop free of exec-masked branches.
+    // Rows past the expert's last row reuse its last row: their accumulator
+    // rows are never stored, and every DMA lane stays in bounds.
     // A tile = 16 units of 8 whole rows (32 floats = 128 B each), copied by
     // LDS DMA: lane i of a unit's DMA brings row i / 8's 16-byte chunk
     // (i % 8) ^ (row % 8), so row r's chunk c sits at r * 32 + 4 (c ^ (r % 8))
     // floats and the fragment reads below are free of bank conflicts.
     constexpr int AUW = (BM / 8) / (2 * WN);
-    const int wa = __builtin_amdgcn_readfirstlane(wave);
+    const int wu = __builtin_amdgcn_readfirstlane(wave);   // (uniform: LDS DMA bases)
     const float *a_src[AUW];
 #pragma unroll
     for (int i = 0; i < AUW; ++i) {
-        const int r = 8 * (wa * AUW + i) + (lane >> 3);
+        const int r = 8 * (wu * AUW + i) + (lane >> 3);
         const int c = (lane & 7) ^ (r & 7);
         const int rr = min(r, rows - 1);
         size_t src_row;
@@ -114,12 +113,11 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     auto adma = [&](int k0, int buf) {
         float *as = As + buf * BM * KT;
 #pragma unroll
-        for (int i = 0; i < AUW; ++i) gemm_dma16(a_src[i] + k0, as + (wa * AUW + i) * 256);
+        for (int i = 0; i < AUW; ++i) gemm_dma16(a_src[i] + k0, as + (wu * AUW + i) * 256);
     };
     // B tile = (BN/16) x 2 units, copied whole by LDS DMA: wave w the units
     // w * BUW .. in the packed unit layout (unit u at u * 256 floats).
     constexpr int BUW = (BN / 16 * 2) / (2 * WN);
-    const int wu = __builtin_amdgcn_readfirstlane(wave);
     const float *b_src[BUW];
 #pragma unroll
     for (int i = 0; i < BUW; ++i) {
@@ -166,7 +164,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + aoff[q]);
-                floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * 32 + aoff[q]);
+                floatx4 a1 = *reinterpret_cast<const floatx4 *>(as + 32 * KT + aoff[q]);
                 floatx4 b0 = *reinterpret_cast<const floatx4 *>(bs + 64 * q);
                 floatx4 b1 = *reinterpret_cast<const floatx4 *>(bs + 4 * 256 + 64 * q);
 #pragma unroll
