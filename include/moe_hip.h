@@ -358,8 +358,11 @@ int moe_hip_synchronize(void);
  * step).  graph_begin starts capturing `stream` (NULL: the library stream):
  * work queued on it until graph_end is recorded, not run.  graph_end
  * instantiates the recording into *graph.  Recorded calls must not allocate:
- * run each once beforehand so the library workspace is already sized (a
- * call that would grow it fails the capture). */
+ * run each once beforehand so the library workspace is already sized.  A
+ * graph keeps the workspace addresses it recorded, so while any graph made
+ * by graph_end is alive, during a capture, and for the rest of the process
+ * once a call was recorded into a capture the caller began on its own stream,
+ * a call that would grow the workspace fails with MOE_HIP_ERR_ARG instead. */
 int moe_hip_graph_begin(void *stream);
 int moe_hip_graph_end(void *stream, void **graph);
 int moe_hip_graph_launch(void *graph, void *stream);

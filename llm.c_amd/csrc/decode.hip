@@ -64,6 +64,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
             const int kc = min(kChunk, kspan - k0);
             __syncthreads();   // every wave is done with the previous rows
             stage_lds(hs, a.x, a.F, list, r0, rows, kbeg + k0, kc);
+            __builtin_amdgcn_sched_barrier(0);   // (the counted wait takes the DMA as issued first)
             gemv_prime<1>(ws, ow + 64 * k0, 0, kc / 16, wa, wb);
             WAIT_VMCNT(2 * Unroll<1>::kU);   // the rows, not the weights behind them
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)

@@ -421,6 +421,10 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             const int kc = min(kChunk, a.d - k0);
             __syncthreads();   // every wave is done with the previous rows
             stage_lds<NW>(xs, a.x, a.d, tok, r0, rows, k0, kc);
+            // The counted wait below takes the rows' DMA as issued before the
+            // weight loads, and other waves read those rows after the barrier:
+            // keep the compiler from moving weight loads above the DMA.
+            __builtin_amdgcn_sched_barrier(0);
             if (MEGA && routed && r0 == 0 && k0 == 0) {
                 WAIT_VMCNT(0);   // primed before the rows
             } else {

@@ -38,6 +38,15 @@ hipEvent_t g_tev[2] = {};
 bool g_have_times = false;
 int g_path = 0;   // 0 auto, 1 grouped GEMM, 2 decode GEMVs, 3 unfused, 4 fused, routed apart
 int g_rpath = 0;  // 0 auto, 1 token x expert tiles, 2 one token per lane
+// A captured graph keeps the workspace addresses it recorded, so the
+// workspace must not be freed and reallocated while one may still run:
+// graphs made by moe_hip_graph_end and not yet destroyed, a capture begun by
+// moe_hip_graph_begin, or a capture the caller began on its own stream and
+// recorded a call into (sticky until moe_hip_shutdown: the library cannot
+// see when such a graph is destroyed).
+int g_live_graphs = 0;
+bool g_api_capture = false;
+bool g_ext_capture = false;
 
 int set_err(int code, const char *fmt, ...) {
     g_err = code;
@@ -68,14 +77,29 @@ int ensure_init() {
     return moe_hip_init(-1);
 }
 
-hipStream_t pick_stream(void *s) { return s ? static_cast<hipStream_t>(s) : g_stream; }
+// The stream a call runs on (NULL: the library stream).  Notes a capture
+// the caller began on it (see g_ext_capture).
+hipStream_t pick_stream(void *s) {
+    hipStream_t st = s ? static_cast<hipStream_t>(s) : g_stream;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (!g_api_capture && hipStreamIsCapturing(st, &cs) == hipSuccess &&
+        cs == hipStreamCaptureStatusActive)
+        g_ext_capture = true;
+    return st;
+}
 
-// Grow-only device buffer.
+// Grow-only device buffer.  It refuses to grow while a captured graph may
+// still use its current address (MOE_HIP_ERR_ARG).
 struct DevBuf {
     void *p = nullptr;
     size_t bytes = 0;
     int reserve(size_t need) {
         if (need <= bytes) return MOE_HIP_OK;
+        if (g_live_graphs > 0 || g_api_capture || g_ext_capture)
+            return set_err(MOE_HIP_ERR_ARG,
+                           "the workspace would grow to %zu bytes while a captured graph may "
+                           "still use it: run the largest call once before capturing or destroy "
+                           "the graphs first", need);
         if (p) {
             hipError_t e = hipFree(p);
             p = nullptr;
@@ -125,6 +149,24 @@ int ensure_counters() {
     HIP_TRY(hipMemsetAsync(g_ws.counters.p, 0, sizeof(int) * kMaxCounters, g_stream));
     HIP_TRY(hipStreamSynchronize(g_stream));
     return MOE_HIP_OK;
+}
+
+// The host drop-ins read the bounded-wait flag back with their outputs (a
+// set flag: a device-side wait gave up and the call's results are invalid).
+int g_host_flag = 0;
+int queue_flag_read() {
+    g_host_flag = 0;
+    if (g_ws.counters.bytes < sizeof(int) * kMaxCounters) return MOE_HIP_OK;
+    HIP_TRY(hipMemcpyAsync(&g_host_flag, g_ws.counters.as<int>() + kLayerErr, sizeof(int),
+                           hipMemcpyDeviceToHost, g_stream));
+    return MOE_HIP_OK;
+}
+// After the library stream has synchronised.
+int take_flag() {
+    if (!g_host_flag) return MOE_HIP_OK;
+    g_host_flag = 0;
+    HIP_TRY(hipMemset(g_ws.counters.as<int>() + kLayerErr, 0, sizeof(int)));
+    return set_err(MOE_HIP_ERR_HIP, "a bounded device-side wait gave up (results invalid)");
 }
 
 // Norm: with x_raw set, the rows to route (x, written here) are first
@@ -243,6 +285,7 @@ void moe_hip_shutdown(void) {
     for (auto &kv : g_resident) moe_hip_layer_destroy(kv.second.layer);
     g_resident.clear();
     g_ws.release_all();
+    g_ext_capture = false;
     for (auto &ev : g_ev) (void)hipEventDestroy(ev);
     for (auto &ev : g_tev) (void)hipEventDestroy(ev);
     (void)hipStreamDestroy(g_stream);
@@ -454,6 +497,7 @@ static int attn_decode(MoeHipAttn *a, float *x, int B, const int *pos, float *k_
         return set_err(MOE_HIP_ERR_ARG, "bad attention arguments");
     if (B == 0) return MOE_HIP_OK;
     TRY(ensure_init());
+    hipStream_t s = pick_stream(stream);
     const int qd = a->nh * a->hd, kd = a->nkv * a->hd;
     TRY(g_ws.aq.reserve(sizeof(float) * (size_t)B * qd));
     TRY(g_ws.ao.reserve(sizeof(float) * (size_t)B * qd));
@@ -472,7 +516,6 @@ static int attn_decode(MoeHipAttn *a, float *x, int B, const int *pos, float *k_
     }
     TRY(ensure_counters());
     const bool fused = g_attn_fused && moe::attn_fused_supported(a->hd, a->nh, a->nkv);
-    hipStream_t s = pick_stream(stream);
     moe::AttnArgs aa{};
     aa.x = x; aa.rms_w = a->rms; aa.eps = eps;
     aa.wq = a->wq; aa.wk = a->wk; aa.wv = a->wv; aa.wo = a->wo;
@@ -505,6 +548,7 @@ int moe_hip_decode_block_dev(MoeHipAttn *a, MoeHipLayer *L, const float *rms_ffn
     if (B < 0) return set_err(MOE_HIP_ERR_ARG, "bad block arguments");
     if (B == 0) return MOE_HIP_OK;
     TRY(ensure_init());
+    (void)pick_stream(stream);   // (notes a capture before the workspace is sized)
     float *xn = x_norm;
     if (!xn) {
         TRY(g_ws.xn.reserve(sizeof(float) * (size_t)B * L->d));
@@ -720,10 +764,12 @@ int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream
     return MOE_HIP_OK;
 }
 
+// Routing (and, with dispatch, the stable counting sort by expert) of T
+// rows.  tile_expert: ceil(T k / kGemmBM) + E ints; counter: one device int,
+// zero between launches (the fused dispatch's last workgroup resets it).
 static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
-                      int *counts, int *offsets, int *tile_off, int *perm, hipStream_t s,
-                      bool dispatch = true, Norm nm = Norm{}) {
-    TRY(ensure_counters());
+                      int *counts, int *offsets, int *tile_off, int *perm, int *tile_expert,
+                      int *counter, hipStream_t s, bool dispatch = true, Norm nm = Norm{}) {
     moe::RouteArgs ra{x, L->wr, L->bias, T, L->d, L->E, L->k, probs, ids, gw};
     ra.no_dispatch = dispatch ? 0 : 1;
     if (nm.x_raw) {
@@ -734,10 +780,8 @@ static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *
         ra.wrT = L->wrT;
         ra.wr_nonfinite = L->wr_nonfinite;
     }
-    const size_t max_mtiles = ((size_t)T * L->k + moe::kGemmBM - 1) / moe::kGemmBM + L->E;
-    TRY(g_ws.tile_expert.reserve(sizeof(int) * max_mtiles));
     moe::DispatchArgs da{ids, T * L->k, L->E, moe::kGemmBM, counts, offsets, tile_off, perm,
-                         g_ws.counters.as<int>(), g_ws.tile_expert.as<int>()};
+                         counter, tile_expert};
     if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
     HIP_TRY(moe::launch_route_dispatch(ra, da, s));
     if (g_timing) {
@@ -747,10 +791,13 @@ static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *
     return MOE_HIP_OK;
 }
 
+static size_t max_mtiles_of(size_t n, int E) { return (n + moe::kGemmBM - 1) / moe::kGemmBM + E; }
+
 int moe_hip_route_dev(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
                       int *counts, int *offsets, int *perm, void *stream) {
     if (!L || (!x && T > 0) || T < 0) return set_err(MOE_HIP_ERR_ARG, "bad route arguments");
     if (T == 0) return MOE_HIP_OK;
+    hipStream_t s = pick_stream(stream);
     const size_t n = (size_t)T * L->k;
     TRY(g_ws.ids.reserve(sizeof(int) * n));
     TRY(g_ws.gw.reserve(sizeof(float) * n));
@@ -758,43 +805,45 @@ int moe_hip_route_dev(MoeHipLayer *L, const float *x, int T, float *probs, int *
     TRY(g_ws.offsets.reserve(sizeof(int) * (L->E + 1)));
     TRY(g_ws.tile_off.reserve(sizeof(int) * (L->E + 1)));
     TRY(g_ws.perm.reserve(sizeof(int) * n));
-    hipStream_t s = pick_stream(stream);
+    TRY(g_ws.tile_expert.reserve(sizeof(int) * max_mtiles_of(n, L->E)));
+    TRY(ensure_counters());
     return route_impl(L, x, T, probs, ids ? ids : g_ws.ids.as<int>(), gw ? gw : g_ws.gw.as<float>(),
                       counts ? counts : g_ws.counts.as<int>(),
                       offsets ? offsets : g_ws.offsets.as<int>(), g_ws.tile_off.as<int>(),
-                      perm ? perm : g_ws.perm.as<int>(), s);
+                      perm ? perm : g_ws.perm.as<int>(), g_ws.tile_expert.as<int>(),
+                      g_ws.counters.as<int>(), s);
 }
 
-int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
-                        int accumulate, void *stream) {
-    return forward_impl(L, x, T, out, probs, ids, accumulate, stream, Norm{});
-}
+namespace {
 
-// x: the rows to route and multiply; with nm.x_raw set they are written
-// first, as rms_norm(nm.x_raw) (then x must be writable device memory).
-static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
-                        int accumulate, void *stream, Norm nm) {
-    if (!L || T < 0 || (T > 0 && (!x || !out))) return set_err(MOE_HIP_ERR_ARG, "bad forward arguments");
-    if (T == 0) return MOE_HIP_OK;
+// How a forward of T rows runs (expert-product path, partial products per
+// slot) and the device memory it takes.
+struct FwdPlan {
+    size_t n = 0;           // T * k assignments
+    int max_mtiles = 0;     // grouped GEMM m-tile bound
+    bool use_decode = false, fused = false, one_launch = false;
+    int ksplit = 1;         // partial products per slot the combine adds
+    size_t h_floats = 0;    // H [n x F] (grouped GEMMs, unfused decode)
+    size_t ys_floats = 0;   // per-slot products / split-K partials
+};
+
+// The device buffers of one forward.
+struct FwdBufs {
+    int *ids = nullptr;     // [n] (used when the caller passes none)
+    float *gw = nullptr;    // [n]
+    int *counts = nullptr, *offsets = nullptr, *tile_off = nullptr, *tile_expert = nullptr;
+    int *perm = nullptr;    // [n]
+    float *h = nullptr, *ys = nullptr;
+    int *counters = nullptr;   // kMaxCounters ints, zero between launches
+};
+
+int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
     const int d = L->d, F = L->F, E = L->E, k = L->k;
     const size_t n = (size_t)T * k;
     if (n > (size_t)0x7fffffff / (size_t)(F > d ? F : d))
         return set_err(MOE_HIP_ERR_UNSUPPORTED, "T*k*max(F,d) exceeds 32-bit indexing");
-
-    TRY(g_ws.ids.reserve(sizeof(int) * n));
-    TRY(g_ws.gw.reserve(sizeof(float) * n));
-    TRY(g_ws.counts.reserve(sizeof(int) * E));
-    TRY(g_ws.offsets.reserve(sizeof(int) * (E + 1)));
-    TRY(g_ws.tile_off.reserve(sizeof(int) * (E + 1)));
-    TRY(g_ws.perm.reserve(sizeof(int) * n));
-    TRY(g_ws.h.reserve(sizeof(float) * n * F));
-    TRY(g_ws.ys.reserve(sizeof(float) * n * d));
-    hipStream_t s = pick_stream(stream);
-    int *ids_d = ids ? ids : g_ws.ids.as<int>();
-    float *gw = g_ws.gw.as<float>();
-    int *offsets = g_ws.offsets.as<int>(), *tile_off = g_ws.tile_off.as<int>();
-    int *perm = g_ws.perm.as<int>();
-
+    p->n = n;
+    p->max_mtiles = (int)max_mtiles_of(n, E);
     // Expert products: skinny decode GEMVs (which find their own slots from
     // the expert ids, so routing skips the dispatch) or grouped GEMMs.
     // (the decode kernels address one expert's gate/up block, 2*F*d floats,
@@ -805,51 +854,98 @@ static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float
         return set_err(MOE_HIP_ERR_UNSUPPORTED,
                        "decode kernels need ffn_hidden %% 64 == 0, T*k <= %d and "
                        "8*ffn_hidden*d_model < 2^31", moe::kDecodeMaxSlots);
-    const bool use_decode = g_path >= 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
+    p->use_decode = g_path >= 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
     // Mode 2 runs routing and the fused expert items (4 waves) as one launch
     // where it fits; everything else routes first (the one-launch layer is
     // not yet faster: its router competes with the expert weight stream).
     const bool one_launch_ok = g_path == 2 && g_rpath != 1 && moe::decode_layer_supported(d, E);
     const int fused_splits = F / (16 * (one_launch_ok ? 4 : moe::decode_fused_waves(d, F)));
-    const size_t fused_bytes = sizeof(float) * (size_t)fused_splits * n * d;
-    const bool fused = use_decode && g_path != 3 && fused_bytes <= moe::kFusedPartialBytes;
-    const bool one_launch = fused && one_launch_ok;
-    if (nm.x_raw && one_launch) {   // (its router blocks do not normalise)
+    const size_t fused_floats = (size_t)fused_splits * n * d;
+    p->fused = p->use_decode && g_path != 3 && sizeof(float) * fused_floats <= moe::kFusedPartialBytes;
+    p->one_launch = p->fused && one_launch_ok;
+    if (p->fused) {
+        p->ksplit = fused_splits;
+        p->ys_floats = fused_floats;
+    } else if (p->use_decode) {
+        p->ksplit = moe::decode_ksplit(d, F, E);
+        p->h_floats = n * F;
+        p->ys_floats = n * d * p->ksplit;
+    } else {
+        // Small grids split the down projection's reduction; the combine adds
+        // the splits in order.
+        p->ksplit = moe::gemm_plan(d, F, p->max_mtiles, true).ksplit;
+        p->h_floats = n * F;
+        p->ys_floats = (size_t)p->ksplit * n * d;
+    }
+    return MOE_HIP_OK;
+}
+
+// Buffers from the grow-only workspace.
+int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
+    TRY(g_ws.ids.reserve(sizeof(int) * p.n));
+    TRY(g_ws.gw.reserve(sizeof(float) * p.n));
+    TRY(g_ws.counts.reserve(sizeof(int) * L->E));
+    TRY(g_ws.offsets.reserve(sizeof(int) * (L->E + 1)));
+    TRY(g_ws.tile_off.reserve(sizeof(int) * (L->E + 1)));
+    TRY(g_ws.tile_expert.reserve(sizeof(int) * p.max_mtiles));
+    TRY(g_ws.perm.reserve(sizeof(int) * p.n));
+    if (p.h_floats) TRY(g_ws.h.reserve(sizeof(float) * p.h_floats));
+    TRY(g_ws.ys.reserve(sizeof(float) * p.ys_floats));
+    TRY(ensure_counters());
+    b->ids = g_ws.ids.as<int>(); b->gw = g_ws.gw.as<float>();
+    b->counts = g_ws.counts.as<int>(); b->offsets = g_ws.offsets.as<int>();
+    b->tile_off = g_ws.tile_off.as<int>(); b->tile_expert = g_ws.tile_expert.as<int>();
+    b->perm = g_ws.perm.as<int>(); b->h = g_ws.h.as<float>(); b->ys = g_ws.ys.as<float>();
+    b->counters = g_ws.counters.as<int>();
+    return MOE_HIP_OK;
+}
+
+}  // namespace
+
+int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
+                        int accumulate, void *stream) {
+    return forward_impl(L, x, T, out, probs, ids, accumulate, stream, Norm{});
+}
+
+// The layer on planned buffers.  x: the rows to route and multiply; with
+// nm.x_raw set they are written first, as rms_norm(nm.x_raw) (then x must be
+// writable device memory).
+static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
+                       int accumulate, hipStream_t s, Norm nm, const FwdPlan &p,
+                       const FwdBufs &b) {
+    const int d = L->d, F = L->F, E = L->E, k = L->k;
+    const size_t n = p.n;
+    int *ids_d = ids ? ids : b.ids;
+    if (nm.x_raw && p.one_launch) {   // (its router blocks do not normalise)
         HIP_TRY(moe::launch_rms_norm(nm.x_raw, nm.rms_w, nm.eps, T, d, const_cast<float *>(x), s));
         nm = Norm{};
     }
-    if (!one_launch)
-        TRY(route_impl(L, x, T, probs, ids_d, gw, g_ws.counts.as<int>(), offsets, tile_off, perm,
-                       s, !use_decode, nm));
-    int ksplit = 1;
-    if (use_decode) {
+    if (!p.one_launch)
+        TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
+                       b.tile_expert, b.counters, s, !p.use_decode, nm));
+    if (p.use_decode) {
         // Fused gate/up + split-K down while its partials stay small, else
         // gate/up then down.
         moe::DecodeArgs gu{};
         gu.x = x; gu.ids = ids_d; gu.topk = k; gu.w = L->wgu;
         gu.d = d; gu.F = F; gu.E = E; gu.ksplit = 1; gu.nslots = (int)n;
-        if (one_launch) {
-            TRY(ensure_counters());
-            ksplit = fused_splits;
-            TRY(g_ws.ys.reserve(fused_bytes));
-            gu.out = g_ws.ys.as<float>();
+        if (p.one_launch) {
+            gu.out = b.ys;
             gu.w2 = L->wdT;
             moe::LayerArgs la{};
-            la.r = moe::RouteArgs{x, L->wr, L->bias, T, d, E, k, probs, ids_d, gw};
+            la.r = moe::RouteArgs{x, L->wr, L->bias, T, d, E, k, probs, ids_d, b.gw};
             la.r.wrT = L->wrT;
             la.r.wr_nonfinite = L->wr_nonfinite;
             la.r.no_dispatch = 1;
             la.g = gu;
-            la.sync = g_ws.counters.as<int>() + kLayerSync;
-            la.err = g_ws.counters.as<int>() + kLayerErr;
+            la.sync = b.counters + kLayerSync;
+            la.err = b.counters + kLayerErr;
             if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
             HIP_TRY(moe::launch_decode_layer(la, s));
             if (g_timing)
                 for (int i = 1; i <= 4; ++i) HIP_TRY(hipEventRecord(g_ev[i], s));
-        } else if (fused) {
-            ksplit = fused_splits;
-            TRY(g_ws.ys.reserve(fused_bytes));
-            gu.out = g_ws.ys.as<float>();
+        } else if (p.fused) {
+            gu.out = b.ys;
             gu.w2 = L->wdT;
             HIP_TRY(moe::launch_decode_gateup(gu, s));
             if (g_timing) {
@@ -857,43 +953,47 @@ static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float
                 HIP_TRY(hipEventRecord(g_ev[4], s));
             }
         } else {
-            ksplit = moe::decode_ksplit(d, F, E);
-            TRY(g_ws.ys.reserve(sizeof(float) * n * d * ksplit));
-            gu.out = g_ws.h.as<float>();
+            gu.out = b.h;
             HIP_TRY(moe::launch_decode_gateup(gu, s));
             if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
             moe::DecodeArgs dn{};
-            dn.x = g_ws.h.as<float>(); dn.ids = ids_d; dn.topk = k; dn.w = L->wdT;
-            dn.out = g_ws.ys.as<float>(); dn.d = d; dn.F = F; dn.E = E; dn.ksplit = ksplit;
+            dn.x = b.h; dn.ids = ids_d; dn.topk = k; dn.w = L->wdT;
+            dn.out = b.ys; dn.d = d; dn.F = F; dn.E = E; dn.ksplit = p.ksplit;
             dn.nslots = (int)n;
             HIP_TRY(moe::launch_decode_down(dn, s));
             if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
         }
     } else {
-        const int max_mtiles = (int)((n + moe::kGemmBM - 1) / moe::kGemmBM) + E;
-        const int *tile_e = g_ws.tile_expert.as<int>();
-        moe::GemmArgs gu{x, perm, k, L->wgu, g_ws.h.as<float>(), offsets, tile_off, tile_e, E, d,
-                         2 * F, F, max_mtiles};
+        moe::GemmArgs gu{x, b.perm, k, L->wgu, b.h, b.offsets, b.tile_off, b.tile_expert, E, d,
+                         2 * F, F, p.max_mtiles};
         HIP_TRY(moe::launch_gemm_gateup(gu, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
-        moe::GemmArgs dn{g_ws.h.as<float>(), perm, k, L->wdT, g_ws.ys.as<float>(), offsets, tile_off,
-                         tile_e, E, F, d, d, max_mtiles};
-        // Small grids split the down projection's reduction; the combine adds
-        // the splits in order.
-        dn.ksplit = ksplit = moe::gemm_plan(d, F, max_mtiles, true).ksplit;
+        moe::GemmArgs dn{b.h, b.perm, k, L->wdT, b.ys, b.offsets, b.tile_off, b.tile_expert, E, F,
+                         d, d, p.max_mtiles};
+        dn.ksplit = p.ksplit;
         dn.split_stride = n * (size_t)d;
-        if (ksplit > 1) TRY(g_ws.ys.reserve(sizeof(float) * (size_t)ksplit * n * d));
-        dn.c = g_ws.ys.as<float>();
         HIP_TRY(moe::launch_gemm_down(dn, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
     }
-    moe::CombineArgs ca{g_ws.ys.as<float>(), gw, out, T, d, k, accumulate, ksplit, n * (size_t)d};
+    moe::CombineArgs ca{b.ys, b.gw, out, T, d, k, accumulate, p.ksplit, n * (size_t)d};
     HIP_TRY(moe::launch_combine(ca, s));
     if (g_timing) {
         HIP_TRY(hipEventRecord(g_ev[5], s));
         g_have_times = true;
     }
     return MOE_HIP_OK;
+}
+
+static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
+                        int accumulate, void *stream, Norm nm) {
+    if (!L || T < 0 || (T > 0 && (!x || !out))) return set_err(MOE_HIP_ERR_ARG, "bad forward arguments");
+    if (T == 0) return MOE_HIP_OK;
+    hipStream_t s = pick_stream(stream);
+    FwdPlan p;
+    TRY(plan_forward(L, T, &p));
+    FwdBufs b;
+    TRY(workspace_bufs(L, p, &b));
+    return run_forward(L, x, T, out, probs, ids, accumulate, s, nm, p, b);
 }
 
 int moe_hip_set_router_path(int mode) {
@@ -964,8 +1064,9 @@ int moe_hip_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg
                            hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
                            hipMemcpyDeviceToHost, g_stream));
+    TRY(queue_flag_read());
     HIP_TRY(hipStreamSynchronize(g_stream));
-    return MOE_HIP_OK;
+    return take_flag();
 }
 
 void moe_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg, ForwardCache *cache,
@@ -991,8 +1092,9 @@ int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x
     HIP_TRY(hipMemcpyAsync(dx, x, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
     TRY(moe_hip_forward_dev(L, dxn, n_rows, dx, nullptr, nullptr, 1, g_stream));
     HIP_TRY(hipMemcpyAsync(x, dx, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
+    TRY(queue_flag_read());
     HIP_TRY(hipStreamSynchronize(g_stream));
-    return MOE_HIP_OK;
+    return take_flag();
 }
 
 void moe_decode_step(const MoEWeights *w, const ModelConfig *cfg, const float *x_norm, float *x) {
@@ -1029,9 +1131,12 @@ int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dou
     TRY(g_ws.offsets.reserve(sizeof(int) * (E + 1)));
     TRY(g_ws.tile_off.reserve(sizeof(int) * (E + 1)));
     TRY(g_ws.perm.reserve(sizeof(int) * n));
+    TRY(g_ws.tile_expert.reserve(sizeof(int) * max_mtiles_of(n, E)));
+    TRY(ensure_counters());
     TRY(route_impl(L, x, T, g_ws.probs.as<float>(), g_ws.ids.as<int>(), g_ws.gw.as<float>(),
                    g_ws.counts.as<int>(), g_ws.offsets.as<int>(), g_ws.tile_off.as<int>(),
-                   g_ws.perm.as<int>(), s, true));
+                   g_ws.perm.as<int>(), g_ws.tile_expert.as<int>(), g_ws.counters.as<int>(), s,
+                   true));
     // Weights: the packed ones and their unit transposes (tile engine), or
     // the reference layout wg, wu [E][d x F], wd [E][F x d].
     const size_t dF = (size_t)d * F;
@@ -1078,6 +1183,7 @@ int moe_hip_ffn_sublayer_dev(MoeHipLayer *L, float *x, const float *rms_w, float
         return set_err(MOE_HIP_ERR_ARG, "bad sublayer arguments");
     if (T == 0) return MOE_HIP_OK;
     TRY(ensure_init());
+    (void)pick_stream(stream);   // (notes a capture before the workspace is sized)
     float *xn = x_norm;
     if (!xn) {
         TRY(g_ws.xn.reserve(sizeof(float) * (size_t)T * L->d));
@@ -1123,7 +1229,9 @@ int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,
                            hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
                            hipMemcpyDeviceToHost, g_stream));
+    TRY(queue_flag_read());
     HIP_TRY(hipStreamSynchronize(g_stream));
+    TRY(take_flag());
     // Residual 2 (src/transformer.c:767, mat_add_inplace).
     for (size_t i = 0; i < xd; ++i) x->data[i] = x->data[i] + fo.data[i];
     return MOE_HIP_OK;
@@ -1185,7 +1293,9 @@ struct MoeHipGraph {
 
 int moe_hip_graph_begin(void *stream) {
     TRY(ensure_init());
-    HIP_TRY(hipStreamBeginCapture(pick_stream(stream), hipStreamCaptureModeThreadLocal));
+    hipStream_t s = pick_stream(stream);
+    HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    g_api_capture = true;
     return MOE_HIP_OK;
 }
 
@@ -1194,12 +1304,14 @@ int moe_hip_graph_end(void *stream, void **graph) {
     *graph = nullptr;
     MoeHipGraph *G = new MoeHipGraph();
     hipError_t e = hipStreamEndCapture(pick_stream(stream), &G->graph);
+    g_api_capture = false;
     if (e == hipSuccess) e = hipGraphInstantiate(&G->exec, G->graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         if (G->graph) (void)hipGraphDestroy(G->graph);
         delete G;
         return set_err(MOE_HIP_ERR_HIP, "graph capture: %s", hipGetErrorString(e));
     }
+    ++g_live_graphs;   // (the workspace stays where it is until the graph is destroyed)
     *graph = G;
     return MOE_HIP_OK;
 }
@@ -1216,16 +1328,24 @@ int moe_hip_graph_destroy(void *graph) {
     if (G->exec) (void)hipGraphExecDestroy(G->exec);
     if (G->graph) (void)hipGraphDestroy(G->graph);
     delete G;
+    if (g_live_graphs > 0) --g_live_graphs;
     return MOE_HIP_OK;
 }
 
 int moe_hip_device_check(void) {
     TRY(ensure_init());
     HIP_TRY(hipStreamSynchronize(g_stream));
-    if (g_ws.counters.bytes < sizeof(int) * kMaxCounters) return MOE_HIP_OK;
-    int flag = 0;
-    HIP_TRY(hipMemcpy(&flag, g_ws.counters.as<int>() + kLayerErr, sizeof(int), hipMemcpyDeviceToHost));
-    if (!flag) return MOE_HIP_OK;
-    HIP_TRY(hipMemset(g_ws.counters.as<int>() + kLayerErr, 0, sizeof(int)));
+    int *flags[1] = {g_ws.counters.bytes >= sizeof(int) * kMaxCounters
+                         ? g_ws.counters.as<int>() + kLayerErr : nullptr};
+    bool raised = false;
+    for (int *f : flags) {
+        if (!f) continue;
+        int flag = 0;
+        HIP_TRY(hipMemcpy(&flag, f, sizeof(int), hipMemcpyDeviceToHost));
+        if (!flag) continue;
+        raised = true;
+        HIP_TRY(hipMemset(f, 0, sizeof(int)));
+    }
+    if (!raised) return MOE_HIP_OK;
     return set_err(MOE_HIP_ERR_HIP, "a bounded device-side wait gave up (results invalid)");
 }

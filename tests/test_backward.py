@@ -73,6 +73,58 @@ def test_oracle_closed_forms():
     assert np.abs(g["dlogits"].sum(axis=1)).max() < 1e-12
 
 
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
+def test_oracle_forward64_matches_compiled_reference(name):
+    """moe_forward64, the forward whose finite differences pin the backward,
+    against the outputs of the reference's own moe_forward
+    (src/transformer.c:287-366, compiled from source): its probabilities, its
+    top-k under the reference's tie rule, and the layer output with the
+    reference's gate renormalisation all agree with the golden fixtures
+    (fp32 reference against fp64 restatement: 1e-6 relative).  A mistake
+    shared by the backward and this forward (the renormalisation, the slot
+    weights, the SwiGLU side) would show here."""
+    from conftest import CONFIGS
+    c = CONFIGS[name]
+    d, F, E, k = c["d"], c["F"], c["E"], c["k"]
+    bias = None
+    if name == "c1":
+        g = np.load(os.path.join(GOLDEN, "golden_c1.npz"))
+        out_g, probs_g, ids_g = g["out"], g["probs"], g["ids"]
+        x = orc.synth((c["T"], d), 0, 0, 1.0)
+        seed = 0
+    else:
+        g = np.load(os.path.join(GOLDEN, "golden_moe.npz"))
+        out_g, probs_g, ids_g = g[f"{name}_out"], g[f"{name}_probs"], g[f"{name}_ids"]
+        x = orc.synth((out_g.shape[0], d), 3, 0, 1.0)
+        seed = 3
+        if name == "c5":
+            bias = np.load(os.path.join(GOLDEN, "zipf_bias_e64_k4.npy")).astype(np.float64)
+    need = sorted(set(ids_g.ravel().tolist()))
+    wr, ex = orc.synth_layer_host(d, F, E, k, seed, c["std_router"], c["std_expert"],
+                                  experts=need)
+    wg = {e: ex[e][0] for e in need}
+    wu = {e: ex[e][1] for e in need}
+    wd = {e: ex[e][2] for e in need}
+    out, p = mb.moe_forward64(x, wr, wg, wu, wd, ids_g, bias)
+    # E < 8: the reference's softmax is all scalar tail (libm expf, correctly
+    # rounded to ~1 ulp); E >= 8 takes exp_avx2 (src/matrix.c:82-116), a
+    # degree-6 Taylor polynomial whose relative error reaches 1.5e-5, which
+    # the fp64 exp does not share: the bar follows that error.
+    rel_p = 1e-6 if E < 8 else 2e-5
+    assert np.all(np.abs(p - probs_g) <= rel_p * probs_g + 1e-12)
+    # the reference's top-k of its probabilities: descending, ties to the
+    # lower expert id, equal to the ids it chose
+    order = np.lexsort((np.broadcast_to(np.arange(E), probs_g.shape), -probs_g), axis=1)[:, :k]
+    assert np.array_equal(order, ids_g)
+    # Renormalised gate weights carry the probabilities' relative error; a
+    # missing renormalisation or a wrong slot weight is off by 10 % or more.
+    rel = orc.rel_l2(out, out_g)
+    assert rel < (1e-6 if E < 8 else 1e-5), rel
+
+
 # ---------------------------------------------------------------- GPU
 def run_device_backward(d, F, E, k, T, seed, aux_coef, accumulate_twice=False):
     layer = mh.Layer(d, F, E, k)

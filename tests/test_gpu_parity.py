@@ -276,7 +276,9 @@ def test_forward_large_skewed(accumulate):
 def test_forward_c5_sampled():
     """Config 5 at full size on the device (12.9 GB of experts, Zipf-skewed
     router bias when its fixture exists); routing compared for all tokens,
-    the layer output for a sample of tokens."""
+    the layer output for a sample of tokens: for every expert the first and
+    the last token routed to it (so every expert's first and last 128-row
+    m-tile of both grouped GEMMs is checked), plus a few random tokens."""
     c = CONFIGS["c5"]
     T, d, F, E, k = c["T"], c["d"], c["F"], c["E"], c["k"]
     say("c5: filling 12.9 GB of synthetic experts on the device")
@@ -303,15 +305,27 @@ def test_forward_c5_sampled():
     counts = np.bincount(ids.ravel(), minlength=E)
     say(f"c5: expert load max/mean {counts.max() / counts.mean():.2f}")
     rng = np.random.default_rng(0)
-    sample = np.sort(rng.choice(T, 6, replace=False))
-    hot = int(np.argmax(counts))
-    hot_tok = int(np.nonzero((ids == hot).any(1))[0][-1])
-    sample = np.unique(np.concatenate([sample, [0, T - 1, hot_tok]]))
+    sample = [rng.choice(T, 6, replace=False), [0, T - 1]]
+    for e in range(E):
+        # the dispatch orders an expert's rows by token: its first token sits
+        # in its first m-tile, its last token in its last one
+        toks = np.nonzero((ids == e).any(1))[0]
+        if toks.size:
+            sample.append([toks[0], toks[-1]])
+    sample = np.unique(np.concatenate(sample))
     need = sorted(set(ids[sample].ravel().tolist()))
-    say(f"c5: generating {len(need)} experts on the host for {sample.size} sampled tokens")
-    _, ex = orc.synth_layer_host(d, F, E, k, 5, c["std_router"], c["std_expert"], experts=need)
-    o_ref, _, _ = orc.moe_forward_experts(x[sample], wr, ex, d, F, E, k, bias, nthreads=16)
-    assert_close(dout.to_host()[sample], o_ref, "c5 sampled")
+    say(f"c5: reading {len(need)} experts back for {sample.size} sampled tokens")
+    out = dout.to_host()
+    o_ref = np.empty((sample.size, d), np.float32)
+    # the oracle in token batches whose experts fit comfortably in host memory
+    for lo in range(0, sample.size, 32):
+        part = sample[lo:lo + 32]
+        ex = {e: layer.get_expert(e) for e in sorted(set(ids[part].ravel().tolist()))}
+        o_ref[lo:lo + 32], _, _ = orc.moe_forward_experts(x[part], wr, ex, d, F, E, k, bias,
+                                                          nthreads=16)
+        del ex
+    assert_close(out[sample], o_ref, f"c5 sampled ({sample.size} tokens, every expert's first "
+                                     "and last m-tile)")
     layer.close()
 
 
@@ -446,6 +460,42 @@ def test_graph_replay(path):
         mh.set_expert_path(0)
         for L in layers:
             L.close()
+
+
+def test_workspace_does_not_move_under_a_live_graph():
+    """A graph keeps the workspace addresses it recorded.  While one is alive,
+    a call that would grow the workspace (here the staging buffer of a
+    larger layer's synthetic fill) is refused with MOE_HIP_ERR_ARG instead of
+    freeing memory the graph still uses; the graph still replays correctly,
+    and once it is destroyed the same call succeeds."""
+    T, d, F, E, k = 16, 128, 256, 4, 2
+    layer = mh.Layer(d, F, E, k)
+    big = mh.Layer(4096, 16384, 1, 1)   # its fill stages 805 MB, more than any other test
+    try:
+        layer.fill_synthetic(3, 0.02, 0.02)
+        x = mh.DeviceArray((T, d))
+        mh.fill_normal_dev(x.ptr, T * d, 3, 0, 0.0, 1.0)
+        out = mh.DeviceArray((T, d))
+        layer.forward_dev(x.ptr, T, out.ptr)      # eager; sizes the workspace
+        mh.synchronize()
+        ref = out.to_host()
+        with mh.Graph() as g:
+            layer.forward_dev(x.ptr, T, out.ptr)
+        try:
+            rc = mh.lib().moe_hip_layer_fill_synthetic(big.h, 1, 0.02, 0.02)
+            assert rc == 1, rc
+            assert b"captured graph" in mh.lib().moe_hip_last_error_message()
+            out.zero()
+            g.launch()
+            mh.synchronize()
+            assert np.array_equal(bits(out.to_host()), bits(ref))
+        finally:
+            g.close()
+        big.fill_synthetic(1, 0.02, 0.02)        # no live graph: it may grow now
+        mh.synchronize()
+    finally:
+        layer.close()
+        big.close()
 
 
 EDGE_CASES = [
