@@ -184,6 +184,23 @@ int moe_hip_layer_get_router(MoeHipLayer *layer, float *wr);
 int moe_hip_forward_dev(MoeHipLayer *layer, const float *x, int T, float *out,
                         float *probs, int *ids, int accumulate, void *stream);
 
+/* moe_hip_forward_dev without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Every
+ * temporary (routing, dispatch, expert activations, partial products,
+ * completion counters) lives in a fixed 64 MiB device array of the library,
+ * one per GPU, held until the process ends; the layer's weights and the
+ * caller's x, out, probs and ids are the only other memory touched.  A call
+ * whose temporaries exceed 64 MiB fails with MOE_HIP_ERR_UNSUPPORTED (the
+ * message gives the need): at d_model 256, ffn_hidden 1024 that is above
+ * about 10k tokens at top-2; the 64-sequence decode layer of d_model 512,
+ * ffn_hidden 2048, E=16 takes 4.2 MB.  The library must be initialised
+ * (moe_hip_init or a layer created) on the calling device first.  All calls
+ * on one GPU share its array and each call keeps it until the next: calls
+ * that overlap on one GPU (two streams, two threads) race. */
+int moe_hip_forward_dev_noalloc(MoeHipLayer *layer, const float *x, int T, float *out,
+                                float *probs, int *ids, int accumulate, void *stream);
+
 /* rms_norm (src/matrix.c:666-711) on device rows: y [rows x cols] =
  * (x * inv_rms) * w with the reference's summation order and fused
  * multiply-adds, and a correctly rounded 1/sqrt (see moe_block_ffn). */
@@ -362,7 +379,8 @@ int moe_hip_synchronize(void);
  * graph keeps the workspace addresses it recorded, so while any graph made
  * by graph_end is alive, during a capture, and for the rest of the process
  * once a call was recorded into a capture the caller began on its own stream,
- * a call that would grow the workspace fails with MOE_HIP_ERR_ARG instead. */
+ * a call that would grow the workspace fails with MOE_HIP_ERR_ARG instead
+ * (moe_hip_forward_dev_noalloc never grows anything). */
 int moe_hip_graph_begin(void *stream);
 int moe_hip_graph_end(void *stream, void **graph);
 int moe_hip_graph_launch(void *graph, void *stream);

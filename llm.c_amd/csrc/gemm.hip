@@ -446,6 +446,10 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(float *dst, size_t n, 
         dst[i] = synth_normal(seed, stream_id, i, mean, std);
 }
 
+__global__ __launch_bounds__(256) void zero_ints_kernel(int *p, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+
 }  // namespace
 
 GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split) {
@@ -580,6 +584,13 @@ hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stre
     unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL(fill_normal_kernel, dim3(blocks), dim3(256), 0, s, dst, n, seed,
                        stream_id, mean, std);
+    return hipGetLastError();
+}
+
+hipError_t launch_zero_ints(int *p, int n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)std::min(1024, (n + 255) / 256)), dim3(256),
+                       0, s, p, n);
     return hipGetLastError();
 }
 

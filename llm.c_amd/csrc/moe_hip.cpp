@@ -25,6 +25,13 @@ struct MoeHipLayer {
     float *wdT = nullptr;    // [E][d][F]
 };
 
+// Temporaries of the allocation-free forward (moe_hip_forward_dev_noalloc):
+// a fixed device array, one copy per GPU the library runs on, held until the
+// process ends.  In host code its name is not a device address: host code
+// uses the per-device address hipGetSymbolAddress returns (scratch_of).
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
 
 int g_err = MOE_HIP_OK;
@@ -98,8 +105,8 @@ struct DevBuf {
         if (g_live_graphs > 0 || g_api_capture || g_ext_capture)
             return set_err(MOE_HIP_ERR_ARG,
                            "the workspace would grow to %zu bytes while a captured graph may "
-                           "still use it: run the largest call once before capturing or destroy "
-                           "the graphs first", need);
+                           "still use it: run the largest call once before capturing, destroy "
+                           "the graphs first, or use moe_hip_forward_dev_noalloc", need);
         if (p) {
             hipError_t e = hipFree(p);
             p = nullptr;
@@ -148,6 +155,27 @@ int ensure_counters() {
     TRY(g_ws.counters.reserve(sizeof(int) * kMaxCounters));
     HIP_TRY(hipMemsetAsync(g_ws.counters.p, 0, sizeof(int) * kMaxCounters, g_stream));
     HIP_TRY(hipStreamSynchronize(g_stream));
+    return MOE_HIP_OK;
+}
+
+// Each device's address of scratch, resolved once per device with that
+// device current (moe_hip_init, or the first allocation-free call there).
+constexpr int kMaxDevices = 64;
+char *g_scratch[kMaxDevices] = {};
+
+// The current device's scratch; on its first use there the counter block at
+// its start (kMaxCounters ints, zero between launches) is cleared on s.
+int scratch_of(hipStream_t s, char **out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return set_err(MOE_HIP_ERR_NODEV, "device %d", dev);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        HIP_TRY(moe::launch_zero_ints(static_cast<int *>(p), kMaxCounters, s));
+        g_scratch[dev] = static_cast<char *>(p);
+    }
+    *out = g_scratch[dev];
     return MOE_HIP_OK;
 }
 
@@ -274,6 +302,9 @@ int moe_hip_init(int device) {
     HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     for (auto &ev : g_ev) HIP_TRY(hipEventCreate(&ev));
     for (auto &ev : g_tev) HIP_TRY(hipEventCreate(&ev));
+    char *sp = nullptr;
+    TRY(scratch_of(g_stream, &sp));
+    HIP_TRY(hipStreamSynchronize(g_stream));
     g_device = device;
     g_init = true;
     return MOE_HIP_OK;
@@ -900,6 +931,32 @@ int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
     return MOE_HIP_OK;
 }
 
+// Buffers carved from one fixed device block of cap bytes at base (the
+// allocation-free entry point's scratch array).  Returns the bytes needed in
+// *need; the pointers are set only when they fit.
+void carve_bufs(const MoeHipLayer *L, const FwdPlan &p, char *base, size_t cap, FwdBufs *b,
+                size_t *need) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> void * {
+        void *q = base + off;
+        off += (bytes + 255) & ~(size_t)255;
+        return q;
+    };
+    FwdBufs c;
+    c.counters = static_cast<int *>(take(sizeof(int) * kMaxCounters));   // (first: cleared at set-up)
+    c.ids = static_cast<int *>(take(sizeof(int) * p.n));
+    c.gw = static_cast<float *>(take(sizeof(float) * p.n));
+    c.counts = static_cast<int *>(take(sizeof(int) * L->E));
+    c.offsets = static_cast<int *>(take(sizeof(int) * (L->E + 1)));
+    c.tile_off = static_cast<int *>(take(sizeof(int) * (L->E + 1)));
+    c.tile_expert = static_cast<int *>(take(sizeof(int) * p.max_mtiles));
+    c.perm = static_cast<int *>(take(sizeof(int) * p.n));
+    c.h = p.h_floats ? static_cast<float *>(take(sizeof(float) * p.h_floats)) : nullptr;
+    c.ys = static_cast<float *>(take(sizeof(float) * p.ys_floats));
+    *need = off;
+    if (off <= cap) *b = c;
+}
+
 }  // namespace
 
 int moe_hip_forward_dev(MoeHipLayer *L, const float *x, int T, float *out, float *probs, int *ids,
@@ -994,6 +1051,29 @@ static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float
     FwdBufs b;
     TRY(workspace_bufs(L, p, &b));
     return run_forward(L, x, T, out, probs, ids, accumulate, s, nm, p, b);
+}
+
+// moe_hip_forward_dev on the fixed scratch array: no device memory is
+// allocated or freed, so callers under graph capture or in serving loops
+// can use it.  Every call on a device shares that device's array.
+int moe_hip_forward_dev_noalloc(MoeHipLayer *L, const float *x, int T, float *out, float *probs,
+                                int *ids, int accumulate, void *stream) {
+    if (!L || T < 0 || (T > 0 && (!x || !out))) return set_err(MOE_HIP_ERR_ARG, "bad forward arguments");
+    if (!g_init) return set_err(MOE_HIP_ERR_ARG, "the library is not initialised (moe_hip_init)");
+    if (T == 0) return MOE_HIP_OK;
+    hipStream_t s = pick_stream(stream);
+    char *base = nullptr;
+    TRY(scratch_of(s, &base));
+    FwdPlan p;
+    TRY(plan_forward(L, T, &p));
+    FwdBufs b;
+    size_t need = 0;
+    carve_bufs(L, p, base, kScratchBytes, &b, &need);
+    if (need > kScratchBytes)
+        return set_err(MOE_HIP_ERR_UNSUPPORTED,
+                       "this forward needs %zu bytes of temporaries, above the fixed %zu-byte "
+                       "scratch of the allocation-free entry point", need, kScratchBytes);
+    return run_forward(L, x, T, out, probs, ids, accumulate, s, Norm{}, p, b);
 }
 
 int moe_hip_set_router_path(int mode) {
@@ -1335,8 +1415,11 @@ int moe_hip_graph_destroy(void *graph) {
 int moe_hip_device_check(void) {
     TRY(ensure_init());
     HIP_TRY(hipStreamSynchronize(g_stream));
-    int *flags[1] = {g_ws.counters.bytes >= sizeof(int) * kMaxCounters
-                         ? g_ws.counters.as<int>() + kLayerErr : nullptr};
+    // The flag of the workspace's counters and of this device's scratch.
+    int *flags[2] = {g_ws.counters.bytes >= sizeof(int) * kMaxCounters
+                         ? g_ws.counters.as<int>() + kLayerErr : nullptr,
+                     g_scratch[g_device] ? reinterpret_cast<int *>(g_scratch[g_device]) + kLayerErr
+                                         : nullptr};
     bool raised = false;
     for (int *f : flags) {
         if (!f) continue;

@@ -56,6 +56,7 @@ SIGNATURES = {
     "moe_hip_layer_get_expert": (C.c_int, [_P, C.c_int, _F, _F, _F]),
     "moe_hip_layer_get_router": (C.c_int, [_P, _F]),
     "moe_hip_forward_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
+    "moe_hip_forward_dev_noalloc": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
     "moe_hip_route_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P, _P, _P, _P]),
     "moe_hip_rms_norm_dev": (C.c_int, [_P, _P, C.c_float, C.c_int, C.c_int, _P, _P]),
     "moe_hip_attn_create": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
@@ -223,6 +224,13 @@ class Layer:
                     stream=None):
         check(lib().moe_hip_forward_dev(self.h, x_ptr, T, out_ptr, probs_ptr, ids_ptr,
                                         accumulate, stream))
+
+    def forward_dev_noalloc(self, x_ptr, T, out_ptr, probs_ptr=None, ids_ptr=None,
+                            accumulate=0, stream=None):
+        """forward_dev on the library's fixed scratch array (no device
+        allocation; moe_hip_forward_dev_noalloc)."""
+        check(lib().moe_hip_forward_dev_noalloc(self.h, x_ptr, T, out_ptr, probs_ptr, ids_ptr,
+                                                accumulate, stream))
 
     def ffn_sublayer_dev(self, x_ptr, rms_w_ptr, eps, T, x_norm_ptr=None, probs_ptr=None,
                          ids_ptr=None, stream=None):

@@ -1,0 +1,142 @@
+"""GPU checks of moe_hip_forward_dev_noalloc, the allocation-free variant of
+moe_hip_forward_dev: called through the C ABI, it must give the same routing
+and the same layer output as the workspace entry point, on two calls in a
+row with the second one smaller (the fixed scratch array keeps the first
+call's contents), when recorded in a HIP graph and replayed, and it must
+refuse a call whose temporaries exceed its fixed array."""
+import numpy as np
+import pytest
+
+import moe_hip as mh
+import orc
+from conftest import CONFIGS
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-5
+ABS_TOL = 1e-4
+
+
+def say(*a):
+    print("[gpu-test]", *a, flush=True)
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def make_layer(T, d, F, E, k, std_router, std_expert, seed):
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(seed, std_router, std_expert)
+    x = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(x.ptr, T * d, seed, 0, 0.0, 1.0)
+    return layer, x
+
+
+def run(layer, fn, x, T, accumulate=0, base=None):
+    """One forward of the first T rows of x through fn (forward_dev or
+    forward_dev_noalloc); returns out, probs, ids on the host."""
+    out = mh.DeviceArray((T, layer.d))
+    if base is not None:
+        out.upload(base[:T])
+    probs = mh.DeviceArray((T, layer.E))
+    ids = mh.DeviceArray((T, layer.k), np.int32)
+    fn(x.ptr, T, out.ptr, probs.ptr, ids.ptr, accumulate)
+    mh.synchronize()
+    return out.to_host(), probs.to_host(), ids.to_host()
+
+
+def assert_same(a, b, what):
+    """The two entry points run the same kernels on the same plan: routing
+    and outputs agree bit for bit."""
+    for name, u, v in zip(("out", "probs", "ids"), a, b):
+        assert np.array_equal(bits(u) if u.dtype == np.float32 else u,
+                              bits(v) if v.dtype == np.float32 else v), f"{what}: {name} differs"
+
+
+# (config, first T, second smaller T): the decode layer (skinny fused
+# GEMVs), the small prefill layer (grouped GEMMs) and the batch-8x512 layer
+# (grouped GEMMs with a split down projection).
+CASES = [("c4", 64, 23), ("c1", 256, 97), ("c2", 4096, 1000)]
+
+
+@pytest.mark.parametrize("cfg,t1,t2", CASES, ids=[c[0] for c in CASES])
+def test_noalloc_matches_forward_dev(cfg, t1, t2):
+    c = CONFIGS[cfg]
+    d, F, E, k = c["d"], c["F"], c["E"], c["k"]
+    say(f"noalloc {cfg}: T={t1} then T={t2}, d={d} F={F} E={E} k={k}")
+    layer, x = make_layer(t1, d, F, E, k, c["std_router"], c["std_expert"], 11)
+    try:
+        for T in (t1, t2):
+            ref = run(layer, layer.forward_dev, x, T)
+            got = run(layer, layer.forward_dev_noalloc, x, T)
+            assert_same(got, ref, f"{cfg} T={T}")
+            # and the oracle's routing (bit-exact) and output (tolerance)
+            xh = x.to_host()[:T]
+            wr = layer.get_router()
+            ex = {e: layer.get_expert(e) for e in range(E)}
+            o_ref, p_ref, i_ref = orc.moe_forward_experts(np.ascontiguousarray(xh), wr, ex, d, F,
+                                                          E, k, None, nthreads=8)
+            assert np.array_equal(bits(got[1]), bits(p_ref)), "router probabilities differ"
+            assert np.array_equal(got[2], i_ref), "expert ids differ"
+            rel = orc.rel_l2(got[0], o_ref)
+            mabs = float(np.abs(got[0].astype(np.float64) - o_ref).max())
+            say(f"{cfg} T={T}: rel-L2 {rel:.2e} max-abs {mabs:.2e}")
+            assert rel <= REL_TOL and mabs <= ABS_TOL, (rel, mabs)
+        # the decode form: out += MoE(x), twice in a row
+        base = np.random.default_rng(5).standard_normal((t1, d)).astype(np.float32)
+        for T in (t1, t2):
+            ref = run(layer, layer.forward_dev, x, T, accumulate=1, base=base)
+            got = run(layer, layer.forward_dev_noalloc, x, T, accumulate=1, base=base)
+            assert_same(got, ref, f"{cfg} accumulate T={T}")
+    finally:
+        layer.close()
+
+
+def test_noalloc_in_graph_replays():
+    """Recorded in a HIP graph (no allocation happens during capture) and
+    replayed several times with eager work and synchronisations between the
+    replays: every replay equals the eager result."""
+    c = CONFIGS["c4"]
+    T, d, F, E, k = c["T"], c["d"], c["F"], c["E"], c["k"]
+    layer, x = make_layer(T, d, F, E, k, c["std_router"], c["std_expert"], 12)
+    other, xo = make_layer(T, d, F, E, k, c["std_router"], c["std_expert"], 13)
+    try:
+        eager = run(layer, layer.forward_dev_noalloc, x, T)
+        out = mh.DeviceArray((T, d))
+        probs = mh.DeviceArray((T, E))
+        ids = mh.DeviceArray((T, k), np.int32)
+        with mh.Graph() as g:
+            layer.forward_dev_noalloc(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
+        try:
+            for rep in range(4):
+                out.zero()
+                g.launch()
+                mh.synchronize()
+                got = (out.to_host(), probs.to_host(), ids.to_host())
+                assert_same(got, eager, f"replay {rep}")
+                # eager work on the same scratch between replays
+                run(other, other.forward_dev_noalloc, xo, T - 7 * rep)
+        finally:
+            g.close()
+    finally:
+        layer.close()
+        other.close()
+
+
+def test_noalloc_refuses_oversized_call():
+    """Temporaries above the fixed array: MOE_HIP_ERR_UNSUPPORTED, before any
+    kernel runs."""
+    d, F, E, k, T = 256, 1024, 8, 2, 16384   # H alone is 128 MiB
+    layer = mh.Layer(d, F, E, k)
+    try:
+        x = mh.DeviceArray((T, d))
+        out = mh.DeviceArray((T, d))
+        rc = mh.lib().moe_hip_forward_dev_noalloc(layer.h, x.ptr, T, out.ptr, None, None, 0,
+                                                  None)
+        assert rc == 2
+        assert b"scratch" in mh.lib().moe_hip_last_error_message()
+        # the bad call left the library usable
+        mh.synchronize()
+    finally:
+        layer.close()
