@@ -319,12 +319,10 @@ int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed,
 /* Expert-product kernels: 0 = automatic (skinny decode GEMVs when the
  * average expert holds at most 16 rows, grouped MFMA GEMMs otherwise),
  * 1 = always grouped GEMMs, 2 = always decode GEMVs (gate/up fused with a
- * split-K down projection while its partials fit 32 MB, and with the routing
- * in the same launch when d_model % 128 == 0 and n_experts <= 64),
- * 3 = always decode GEMVs as separate gate/up and down launches, 4 = always
- * decode GEMVs fused as in 2 but routed by a launch of its own.  Modes 2-4
- * need ffn_hidden % 64 == 0 and T * top_k <= 4096.  Process-wide; every
- * path computes the same layer. */
+ * split-K down projection while its partials fit 32 MB, else as 3),
+ * 3 = always decode GEMVs as separate gate/up and down launches.  Modes 2
+ * and 3 need ffn_hidden % 64 == 0 and T * top_k <= 4096.  Process-wide;
+ * every path computes the same layer. */
 int moe_hip_set_expert_path(int mode);
 
 /* Routing kernel selection: 0 = automatic, 1 = token x expert tiles,
@@ -340,8 +338,8 @@ int moe_hip_get_attn_path(void);
 
 
 /* Waits for the library stream and reports whether a bounded device-side
- * wait of the one-launch decode layer or decode attention gave up since the
- * last check (the results of that call are then invalid); clears the flag. */
+ * wait of the one-launch decode attention gave up since the last check (the
+ * results of that call are then invalid); clears the flag. */
 int moe_hip_device_check(void);
 
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,

@@ -35,6 +35,7 @@
 // tolerance, not bit for bit.
 #include <type_traits>
 
+#include "handoff.h"
 #include "moe_internal.h"
 #include "moe_math.h"
 
@@ -44,7 +45,6 @@ namespace {
 constexpr int kChunkPos = 128;   // positions per attention workgroup
 constexpr int kTile = 32;        // rows and columns of a projection tile
 constexpr int kSliceK = 128;     // reduction length per projection workgroup
-constexpr int kSpinLimit = 1 << 20;
 
 // RoPE on the pair (v0, v1) = columns 2i, 2i + 1 of a head (:196-199).
 __device__ inline void rope_pair(float &v0, float &v1, float c, float s) {
@@ -61,50 +61,6 @@ __device__ inline float comp(const float4 &v, int j) {
     return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
 }
 
-// Data handed between workgroups of one launch is written with
-// device-scope relaxed atomic stores, which are coherent across the XCDs'
-// separate L2s, and read with loads of the same (sc1) cache policy.  The
-// writer waits for its stores, passes a barrier and then bumps a counter;
-// the reader loads only after seeing the count.  (A device-scope fence per
-// workgroup instead writes back and invalidates the XCD's L2 each time,
-// which serialises the workgroups.)
-__device__ inline void cstore(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline void cstore4(float *p, float4 v) {
-    cstore(p, v.x); cstore(p + 1, v.y); cstore(p + 2, v.z); cstore(p + 3, v.w);
-}
-// Reader side: buffer loads with the sc1 cache policy from a workgroup-
-// uniform base at per-lane offsets (under 2 GiB).  Unlike atomic loads they
-// carry no ordering among themselves, so a batch is in flight together.
-constexpr int kCachePolicySc1 = 16;
-struct CRead {
-    __amdgpu_buffer_rsrc_t r;
-    __device__ explicit CRead(const float *base)
-        : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, 0x7FFFFFFF,
-                                              0x00020000)) {}
-    __device__ float operator()(size_t idx) const {
-        return __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)(idx * 4), 0, kCachePolicySc1));
-    }
-    __device__ float4 f4(size_t idx) const {   // idx a multiple of 4
-        return __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(idx * 4), 0, kCachePolicySc1));
-    }
-};
-// Plain loads, for data written by an earlier launch.
-struct PRead {
-    const float *p;
-    __device__ explicit PRead(const float *base) : p(base) {}
-    __device__ float operator()(size_t idx) const { return p[idx]; }
-    __device__ float4 f4(size_t idx) const { return *reinterpret_cast<const float4 *>(p + idx); }
-};
-
-// Every thread's stores are performed, then the workgroup passes a barrier.
-__device__ inline void publish() {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-    __syncthreads();
-}
 // Readiness of a count in the one-launch sublayer: kFlagCopies flags, one
 // per 128-byte line, all set by the workgroup that completes the count;
 // waiters each poll one copy, so polling is spread over many addresses.

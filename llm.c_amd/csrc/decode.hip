@@ -23,15 +23,35 @@
 namespace moe {
 namespace {
 
+// Item (expert e, feature block fb) of workgroup b.  With E a multiple of 8
+// an expert's items are the workgroups b = x + 8 j of one x, i.e. (as the
+// hardware hands workgroups to the 8 XCDs in turn) all on one XCD, which
+// shares the expert's staged activation rows in that XCD's L2 (measured 1.1-
+// 1.6 us faster per 64-token, E = 16 layer than experts spread over XCDs).
+__device__ inline void item_of(int b, int E, int nfb, int &e, int &fb) {
+    if (E % 8 == 0) {
+        const int x = b % 8, j = b / 8;
+        e = x + 8 * (j / nfb);
+        fb = j % nfb;
+    } else {
+        e = b / nfb;
+        fb = b % nfb;
+    }
+}
+
 // grid = E x (F/(16*NW)): one gate/up item of NW waves per workgroup (NW =
-// 8: one workgroup per CU, two waves per SIMD).
+// 8: one workgroup per CU, two waves per SIMD).  The fused items store their
+// split-K partials write-through (coherent stores): none are left dirty in an
+// XCD's L2 when the launch ends, and the combine launch reads them from
+// memory either way.
 template <bool FUSED, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void decode_gateup_kernel(DecodeArgs a) {
     extern __shared__ __align__(16) float xs[];     // [kRows][kLd], slot list, token list
     __shared__ int wcnt[NW];
     const int nfb = a.F / (16 * NW);
-    gateup_item<FUSED, false, NW>(a, blockIdx.x / nfb, blockIdx.x % nfb, xs, wcnt, nullptr, 0,
-                                  nullptr);
+    int e, fb;
+    item_of(blockIdx.x, a.E, nfb, e, fb);
+    gateup_item<FUSED, NW, FUSED>(a, e, fb, xs, wcnt);
 }
 
 __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
@@ -55,7 +75,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
 
     const int id0 = (int)threadIdx.x < a.nslots ? a.ids[threadIdx.x] : -1;
     WGroup<1> wa, wb;
-    const int cnt = expert_slots<false>(a.ids, a.nslots, e, id0, a.topk, list, nullptr, wcnt);
+    const int cnt = expert_slots(a.ids, a.nslots, e, id0, a.topk, list, nullptr, wcnt);
     if (cnt == 0) return;
     for (int r0 = 0; r0 < cnt; r0 += kRows) {
         const int rows = min(kRows, cnt - r0);

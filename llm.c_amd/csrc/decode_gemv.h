@@ -1,5 +1,5 @@
 // decode_gemv.h — building blocks of the bandwidth-bound decode expert
-// products (decode.hip) and of the fused decode-layer kernel (layer.hip).
+// products (decode.hip).
 //
 // Weights stream from HBM straight into v_mfma_f32_16x16x4f32 operands: a
 // lane holds a 16-byte piece of one weight row (K contiguous), the MFMA's
@@ -10,6 +10,7 @@
 #pragma once
 #include <type_traits>
 
+#include "handoff.h"
 #include "moe_internal.h"
 #include "moe_math.h"
 
@@ -55,45 +56,16 @@ __device__ inline void slot_chunk(int i, int n, int e, int id, int topk, int *li
     __syncthreads();
 }
 
-// An expert id: COHERENT reads one written earlier in the same launch by
-// another workgroup (device-scope atomic load).
-template <bool COHERENT>
-__device__ inline int load_id(const int *p) {
-    if (COHERENT) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return *p;
-}
-
-template <bool COHERENT, int NW = 4>
+template <int NW = 4>
 __device__ int expert_slots(const int *ids, int n, int e, int id0, int topk, int *list, int *tok,
                             int *wcnt) {
     int total = 0;
     slot_chunk<NW>(threadIdx.x, n, e, id0, topk, list, tok, wcnt, total);
     for (int base = 64 * NW; base < n; base += 64 * NW) {
         const int i = base + threadIdx.x;
-        slot_chunk<NW>(i, n, e, load_id<COHERENT>(ids + min(i, n - 1)), topk, list, tok, wcnt,
-                       total);
+        slot_chunk<NW>(i, n, e, ids[min(i, n - 1)], topk, list, tok, wcnt, total);
     }
     return total;
-}
-
-// Spins (thread 0, bounded) until *ctr >= target, read with device-scope
-// atomic loads; past the bound it raises *err and goes on, so every wave
-// always ends.  The workgroup then passes a barrier (no fence: pending
-// weight loads need not complete).
-constexpr int kSpinLimit = 1 << 20;
-
-__device__ inline void wait_count(const int *ctr, int target, int *err) {
-    if (threadIdx.x == 0) {
-        int spins = 0;
-        while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (++spins > kSpinLimit) {
-                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(16);   // ~1000 cycles: hundreds of pollers stay light
-        }
-    }
-    __builtin_amdgcn_s_barrier();
 }
 
 // Staging of rows rowlist[pos0 .. pos0 + rows) of src, columns [k0, k0 + kc),
@@ -317,8 +289,9 @@ template <int NW> constexpr int hld() { return 16 * NW + 4; }
 // MFMAs of one down group: column blocks CB*g .. CB*g + CB - 1 of the wave
 // (CB = 8 / NW; those below nbw), K = the block's 16 * NW features (A
 // operands from the H block in LDS at as), each block written at yoff + its
-// column once complete (yoff < 0: a row past the pass).
-template <int RB, int NW>
+// column once complete (yoff < 0: a row past the pass); CS: with coherent
+// (write-through) stores.
+template <int RB, int NW, bool CS = false>
 __device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int nbw, int cb0,
                               const int (&yoff)[2][4], float *yp, int j) {
     constexpr int CB = 8 / NW;
@@ -345,7 +318,10 @@ __device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int
             for (int b = 0; b < RB; ++b)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (yoff[b][r] >= 0) yp[yoff[b][r] + col] = acc[b][r];
+                    if (yoff[b][r] >= 0) {
+                        if (CS) cstore(yp + yoff[b][r] + col, acc[b][r]);
+                        else    yp[yoff[b][r] + col] = acc[b][r];
+                    }
         }
     }
 }
@@ -355,12 +331,10 @@ __device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int
 // true: keeps the item's H columns in LDS and multiplies them by the matching
 // rows of W_down, writing the split-K partial Yp[fb][a][0 .. d) (the combine
 // adds the F/(16*NW) partials in order).  xs: the dynamic LDS (rows, slot
-// list, token list); wcnt: NW ints of LDS.  MEGA: expert ids come from the
-// same launch (device-scope loads) and, when routed is set, the item first
-// waits for the router.
-template <bool FUSED, bool MEGA, int NW = 4>
-__device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *wcnt,
-                            const int *routed, int routed_target, int *err) {
+// list, token list); wcnt: NW ints of LDS.  CS: partials go out with
+// coherent (write-through) stores.
+template <bool FUSED, int NW = 4, bool CS = false>
+__device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *wcnt) {
     static_assert(NW == 4 || NW == 8, "an item is 4 or 8 waves of 16 features");
     int *list = reinterpret_cast<int *>(xs + kRows * kLd);
     int *tok = list + a.nslots;
@@ -381,11 +355,9 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
     const int og = kUnitBytes * nbg * (a.d / 16);
     const int ou = og + kUnitBytes * 2 * (a.d / 16);
 
-    // Standalone: the slot list first (its loads are not queued behind
-    // weight loads), then per chunk the activation rows (DMA), the first two
-    // weight groups and a wait for the rows only.  MEGA: the first chunk's
-    // weights go out before waiting for the router (routed reaching
-    // routed_target), as they depend on nothing it computes.
+    // The slot list first (its loads are not queued behind weight loads),
+    // then per chunk the activation rows (DMA), the first two weight groups
+    // and a wait for the rows only.
     // Down weights (FUSED): wave w's 16-column blocks w*nbw .. of the
     // expert's W_down, this item's NW feature units.
     const int fq = a.F / 16;
@@ -403,12 +375,8 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
     };
     const DownHead<NW> dh{ds, od, fq, last, ngd >= 2 ? (3 * spread) % ngd : 0, ngd};
     WGroup<2> wa, wb;
-    if (MEGA && routed) {
-        gemv_prime<2>(gs, og, ou, min(kChunk, a.d) / 16, wa, wb, rot_of(min(kChunk, a.d) / 16));
-        wait_count(routed, routed_target, err);
-    }
-    const int id0 = (int)threadIdx.x < a.nslots ? load_id<MEGA>(a.ids + threadIdx.x) : -1;
-    const int cnt = expert_slots<MEGA, NW>(a.ids, a.nslots, e, id0, a.topk, list, tok, wcnt);
+    const int id0 = (int)threadIdx.x < a.nslots ? a.ids[threadIdx.x] : -1;
+    const int cnt = expert_slots<NW>(a.ids, a.nslots, e, id0, a.topk, list, tok, wcnt);
     if (cnt == 0) return;
     for (int r0 = 0; r0 < cnt; r0 += kRows) {
         const int rows = min(kRows, cnt - r0);
@@ -425,12 +393,8 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             // weight loads, and other waves read those rows after the barrier:
             // keep the compiler from moving weight loads above the DMA.
             __builtin_amdgcn_sched_barrier(0);
-            if (MEGA && routed && r0 == 0 && k0 == 0) {
-                WAIT_VMCNT(0);   // primed before the rows
-            } else {
-                gemv_prime<2>(gs, og + 64 * k0, ou + 64 * k0, kc / 16, wa, wb, rot_of(kc / 16));
-                WAIT_VMCNT(4 * Unroll<2>::kU);   // the rows, not the weights behind them
-            }
+            gemv_prime<2>(gs, og + 64 * k0, ou + 64 * k0, kc / 16, wa, wb, rot_of(kc / 16));
+            WAIT_VMCNT(4 * Unroll<2>::kU);   // the rows, not the weights behind them
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
             dma_landed(xs);
             const float *as = xs + j * kLd + 4 * h;
@@ -494,26 +458,26 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             constexpr int RB = decltype(rb)::value;
             int g = 0;
             for (; g + 4 <= ngd; g += 2) {
-                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
                 dload<NW>(ds, od, fq, dh.rot(g + 2), last, da);
                 __builtin_amdgcn_sched_barrier(0);
-                dgroup<RB, NW>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
                 __builtin_amdgcn_sched_barrier(0);
                 dload<NW>(ds, od, fq, dh.rot(g + 3), last, db);
                 __builtin_amdgcn_sched_barrier(0);
             }
             const int left = ngd - g;
             if (left == 3) {
-                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
                 dload<NW>(ds, od, fq, dh.rot(g + 2), last, da);
-                dgroup<RB, NW>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
-                dgroup<RB, NW>(da, as, dh.rot(g + 2), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(da, as, dh.rot(g + 2), nbw, cb0, yoff, a.out, j);
             } else if (left == 2) {
-                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
-                dgroup<RB, NW>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
             } else if (left == 1) {
-                dgroup<RB, NW>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
+                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
             }
         };
         if (rows > 16) run(std::integral_constant<int, 2>{});

@@ -43,7 +43,7 @@ bool g_timing = false;
 hipEvent_t g_ev[6] = {};
 hipEvent_t g_tev[2] = {};
 bool g_have_times = false;
-int g_path = 0;   // 0 auto, 1 grouped GEMM, 2 decode GEMVs, 3 unfused, 4 fused, routed apart
+int g_path = 0;   // 0 auto, 1 grouped GEMMs, 2 decode GEMVs (fused), 3 decode GEMVs (two launches)
 int g_rpath = 0;  // 0 auto, 1 token x expert tiles, 2 one token per lane
 // A captured graph keeps the workspace addresses it recorded, so the
 // workspace must not be freed and reallocated while one may still run:
@@ -142,14 +142,12 @@ struct Workspace {
 };
 Workspace g_ws;
 
-// Completion counter of the fused route+dispatch launch ("last workgroup
-// does the tail work"); it is zero between launches because the last
-// workgroup resets it, so it is cleared only when allocated.
-constexpr int kMaxCounters = 64;
-// Further device ints in the same buffer: the decode-layer launch's four
-// counters and its wait-gave-up flag.
-constexpr int kLayerSync = 8;
+// Device ints that are zero between launches (each launch's last workgroup
+// resets what it counted), so they are cleared only when allocated: [0] the
+// fused route+dispatch launch's completion counter, [kLayerErr] the flag a
+// bounded device-side wait raises when it gives up.
 constexpr int kLayerErr = 12;
+constexpr int kMaxCounters = 64;
 int ensure_counters() {
     if (g_ws.counters.bytes >= sizeof(int) * kMaxCounters) return MOE_HIP_OK;
     TRY(g_ws.counters.reserve(sizeof(int) * kMaxCounters));
@@ -852,7 +850,7 @@ namespace {
 struct FwdPlan {
     size_t n = 0;           // T * k assignments
     int max_mtiles = 0;     // grouped GEMM m-tile bound
-    bool use_decode = false, fused = false, one_launch = false;
+    bool use_decode = false, fused = false;
     int ksplit = 1;         // partial products per slot the combine adds
     size_t h_floats = 0;    // H [n x F] (grouped GEMMs, unfused decode)
     size_t ys_floats = 0;   // per-slot products / split-K partials
@@ -886,14 +884,9 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
                        "decode kernels need ffn_hidden %% 64 == 0, T*k <= %d and "
                        "8*ffn_hidden*d_model < 2^31", moe::kDecodeMaxSlots);
     p->use_decode = g_path >= 2 || (g_path == 0 && decode_ok && n <= (size_t)16 * E);
-    // Mode 2 runs routing and the fused expert items (4 waves) as one launch
-    // where it fits; everything else routes first (the one-launch layer is
-    // not yet faster: its router competes with the expert weight stream).
-    const bool one_launch_ok = g_path == 2 && g_rpath != 1 && moe::decode_layer_supported(d, E);
-    const int fused_splits = F / (16 * (one_launch_ok ? 4 : moe::decode_fused_waves(d, F)));
+    const int fused_splits = F / (16 * moe::decode_fused_waves(d, F));
     const size_t fused_floats = (size_t)fused_splits * n * d;
     p->fused = p->use_decode && g_path != 3 && sizeof(float) * fused_floats <= moe::kFusedPartialBytes;
-    p->one_launch = p->fused && one_launch_ok;
     if (p->fused) {
         p->ksplit = fused_splits;
         p->ys_floats = fused_floats;
@@ -973,35 +966,15 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
     const int d = L->d, F = L->F, E = L->E, k = L->k;
     const size_t n = p.n;
     int *ids_d = ids ? ids : b.ids;
-    if (nm.x_raw && p.one_launch) {   // (its router blocks do not normalise)
-        HIP_TRY(moe::launch_rms_norm(nm.x_raw, nm.rms_w, nm.eps, T, d, const_cast<float *>(x), s));
-        nm = Norm{};
-    }
-    if (!p.one_launch)
-        TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
-                       b.tile_expert, b.counters, s, !p.use_decode, nm));
+    TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
+                   b.tile_expert, b.counters, s, !p.use_decode, nm));
     if (p.use_decode) {
         // Fused gate/up + split-K down while its partials stay small, else
         // gate/up then down.
         moe::DecodeArgs gu{};
         gu.x = x; gu.ids = ids_d; gu.topk = k; gu.w = L->wgu;
         gu.d = d; gu.F = F; gu.E = E; gu.ksplit = 1; gu.nslots = (int)n;
-        if (p.one_launch) {
-            gu.out = b.ys;
-            gu.w2 = L->wdT;
-            moe::LayerArgs la{};
-            la.r = moe::RouteArgs{x, L->wr, L->bias, T, d, E, k, probs, ids_d, b.gw};
-            la.r.wrT = L->wrT;
-            la.r.wr_nonfinite = L->wr_nonfinite;
-            la.r.no_dispatch = 1;
-            la.g = gu;
-            la.sync = b.counters + kLayerSync;
-            la.err = b.counters + kLayerErr;
-            if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
-            HIP_TRY(moe::launch_decode_layer(la, s));
-            if (g_timing)
-                for (int i = 1; i <= 4; ++i) HIP_TRY(hipEventRecord(g_ev[i], s));
-        } else if (p.fused) {
+        if (p.fused) {
             gu.out = b.ys;
             gu.w2 = L->wdT;
             HIP_TRY(moe::launch_decode_gateup(gu, s));
@@ -1083,7 +1056,7 @@ int moe_hip_set_router_path(int mode) {
 }
 
 int moe_hip_set_expert_path(int mode) {
-    if (mode < 0 || mode > 4) return set_err(MOE_HIP_ERR_ARG, "expert path mode %d", mode);
+    if (mode < 0 || mode > 3) return set_err(MOE_HIP_ERR_ARG, "expert path mode %d", mode);
     g_path = mode;
     return MOE_HIP_OK;
 }

@@ -109,17 +109,6 @@ constexpr int kDecodeMaxSlots = 4096;
 // decode kernel may write; larger layers use the separate down kernel.
 constexpr size_t kFusedPartialBytes = (size_t)32 << 20;
 
-// One launch per decode layer: routing plus fused gate/up + split-K down
-// items (layer.hip).  sync: 4 ints, zero between launches; err: raised if a
-// bounded device-side wait gave up.
-struct LayerArgs {
-    RouteArgs r;         // wrT set; ids written device-coherently; no dispatch
-    DecodeArgs g;        // w2 set: fused items writing Yp [F/64][n][d]
-    int *sync;
-    int *err;
-};
-bool decode_layer_supported(int d, int E);
-hipError_t launch_decode_layer(const LayerArgs &a, hipStream_t s);
 
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);

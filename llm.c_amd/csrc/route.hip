@@ -402,7 +402,7 @@ __global__ __launch_bounds__(64 * NWV) void router_rows_kernel(RouteArgs a, Disp
     __shared__ __align__(16) float smem[RowsSmem<KC>::kFloats];
     __shared__ int is_last;
     const int tid = threadIdx.x;
-    route_rows_block<NWV, RE, KC, SKIP, false>(a, blockIdx.x, smem);
+    route_rows_block<NWV, RE, KC, SKIP>(a, blockIdx.x, smem);
     if (FUSE) {
         // The last workgroup to finish runs the dispatch over every token's
         // ids (release/acquire through the device-scope fences), then resets

@@ -1,7 +1,6 @@
-// route_rows.h — the row-block router as a device function, shared by the
-// routing kernel (route.hip) and the fused decode-layer kernel (layer.hip).
-// Both translation units are built with fp32 denormal flushing, matching
-// the FTZ/DAZ mode of the reference's -ffast-math executables.
+// route_rows.h — the row-block router as a device function of the routing
+// kernel (route.hip), built with fp32 denormal flushing, matching the
+// FTZ/DAZ mode of the reference's -ffast-math executables.
 #pragma once
 #include "moe_internal.h"
 #include "moe_math.h"
@@ -193,12 +192,9 @@ struct RowsSmem {
 
 // Routes token block tb (tokens 16*tb ..) with NWV waves; every thread of
 // the workgroup calls this.  smem: RowsSmem<KC>::kFloats floats of LDS,
-// 16-byte aligned.  COHERENT: expert ids are stored with device-scope
-// atomic stores, for other workgroups of the same launch to read, and
-// *loaded (if set) is incremented once the first chunk of x and router
-// rows is in LDS.
-template <int NWV, int RE, int KC, bool SKIP, bool COHERENT>
-__device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *loaded = nullptr) {
+// 16-byte aligned.
+template <int NWV, int RE, int KC, bool SKIP>
+__device__ void route_rows_block(const RouteArgs &a, int tb, float *smem) {
     static_assert(NWV >= 2, "two waves finish the block's 16 tokens");
     constexpr int NT = 64 * NWV;
     constexpr int LD = KC + 4;                     // padded LDS row of x (floats)
@@ -281,8 +277,6 @@ __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *l
     if (!pre) gload(0);
     sstore(0, !pre);
     __syncthreads();
-    if (COHERENT && loaded && tid == 0)
-        __hip_atomic_fetch_add(loaded, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int ch = 0; ch < nchunk; ++ch) {
         const int buf = ch & 1;
         if (ch + 1 < nchunk) gload((ch + 1) * KC);
@@ -331,11 +325,7 @@ __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem, int *l
         for (int i = tid; i < tn * k; i += NT) {
             const int ct = i / k, ki = i - ct * k;
             const size_t o = (size_t)(t0 + ct) * k + ki;
-            if (a.ids) {
-                if (COHERENT) __hip_atomic_store(&a.ids[o], id_sel[ct][ki], __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-                else          a.ids[o] = id_sel[ct][ki];
-            }
+            if (a.ids) a.ids[o] = id_sel[ct][ki];
             if (a.gw) a.gw[o] = ftz_f(p_sel[ct][ki] * inv_sel[ct]);
         }
     if (a.probs)

@@ -414,9 +414,8 @@ class Graph:
 
 
 def set_expert_path(mode):
-    """0 automatic, 1 grouped GEMMs, 2 decode GEMVs (fused gate/up + down,
-    routed in the same launch where supported), 3 decode GEMVs as two
-    launches, 4 fused decode GEMVs routed by a launch of their own."""
+    """0 automatic, 1 grouped GEMMs, 2 decode GEMVs (gate/up fused with a
+    split-K down projection), 3 decode GEMVs as two launches."""
     check(lib().moe_hip_set_expert_path(int(mode)))
 
 
