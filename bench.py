@@ -4,22 +4,34 @@ Headline workload: the large imbalanced prefill layer — T=16384 tokens,
 d_model=2048, d_ff=8192, E=64 experts, top-4, Zipf-skewed router bias,
 inputs N(0,1), weights N(0,0.02), all fp32, synthetic and resident in HBM
 before the timed region.  A "step" is one full layer forward (route,
-dispatch, gate/up GEMM, down GEMM, combine).
+dispatch, gate/up GEMM, down GEMM, combine).  K steps are issued back to back
+on the library stream with device marks between them and nothing waiting
+inside the loop (the loop is synchronised on both sides); the per-step
+figure is the median of the K marked intervals.  The phase breakdown comes
+from a separate pass with per-phase events.
 
-Also measured in the same run:
+Also measured in the same run (each a median of K marked steps unless said):
+  * prefill_host_io: the headline layer with x read from and out, probs,
+    ids written to pageable host memory, as the moe_forward drop-in does
+    (PCIe included; wall time per synchronous call);
   * decode: 64 sequences x 1 token through 8 MoE layers of d=512, d_ff=2048,
     E=16, top-2 (8 layers' weights, 1.6 GB, so the 256 MB last-level cache
     cannot hold them), reported as MoE decode tokens/s and HBM GB/s;
+  * decode_host_dropin: the same 8 layers through moe_decode_batch with
+    host x_norm and x (the inference_step slot, batched; wall time);
   * prefill_batch8x512: the T=4096 (batch 8 x seq 512) layer, d=256,
-    d_ff=1024, E=8, top-2, timed the same way;
-  * backward_batch8x512: the same layer's backward pass (every gradient and
-    the load-balancing loss);
+    d_ff=1024, E=8, top-2, plus its host-pointer moe_forward drop-in and its
+    backward pass (every gradient and the load-balancing loss);
+  * moe_layer_c3 / moe_stack_c3: one MoE layer of the 8-block decoder
+    (T=4096, d=512, d_ff=2048, E=8, top-2), and its 8 MoE FFN sublayers
+    x += MoE(rms_norm(x)) in place through moe_hip_ffn_sublayer_dev;
   * decode_step: the whole block stack of that decode step (GQA attention
     over a 1024-position KV cache, then the MoE FFN sublayer, per block) with
     the residual stream on the device;
   * cpu_baseline: the CPU oracle (a restatement of the reference's
     moe_forward, bit-identical routing) on a bounded token sample of the same
-    prefill workload, on this host's cores.
+    prefill workload, on this host's cores: one warm-up pass, then the median
+    of 5 passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
 """
@@ -37,10 +49,22 @@ sys.path.insert(0, os.path.join(ROOT, "llm.c_amd"))
 METRIC = "MoE layer tokens/s + % fp32 MFMA peak (prefill); decode tok/s + HBM GB/s"
 PEAK_FP32_MFMA_TFLOPS = 157.3      # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0              # MI355X HBM3E
+# How oracle/Makefile builds the CPU oracle timed as the baseline.
+ORACLE_BUILD = "gcc -O3 -mavx2 -mfma -ffp-contract=off -fopenmp (oracle/Makefile)"
 
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def stats(ms):
+    a = np.asarray(ms, np.float64)
+    return dict(median=float(np.median(a)), mean=float(a.mean()), min=float(a.min()),
+                max=float(a.max()), n=int(a.size))
+
+
+def layer_flops(T, d, F, E, k):
+    return 6.0 * T * k * d * F + 2.0 * T * d * E
 
 
 def prefill(mh, steps, warmup, T=16384, d=2048, F=8192, E=64, k=4, seed=5):
@@ -60,54 +84,107 @@ def prefill(mh, steps, warmup, T=16384, d=2048, F=8192, E=64, k=4, seed=5):
     mh.synchronize()
     log(f"prefill setup {time.time() - t0:.1f}s (weights {3 * E * d * F * 4 / 1e9:.2f} GB)")
 
-    mh.set_timing(True)
-    for _ in range(warmup):
-        layer.forward_dev(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
-        mh.last_timings()
-    mh.synchronize()
-    phase = np.zeros(5)
+    step = lambda: layer.forward_dev(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
     t0 = time.perf_counter()
-    for _ in range(steps):
-        layer.forward_dev(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
-        phase += np.array(mh.last_timings())
-    mh.synchronize()
+    per = mh.timed_steps(step, steps, warmup)
     wall = time.perf_counter() - t0
+    st = stats(per)
+    # Phase breakdown (separate pass; per-phase events and a wait per step).
+    mh.set_timing(True)
+    phase = np.zeros(5)
+    nph = 5
+    for _ in range(nph):
+        step()
+        phase += np.array(mh.last_timings())
     mh.set_timing(False)
-    phase /= steps
-    ms = wall * 1e3 / steps
+    phase /= nph
     counts = np.bincount(ids.to_host().ravel(), minlength=E)
     flops_gu = 4.0 * T * k * d * F
     flops_dn = 2.0 * T * k * d * F
-    flops_layer = 6.0 * T * k * d * F + 2.0 * T * d * E
-    res = dict(T=T, d=d, F=F, E=E, k=k, ms=ms, phase_ms=phase.tolist(),
+    ms = st["median"]
+    res = dict(T=T, d=d, F=F, E=E, k=k, ms=ms, step_ms=st, wall_s=wall, phase_ms=phase.tolist(),
                counts_max_over_mean=float(counts.max() / counts.mean()),
                gateup_tflops=flops_gu / (phase[2] * 1e-3) / 1e12,
                down_tflops=flops_dn / (phase[3] * 1e-3) / 1e12,
-               layer_tflops=flops_layer / (ms * 1e-3) / 1e12,
+               layer_tflops=layer_flops(T, d, F, E, k) / (ms * 1e-3) / 1e12,
                bias=bias is not None)
-    state = dict(layer=layer, x=x, bias=bias, ids=ids.to_host(), seed=seed)
+    state = dict(layer=layer, x=x, out=out, probs=probs, ids_dev=ids, bias=bias,
+                 ids=ids.to_host(), seed=seed)
     return res, state
 
 
-def prefill_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2):
-    """The batch-8 x seq-512 prefill layer (d=256, d_ff=1024, E=8, top-2;
-    router weights N(0, 0.1), experts N(0, 0.02)), timed like the headline."""
-    layer = mh.Layer(d, F, E, k)
-    layer.fill_synthetic(2, 0.1, 0.02)
-    x = mh.DeviceArray((T, d))
-    mh.fill_normal_dev(x.ptr, T * d, 2, 0, 0.0, 1.0)
-    out = mh.DeviceArray((T, d))
-    for _ in range(max(warmup, 1)):
-        layer.forward_dev(x.ptr, T, out.ptr)
-    mh.synchronize()
-    mh.timer_start()
+def prefill_host_io(mh, st, steps=5):
+    """The headline layer with its activations in pageable host memory: x
+    copied in, the layer, out / probs / ids copied back, synchronous (the
+    moe_forward drop-in's data movement, on the same router-biased layer)."""
+    layer, x, out, probs, ids = st["layer"], st["x"], st["out"], st["probs"], st["ids_dev"]
+    T, d = x.shape
+    xh = x.to_host()
+    oh = np.empty_like(xh)
+    ph = np.empty(probs.shape, np.float32)
+    ih = np.empty(ids.shape, np.int32)
+
+    def call():
+        x.upload(xh)
+        layer.forward_dev(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
+        mh.check(mh.lib().moe_hip_memcpy(oh.ctypes.data_as(mh._P), out.ptr, oh.nbytes, 2))
+        mh.check(mh.lib().moe_hip_memcpy(ph.ctypes.data_as(mh._P), probs.ptr, ph.nbytes, 2))
+        mh.check(mh.lib().moe_hip_memcpy(ih.ctypes.data_as(mh._P), ids.ptr, ih.nbytes, 2))
+
+    call()
+    per = []
     for _ in range(steps):
-        layer.forward_dev(x.ptr, T, out.ptr)
-    ms = mh.timer_stop() / steps
+        t0 = time.perf_counter()
+        call()
+        per.append((time.perf_counter() - t0) * 1e3)
+    s = stats(per)
+    pcie = float(xh.nbytes + oh.nbytes + ph.nbytes + ih.nbytes)
+    return dict(T=T, ms=s["median"], step_ms=s, tokens_per_s=T / (s["median"] * 1e-3),
+                pcie_bytes=pcie)
+
+
+def layer_bench(mh, steps, warmup, T, d, F, E, k, std_router, seed):
+    """One layer forward on device rows (median of marked steps)."""
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(seed, std_router, 0.02)
+    x = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(x.ptr, T * d, seed, 0, 0.0, 1.0)
+    out = mh.DeviceArray((T, d))
+    mh.synchronize()
+    s = stats(mh.timed_steps(lambda: layer.forward_dev(x.ptr, T, out.ptr), steps, warmup))
     layer.close()
-    flops = 6.0 * T * k * d * F + 2.0 * T * d * E
-    return dict(T=T, d=d, F=F, E=E, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3),
-                mfma_frac=flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
+    ms = s["median"]
+    return dict(T=T, d=d, F=F, E=E, k=k, ms=ms, step_ms=s, tokens_per_s=T / (ms * 1e-3),
+                mfma_frac=layer_flops(T, d, F, E, k) / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS)
+
+
+def ffn_stack(mh, steps, warmup, n_layers=8, T=4096, d=512, F=2048, E=8, k=2, eps=1e-5):
+    """The MoE FFN half of every block of the 8-block decoder at batch 8 x
+    seq 512: x += MoE(rms_norm(x; rms_ffn)) in place, block after block
+    (src/transformer.c:760-767), through moe_hip_ffn_sublayer_dev.  Weights
+    N(0, 0.02), rms_ffn = 1 (src/transformer.c:429-433), x ~ N(0, 1)."""
+    layers = []
+    for li in range(n_layers):
+        L = mh.Layer(d, F, E, k)
+        L.fill_synthetic(200 + li, 0.02, 0.02)
+        layers.append(L)
+    rms = mh.DeviceArray.from_host(np.ones(d, np.float32))
+    x = mh.DeviceArray((T, d))
+    mh.fill_normal_dev(x.ptr, T * d, 201, 0, 0.0, 1.0)
+    mh.synchronize()
+
+    def step():
+        for L in layers:
+            L.ffn_sublayer_dev(x.ptr, rms.ptr, eps, T)
+
+    s = stats(mh.timed_steps(step, steps, warmup))
+    for L in layers:
+        L.close()
+    ms = s["median"]
+    return dict(layers=n_layers, T=T, d=d, F=F, E=E, k=k, ms_per_step=ms, step_ms=s,
+                tokens_per_s=T / (ms * 1e-3), ms_per_layer=ms / n_layers,
+                mfma_frac=n_layers * layer_flops(T, d, F, E, k) / (ms * 1e-3) / 1e12
+                / PEAK_FP32_MFMA_TFLOPS)
 
 
 def dropin_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2):
@@ -122,12 +199,15 @@ def dropin_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2):
     x = f(T, d, sd=1.0)
     for _ in range(max(warmup, 1)):
         mh.moe_forward(x, hw)
-    t0 = time.perf_counter()
+    per = []
     for _ in range(steps):
+        t0 = time.perf_counter()
         mh.moe_forward(x, hw)
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+        per.append((time.perf_counter() - t0) * 1e3)
+    s = stats(per)
     pcie_bytes = 4.0 * T * (2 * d + E + k)
-    return dict(T=T, ms=ms, tokens_per_s=T / (ms * 1e-3), pcie_bytes=pcie_bytes)
+    return dict(T=T, ms=s["median"], step_ms=s, tokens_per_s=T / (s["median"] * 1e-3),
+                pcie_bytes=pcie_bytes)
 
 
 def backward_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2, aux_coef=0.01):
@@ -143,17 +223,12 @@ def backward_small(mh, steps, warmup, T=4096, d=256, F=1024, E=8, k=2, aux_coef=
     bufs = [mh.DeviceArray(sh) for sh in ((T, d), (d, E), (E, d, F), (E, d, F), (E, F, d))]
     aux = mh.DeviceArray((1,))
     run = lambda: layer.backward_dev(x.ptr, T, dout.ptr, aux_coef, *[b.ptr for b in bufs], aux.ptr)
-    for _ in range(max(warmup, 1)):
-        run()
-    mh.synchronize()
-    mh.timer_start()
-    for _ in range(steps):
-        run()
-    ms = mh.timer_stop() / steps
+    s = stats(mh.timed_steps(run, steps, max(warmup, 1)))
     layer.close()
+    ms = s["median"]
     tflops = 18.0 * T * k * d * F / (ms * 1e-3) / 1e12
-    return dict(T=T, d=d, F=F, E=E, k=k, ms=ms, tokens_per_s=T / (ms * 1e-3), tflops=tflops,
-                mfma_frac=tflops / PEAK_FP32_MFMA_TFLOPS)
+    return dict(T=T, d=d, F=F, E=E, k=k, ms=ms, step_ms=s, tokens_per_s=T / (ms * 1e-3),
+                tflops=tflops, mfma_frac=tflops / PEAK_FP32_MFMA_TFLOPS)
 
 
 def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
@@ -173,26 +248,14 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
         for li, L in enumerate(layers):
             L.forward_dev(xn.ptr, T, x.ptr, None, ids[li].ptr, accumulate=1)
 
-    for _ in range(max(warmup, 1)):
-        step()
-    mh.synchronize()
-    # Headline: K decode steps issued back to back on the library stream,
-    # device time between two events on that stream.
-    mh.timer_start()
+    # Headline: K decode steps issued back to back on the library stream.
     t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    dev_ms = mh.timer_stop()
+    s = stats(mh.timed_steps(step, steps, max(warmup, 1)))
     wall = time.perf_counter() - t0
     # The same step replayed from a captured HIP graph (informational).
     with mh.Graph() as graph:
         step()
-    graph.launch()
-    mh.synchronize()
-    mh.timer_start()
-    for _ in range(steps):
-        graph.launch()
-    graph_ms = mh.timer_stop() / steps
+    graph_s = stats(mh.timed_steps(graph.launch, steps, 1))
     graph.close()
     # Breakdown (informational): one more pass with per-phase events, which
     # themselves add a few microseconds each.
@@ -203,7 +266,7 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
         phase += np.array(mh.last_timings())
     mh.set_timing(False)
     phase /= n_layers
-    ms_step = dev_ms / steps
+    ms_step = s["median"]
     used = [int((np.bincount(i.to_host().ravel(), minlength=E) > 0).sum()) for i in ids]
     bytes_layer = [4.0 * (3 * d * F * u + d * E + 2 * T * d) for u in used]
     bytes_experts = [4.0 * 3 * d * F * u for u in used]
@@ -211,18 +274,50 @@ def decode(mh, steps, warmup, n_layers=8, T=64, d=512, F=2048, E=16, k=2):
     # Events: [route, (dispatch: none in decode), gate/up (the fused kernel
     # does gate/up and down), down (only in the two-launch mode), combine].
     experts_ms = phase[2] + phase[3]
-    res = dict(layers=n_layers, T=T, d=d, F=F, E=E, k=k, ms_per_step=ms_step,
-               wall_ms_per_step=wall * 1e3 / steps, graph_ms_per_step=graph_ms,
+    res = dict(layers=n_layers, T=T, d=d, F=F, E=E, k=k, ms_per_step=ms_step, step_ms=s,
+               wall_ms_per_step=wall * 1e3 / (steps + max(warmup, 1)),
+               graph_ms_per_step=graph_s["median"],
                tokens_per_s=T / (ms_step * 1e-3),
                device_ms_per_layer=dev_ms_layer,
                phase_ms={"route": phase[0], "experts": experts_ms, "combine": phase[4]},
                experts_used=used,
                hbm_gbs_layer=float(np.mean(bytes_layer)) / (dev_ms_layer * 1e-3) / 1e9,
-               hbm_gbs_step=float(np.sum(bytes_layer)) / (ms_step * 1e-3) / 1e9,
                experts_gbs=float(np.mean(bytes_experts)) / (experts_ms * 1e-3) / 1e9)
-    for L in layers:
-        L.close()
-    return res
+    state = dict(layers=layers, xn=xn, x=x)
+    return res, state
+
+
+def decode_host_dropin(mh, st, steps=10, T=64):
+    """moe_decode_batch (host x_norm and x, synchronous) through the same 8
+    layers' weights: the inference_step slot batched over 64 sequences, with
+    its PCIe transfers; weights become resident on the first call."""
+    import abi_types
+    hws = []
+    for L in st["layers"]:
+        wg = np.empty((L.E, L.d, L.F), np.float32)
+        wu = np.empty((L.E, L.d, L.F), np.float32)
+        wd = np.empty((L.E, L.F, L.d), np.float32)
+        for e in range(L.E):
+            mh.check(mh.lib().moe_hip_layer_get_expert(L.h, e, mh.fptr(wg[e]), mh.fptr(wu[e]),
+                                                       mh.fptr(wd[e])))
+        hws.append(abi_types.HostMoE(L.get_router(), wg, wu, wd, L.k))
+    xn = st["xn"].to_host()
+    x = st["x"].to_host()
+
+    def step():
+        for hw in hws:
+            mh.decode_batch(xn, x, hw)
+
+    step()
+    per = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        step()
+        per.append((time.perf_counter() - t0) * 1e3)
+    s = stats(per)
+    return dict(T=T, layers=len(hws), ms_per_step=s["median"], step_ms=s,
+                tokens_per_s=T / (s["median"] * 1e-3),
+                pcie_bytes_per_layer=4.0 * 3 * T * hws[0].d)
 
 
 def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=2, F=2048,
@@ -266,46 +361,32 @@ def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=
             attn[li].decode_block_dev(layers[li], rms.ptr, x.ptr, B, pos.ptr, caches[li][0].ptr,
                                       caches[li][1].ptr, eps)
 
-    def timed(fn):
-        # Steps issued back to back on the library stream, device time between
-        # two events on it; the residual updates are small enough that x stays
-        # near N(0, 1) over the run.
-        for _ in range(max(warmup, 1)):
-            fn()
-        mh.synchronize()
-        mh.timer_start()
-        for _ in range(steps):
-            fn()
-        return mh.timer_stop() / steps
-
+    # (the residual updates are small enough that x stays near N(0, 1))
     mh.fill_normal_dev(x.ptr, B * d, 99, 2, 0.0, 1.0)
-    step_ms = timed(step)
-    attn_ms = timed(attn_only)
+    step_s = stats(mh.timed_steps(step, steps, max(warmup, 1)))
+    attn_s = stats(mh.timed_steps(attn_only, steps, max(warmup, 1)))
     # The attention's other launch arrangement (informational).
     mh.set_attn_path(0 if mh.attn_path() else 1)
-    attn_alt_ms = timed(attn_only)
+    attn_alt = stats(mh.timed_steps(attn_only, steps, max(warmup, 1)))
     mh.set_attn_path(0 if mh.attn_path() else 1)
     # The same step replayed from a captured HIP graph (informational).
     with mh.Graph() as graph:
         step()
-    graph.launch()
-    mh.synchronize()
-    mh.timer_start()
-    for _ in range(steps):
-        graph.launch()
-    graph_ms = mh.timer_stop() / steps
+    graph_s = stats(mh.timed_steps(graph.launch, steps, 1))
     graph.close()
     # Algorithmic bytes of one block's attention: K and V rows 0..ctx of each
     # sequence read once (the new row written once), plus W_Q, W_K, W_V, W_O.
     kv_bytes = 4.0 * 2 * B * (ctx + 1) * kd
     w_bytes = 4.0 * (2 * d * nh * hd + 2 * d * kd)
+    step_ms, attn_ms = step_s["median"], attn_s["median"]
     attn_layer = attn_ms / n_layers
     res = dict(layers=n_layers, B=B, ctx=ctx, d=d, nh=nh, nkv=nkv, hd=hd, F=F, E=E, k=k,
-               ms_per_step=step_ms, tokens_per_s=B / (step_ms * 1e-3),
-               graph_ms_per_step=graph_ms, graph_tokens_per_s=B / (graph_ms * 1e-3),
+               ms_per_step=step_ms, step_ms=step_s, tokens_per_s=B / (step_ms * 1e-3),
+               graph_ms_per_step=graph_s["median"],
+               graph_tokens_per_s=B / (graph_s["median"] * 1e-3),
                attn_ms_per_layer=attn_layer,
                attn_path="one launch" if mh.attn_path() else "launches",
-               attn_other_path_ms_per_layer=attn_alt_ms / n_layers,
+               attn_other_path_ms_per_layer=attn_alt["median"] / n_layers,
                attn_gbs=(kv_bytes + w_bytes) / (attn_layer * 1e-3) / 1e9,
                moe_ms_per_layer=(step_ms - attn_ms) / n_layers)
     for o in attn + layers:
@@ -323,11 +404,12 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, budget_s=15.0, threads=None):
-    """Oracle moe_forward on the first tokens of the prefill workload, `threads`
-    host threads (all cores by default), until ~budget_s of CPU work;
-    tokens/s extrapolates linearly (tokens are independent in the reference
-    loop, src/transformer.c:312)."""
+def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, pass_s=2.5, threads=None):
+    """Oracle moe_forward on the first tokens of the prefill workload with
+    `threads` host threads (all cores by default): the sample is sized so one
+    pass takes about pass_s seconds, then one warm-up pass and the median of
+    5 timed passes.  Tokens/s extrapolates linearly (tokens are independent in
+    the reference loop, src/transformer.c:312)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     layer, ids = st["layer"], st["ids"]
@@ -335,26 +417,32 @@ def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, budget_s=15.0, thre
     xh = st["x"].to_host()
     threads = threads or os.cpu_count() or 1
     ex = st.setdefault("host_experts", {})
-    done, secs = 0, 0.0
-    chunk = max(threads, 16)
-    while secs < budget_s and done < T:
-        rows = slice(done, min(T, done + chunk))
-        for e in sorted(set(ids[rows].ravel().tolist()) - set(ex)):
+
+    def run(n):
+        for e in sorted(set(ids[:n].ravel().tolist()) - set(ex)):
             ex[e] = layer.get_expert(e)
-        xs = np.ascontiguousarray(xh[rows])
+        xs = np.ascontiguousarray(xh[:n])
         t0 = time.perf_counter()
         orc.moe_forward_experts(xs, wr, ex, d, F, E, k, st["bias"], nthreads=threads)
-        secs += time.perf_counter() - t0
-        done = rows.stop
-    return dict(value=done / secs, unit="tokens/s", cores=threads, kind="port",
-                sample=f"first {done} of {T} tokens of the same prefill layer "
-                       f"({secs:.1f} s of oracle time, {threads} threads, {cpu_model()})")
+        return time.perf_counter() - t0
+
+    n = max(4 * threads, 8)
+    for _ in range(2):   # calibration (small samples run slower per token)
+        secs = run(n)
+        n = int(min(T, max(n, n * pass_s / max(secs, 1e-6))))
+    run(n)               # warm-up at the sample size
+    times = [run(n) for _ in range(5)]
+    med = float(np.median(times))
+    return dict(value=n / med, unit="tokens/s", cores=threads, kind="port",
+                sample=f"first {n} of {T} tokens of the same prefill layer, warm-up then "
+                       f"median of 5 passes ({med:.2f} s each), {threads} threads, "
+                       f"{cpu_model()}; oracle built with {ORACLE_BUILD}")
 
 
 def cpu_decode_baseline(mh, T=64, d=512, F=2048, E=16, k=2, n_layers=8):
     """Oracle moe_forward on the 64 decode rows of one layer (all experts
-    host-resident), all host threads; decode tokens/s = 64 / (8 layers x
-    that time)."""
+    host-resident), all host threads, warm-up then the median of 5; decode
+    tokens/s = 64 / (8 layers x that time)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     L = mh.Layer(d, F, E, k)
@@ -365,24 +453,27 @@ def cpu_decode_baseline(mh, T=64, d=512, F=2048, E=16, k=2, n_layers=8):
     x = np.random.default_rng(3).standard_normal((T, d)).astype(np.float32)
     threads = os.cpu_count() or 1
     orc.moe_forward_experts(x, wr, ex, d, F, E, k, None, nthreads=threads)
-    t0 = time.perf_counter()
-    reps = 3
-    for _ in range(reps):
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
         orc.moe_forward_experts(x, wr, ex, d, F, E, k, None, nthreads=threads)
-    layer_s = (time.perf_counter() - t0) / reps
+        times.append(time.perf_counter() - t0)
+    layer_s = float(np.median(times))
     return dict(value=T / (n_layers * layer_s), unit="tokens/s", cores=threads, kind="port",
-                sample=f"one MoE layer on the 64 decode rows, x{n_layers} layers "
-                       f"({layer_s * 1e3:.1f} ms per layer, {threads} threads, {cpu_model()})")
+                sample=f"one MoE layer on the 64 decode rows, x{n_layers} layers, warm-up then "
+                       f"median of 5 ({layer_s * 1e3:.1f} ms per layer), {threads} threads, "
+                       f"{cpu_model()}; oracle built with {ORACLE_BUILD}")
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "prefill_small", "backward", "decode", "decode_step", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "prefill_small", "backward", "decode",
+                                       "decode_step", "c3", "copy"], default=None,
                     help="run one section only (for profiling); prints its JSON to stderr")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -402,11 +493,13 @@ def main():
         mh.check(mh.lib().moe_hip_memcpy(b.ptr, a.ptr, 4 * n, 3))
         log("copy", json.dumps({"bytes": 4 * n}))
         return
+    small_shape = dict(T=4096, d=256, F=1024, E=8, k=2, std_router=0.1, seed=2)
+    c3_shape = dict(T=4096, d=512, F=2048, E=8, k=2, std_router=0.02, seed=3)
     if args.only == "decode":
-        log("decode", json.dumps(decode(mh, args.steps, args.warmup)))
+        log("decode", json.dumps(decode(mh, args.steps, args.warmup)[0]))
         return
     if args.only == "prefill_small":
-        log("prefill_small", json.dumps(prefill_small(mh, args.steps, args.warmup)))
+        log("prefill_small", json.dumps(layer_bench(mh, args.steps, args.warmup, **small_shape)))
         return
     if args.only == "backward":
         log("backward", json.dumps(backward_small(mh, args.steps, args.warmup)))
@@ -414,28 +507,41 @@ def main():
     if args.only == "decode_step":
         log("decode_step", json.dumps(decode_step(mh, args.steps, args.warmup)))
         return
-    pre, st = prefill(mh, args.steps, args.warmup)
-    if args.only == "prefill":
-        log("prefill", json.dumps(pre))
+    if args.only == "c3":
+        log("c3_layer", json.dumps(layer_bench(mh, args.steps, args.warmup, **c3_shape)))
+        log("c3_stack", json.dumps(ffn_stack(mh, args.steps, args.warmup)))
         return
+    pre, st = prefill(mh, args.steps, args.warmup)
     log("prefill", json.dumps(pre))
-    small = prefill_small(mh, args.steps, args.warmup)
+    if args.only == "prefill":
+        return
+    hio = prefill_host_io(mh, st)
+    log("prefill_host_io", json.dumps(hio))
+    small = layer_bench(mh, args.steps, args.warmup, **small_shape)
     log("prefill_small", json.dumps(small))
     bwd = backward_small(mh, args.steps, args.warmup)
     log("backward", json.dumps(bwd))
     dropin = dropin_small(mh, args.steps, args.warmup)
     log("dropin", json.dumps(dropin))
-    dec = stp = None
+    c3 = layer_bench(mh, args.steps, args.warmup, **c3_shape)
+    log("c3_layer", json.dumps(c3))
+    c3s = ffn_stack(mh, args.steps, args.warmup)
+    log("c3_stack", json.dumps(c3s))
+    dec = dech = stp = None
     if not args.no_decode:
-        dec = decode(mh, args.steps, args.warmup)
+        dec, dst = decode(mh, args.steps, args.warmup)
         log("decode", json.dumps(dec))
+        dech = decode_host_dropin(mh, dst)
+        log("decode_host_dropin", json.dumps(dech))
+        for L in dst["layers"]:
+            L.close()
         stp = decode_step(mh, args.steps, args.warmup)
         log("decode_step", json.dumps(stp))
     cpu = cpu1 = cpu_dec = None
     if not args.no_cpu:
         cpu = cpu_baseline(mh, st)
         log("cpu", json.dumps(cpu))
-        cpu1 = cpu_baseline(mh, st, budget_s=5.0, threads=1)
+        cpu1 = cpu_baseline(mh, st, pass_s=1.0, threads=1)
         log("cpu 1 thread", json.dumps(cpu1))
         cpu_dec = cpu_decode_baseline(mh)
         log("cpu decode", json.dumps(cpu_dec))
@@ -457,6 +563,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "ms_per_step_stats": pre["step_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -475,6 +582,11 @@ def main():
         "cpu_baseline": cpu,
         "cpu_baseline_1thread": cpu1,
     }
+    line["prefill_host_io"] = {
+        "workload": "the headline layer with x from and out / probs / ids to pageable host "
+                    "memory (PCIe included, synchronous call)",
+        "tokens_per_s": hio["tokens_per_s"], "ms_per_step": hio["ms"],
+        "pcie_bytes_per_call": hio["pcie_bytes"]}
     line["prefill_batch8x512"] = {
         "workload": "moe prefill layer T=4096 (8 x 512) d=256 d_ff=1024 E=8 top-2",
         "tokens_per_s": small["tokens_per_s"], "ms_per_step": small["ms"],
@@ -488,6 +600,16 @@ def main():
                     "(routing and expert products recomputed)",
         "ms_per_step": bwd["ms"], "tokens_per_s": bwd["tokens_per_s"],
         "tflops": bwd["tflops"], "fp32_peak_frac": bwd["mfma_frac"]}
+    line["moe_layer_c3"] = {
+        "workload": "one MoE layer of the 8-block decoder at batch 8 x seq 512: T=4096 d=512 "
+                    "d_ff=2048 E=8 top-2",
+        "tokens_per_s": c3["tokens_per_s"], "ms_per_step": c3["ms"],
+        "layer_mfma_frac": c3["mfma_frac"]}
+    line["moe_stack_c3"] = {
+        "workload": "the 8 MoE FFN sublayers of that decoder, x += MoE(rms_norm(x)) in place "
+                    "(moe_hip_ffn_sublayer_dev)",
+        "tokens_per_s": c3s["tokens_per_s"], "ms_per_step": c3s["ms_per_step"],
+        "ms_per_layer": c3s["ms_per_layer"], "mfma_frac": c3s["mfma_frac"]}
     if dec:
         line["decode"] = {
             "workload": "64 seqs x 1 token, 8 MoE layers d=512 d_ff=2048 E=16 top-2",
@@ -500,6 +622,10 @@ def main():
             "phase_ms_per_layer": dec["phase_ms"],
             "cpu_baseline": cpu_dec,
         }
+        line["decode_host_dropin"] = {
+            "workload": "the same 8 layers through moe_decode_batch, host x_norm and x "
+                        "(PCIe included, synchronous calls)",
+            "tokens_per_s": dech["tokens_per_s"], "ms_per_step": dech["ms_per_step"]}
     if stp:
         line["decode_step"] = {
             "workload": "64 seqs x 1 token at context 1024, 8 blocks of GQA 8/2 attention "

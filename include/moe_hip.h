@@ -356,6 +356,11 @@ int moe_hip_set_timing(int on);
  * timer_stop (which waits for the stream), in milliseconds. */
 int moe_hip_timer_start(void);
 int moe_hip_timer_stop(float *ms);
+/* Mark i (0 <= i < 64) recorded on the library stream without waiting, and
+ * the device time between marks i and j (waits for mark j): per-call times
+ * of a loop that is not synchronised inside. */
+int moe_hip_timer_mark(int i);
+int moe_hip_timer_between(int i, int j, float *ms);
 
 /* ---------------------------------------------------------------------------
  * Device memory helpers for callers with no HIP binding of their own (the

@@ -42,6 +42,8 @@ hipStream_t g_stream = nullptr;
 bool g_timing = false;
 hipEvent_t g_ev[6] = {};
 hipEvent_t g_tev[2] = {};
+constexpr int kMarks = 64;
+hipEvent_t g_marks[kMarks] = {};
 bool g_have_times = false;
 int g_path = 0;   // 0 auto, 1 grouped GEMMs, 2 decode GEMVs (fused), 3 decode GEMVs (two launches)
 int g_rpath = 0;  // 0 auto, 1 token x expert tiles, 2 one token per lane
@@ -300,6 +302,7 @@ int moe_hip_init(int device) {
     HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     for (auto &ev : g_ev) HIP_TRY(hipEventCreate(&ev));
     for (auto &ev : g_tev) HIP_TRY(hipEventCreate(&ev));
+    for (auto &ev : g_marks) HIP_TRY(hipEventCreate(&ev));
     char *sp = nullptr;
     TRY(scratch_of(g_stream, &sp));
     HIP_TRY(hipStreamSynchronize(g_stream));
@@ -317,6 +320,7 @@ void moe_hip_shutdown(void) {
     g_ext_capture = false;
     for (auto &ev : g_ev) (void)hipEventDestroy(ev);
     for (auto &ev : g_tev) (void)hipEventDestroy(ev);
+    for (auto &ev : g_marks) (void)hipEventDestroy(ev);
     (void)hipStreamDestroy(g_stream);
     g_stream = nullptr;
     g_init = false;
@@ -1072,6 +1076,22 @@ int moe_hip_timer_stop(float *ms) {
     HIP_TRY(hipEventRecord(g_tev[1], g_stream));
     HIP_TRY(hipEventSynchronize(g_tev[1]));
     HIP_TRY(hipEventElapsedTime(ms, g_tev[0], g_tev[1]));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_timer_mark(int i) {
+    TRY(ensure_init());
+    if (i < 0 || i >= kMarks) return set_err(MOE_HIP_ERR_ARG, "mark %d outside [0, %d)", i, kMarks);
+    HIP_TRY(hipEventRecord(g_marks[i], g_stream));
+    return MOE_HIP_OK;
+}
+
+int moe_hip_timer_between(int i, int j, float *ms) {
+    if (!ms || i < 0 || j < 0 || i >= kMarks || j >= kMarks)
+        return set_err(MOE_HIP_ERR_ARG, "bad marks %d, %d", i, j);
+    TRY(ensure_init());
+    HIP_TRY(hipEventSynchronize(g_marks[j]));
+    HIP_TRY(hipEventElapsedTime(ms, g_marks[i], g_marks[j]));
     return MOE_HIP_OK;
 }
 

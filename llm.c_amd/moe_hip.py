@@ -87,6 +87,8 @@ SIGNATURES = {
     "moe_hip_device_check": (C.c_int, []),
     "moe_hip_timer_start": (C.c_int, []),
     "moe_hip_timer_stop": (C.c_int, [_F]),
+    "moe_hip_timer_mark": (C.c_int, [C.c_int]),
+    "moe_hip_timer_between": (C.c_int, [C.c_int, C.c_int, _F]),
     "moe_hip_dev_alloc": (C.c_int, [C.POINTER(_P), C.c_size_t]),
     "moe_hip_dev_free": (C.c_int, [_P]),
     "moe_hip_memcpy": (C.c_int, [_P, _P, C.c_size_t, C.c_int]),
@@ -460,6 +462,30 @@ def timer_stop():
     ms = C.c_float()
     check(lib().moe_hip_timer_stop(C.byref(ms)))
     return ms.value
+
+
+def timed_steps(fn, steps, warmup):
+    """Device milliseconds of each of `steps` calls of fn() on the library
+    stream, read from marks recorded between the calls (nothing inside the
+    loop waits); warmup untimed calls first.  Returns the per-call list."""
+    for _ in range(warmup):
+        fn()
+    synchronize()
+    out = []
+    done = 0
+    while done < steps:
+        n = min(steps - done, 63)
+        check(lib().moe_hip_timer_mark(0))
+        for i in range(n):
+            fn()
+            check(lib().moe_hip_timer_mark(i + 1))
+        ms = C.c_float()
+        for i in range(n):
+            check(lib().moe_hip_timer_between(i, i + 1, C.byref(ms)))
+            out.append(ms.value)
+        done += n
+    synchronize()
+    return out
 
 
 def last_timings():
