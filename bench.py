@@ -365,10 +365,6 @@ def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=
     mh.fill_normal_dev(x.ptr, B * d, 99, 2, 0.0, 1.0)
     step_s = stats(mh.timed_steps(step, steps, max(warmup, 1)))
     attn_s = stats(mh.timed_steps(attn_only, steps, max(warmup, 1)))
-    # The attention's other launch arrangement (informational).
-    mh.set_attn_path(0 if mh.attn_path() else 1)
-    attn_alt = stats(mh.timed_steps(attn_only, steps, max(warmup, 1)))
-    mh.set_attn_path(0 if mh.attn_path() else 1)
     # The same step replayed from a captured HIP graph (informational).
     with mh.Graph() as graph:
         step()
@@ -385,8 +381,6 @@ def decode_step(mh, steps, warmup, n_layers=8, B=64, ctx=1024, d=512, nh=8, nkv=
                graph_ms_per_step=graph_s["median"],
                graph_tokens_per_s=B / (graph_s["median"] * 1e-3),
                attn_ms_per_layer=attn_layer,
-               attn_path="one launch" if mh.attn_path() else "launches",
-               attn_other_path_ms_per_layer=attn_alt["median"] / n_layers,
                attn_gbs=(kv_bytes + w_bytes) / (attn_layer * 1e-3) / 1e9,
                moe_ms_per_layer=(step_ms - attn_ms) / n_layers)
     for o in attn + layers:

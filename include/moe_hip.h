@@ -267,12 +267,11 @@ int moe_hip_attn_set_rope(MoeHipAttn *attn, const float *cos_table, const float 
  * [B][max_seq_len][nkv*hd] (a LayerKVCache per sequence, contiguous), and
  * head h attends positions 0 .. pos[b] of kv head h / (nh/nkv)
  * (src/inference.c:252-308).  pos: device ints.  The projections are
- * split-reduction tiles with rms_norm's row scale applied after the
+ * 16 x 16 output tiles with rms_norm's row scale applied after the
  * reduction, and the softmax and V sums run in 128-position chunks, so
  * results match the reference within the layer tolerance rather than bit
  * for bit (deterministically).  Three launches (four for head shapes other
- * than head_dim 16/32/64 with 2, 4 or 8 query heads per kv head), or one
- * (moe_hip_set_attn_path; see moe_hip_device_check).
+ * than head_dim 16/32/64 with 2, 4 or 8 query heads per kv head).
  * A pos[b] outside [0, max_seq_len) leaves sequence b's caches and x row
  * unchanged. */
 int moe_hip_attn_decode_dev(MoeHipAttn *attn, float *x, int B, const int *pos, float *k_cache,
@@ -329,18 +328,6 @@ int moe_hip_set_expert_path(int mode);
  * 2 = 16-token row blocks with every expert in one workgroup.  Process-wide;
  * both give the same bits. */
 int moe_hip_set_router_path(int mode);
-
-/* Decode attention as one launch where the head shape allows (fused = 1)
- * or as separate launches (0, the default).  Process-wide; both compute the
- * same values.  get returns the current setting. */
-int moe_hip_set_attn_path(int fused);
-int moe_hip_get_attn_path(void);
-
-
-/* Waits for the library stream and reports whether a bounded device-side
- * wait of the one-launch decode attention gave up since the last check (the
- * results of that call are then invalid); clears the flag. */
-int moe_hip_device_check(void);
 
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,
  * src/matrix.c:82-116) or glibc-expf restatement (which = 1) of x[i], the two

@@ -3,31 +3,23 @@
 // position, on gfx950:  x += W_O . Attn(RoPE(W_Q xn), RoPE(W_K xn), W_V xn)
 // with xn = rms_norm(x) and the new k, v rows appended to the caches.
 //
-// Three roles, run as one launch (attn_fused_kernel, head_dim 16/32/64 with
-// 2/4/8 query heads per kv head) or as separate launches:
-//   QKV tile      q, k, v as a split-K tiled product: 32 x 32 output tiles,
-//                 128-long reduction slices per workgroup (32 per wave,
-//                 summed through LDS).  rms_norm's row scale 1/rms (:48-60)
-//                 is taken out of the reduction: tiles multiply x * w_rms,
-//                 each slice also sums its x^2, and the tile's last slice
-//                 to finish adds the slices, scales by 1/sqrt(ss/d + eps),
-//                 applies RoPE at the sequence's position from the caller's
-//                 tables (:187-203) to q and k, and writes q and the cache
-//                 rows at pos.
-//   chunk         one workgroup per (sequence, kv head, 128 positions)
+// Three launches:
+//   QKV tiles     q, k, v = rms_norm(x) . [W_Q | W_K | W_V]: one 1024-thread
+//                 workgroup per 16 x 16 output tile with the whole reduction
+//                 (proj16_kernel).  rms_norm's row scale 1/rms (:48-60) is
+//                 taken out of the reduction: tiles multiply x * w_rms, sum
+//                 x^2 on the side, scale by 1/sqrt(ss/d + eps), apply RoPE at
+//                 the sequence's position from the caller's tables (:187-203)
+//                 to q and k, and write q and the cache rows at pos.
+//   chunks        one workgroup per (sequence, kv head, 128 positions)
 //                 streams that K and V once for the kv head's query heads:
 //                 scores times 1/sqrt(hd), exp against the chunk maximum,
 //                 the V sum; the last chunk of a (sequence, kv head) merges
 //                 the chunk partials (m, l, o) into o.  Bound by the K/V
-//                 reads.  In the fused launch the cache rows before pos are
-//                 requested at once, before the QKV tiles are done; only q
-//                 and the new row wait for them.
-//   W_O tile      x += o . W_O with the same tiles; the tile's last slice
-//                 adds the slices into x (the element add of :306).
-// Roles hand data to each other within a launch through device-scope
-// coherent stores and loads and counters (see the helpers below); in the
-// fused launch later roles wait, boundedly, for earlier ones, which sit at
-// lower workgroup indices and so are dispatched first.
+//                 reads.
+//   W_O tiles     x += o . W_O with the same tiles (the element add of :306).
+// The chunks hand their partials to the merging chunk through device-scope
+// coherent stores and a counter (the last to arrive merges; nothing waits).
 // Sequences whose position lies outside [0, max_seq) are left untouched.
 // Reductions run in a fixed order, so results are deterministic, but the
 // order differs from the reference's sequential sums (and the reference
@@ -43,8 +35,6 @@ namespace moe {
 namespace {
 
 constexpr int kChunkPos = 128;   // positions per attention workgroup
-constexpr int kTile = 32;        // rows and columns of a projection tile
-constexpr int kSliceK = 128;     // reduction length per projection workgroup
 
 // RoPE on the pair (v0, v1) = columns 2i, 2i + 1 of a head (:196-199).
 __device__ inline void rope_pair(float &v0, float &v1, float c, float s) {
@@ -61,24 +51,6 @@ __device__ inline float comp(const float4 &v, int j) {
     return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
 }
 
-// Readiness of a count in the one-launch sublayer: kFlagCopies flags, one
-// per 128-byte line, all set by the workgroup that completes the count;
-// waiters each poll one copy, so polling is spread over many addresses.
-constexpr int kFlagCopies = 64, kFlagStride = 32;   // ints
-// sync layout: [0] QKV tiles done, [1] merges done, [2] workgroups out, then
-// the two flag sets.
-constexpr int kSyncQkvFlags = kFlagStride;
-constexpr int kSyncMergeFlags = kSyncQkvFlags + kFlagCopies * kFlagStride;
-// After publish(), one bump of *ctr; the bump that makes it `expect` sets
-// the flags.
-__device__ inline void signal(int *ctr, int expect, int *flags) {
-    publish();
-    if (threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expect - 1)
-        for (int i = 0; i < kFlagCopies; ++i)
-            __hip_atomic_store(flags + i * kFlagStride, 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-}
 // True in every thread of the workgroup that arrives last of `expect` at
 // *cnt (after publishing its stores); that one also resets the counter.
 __device__ inline bool arrive_last(int *cnt, int expect, int *flag) {
@@ -92,204 +64,7 @@ __device__ inline bool arrive_last(int *cnt, int expect, int *flag) {
     __syncthreads();
     return *flag;
 }
-// Thread 0 waits (bounded; past the bound it raises *err and goes on, so
-// every wave ends) until its copy of the flags is set; then the workgroup
-// passes a barrier.
-__device__ inline void wait_flag(const int *flags, int *err) {
-    if (threadIdx.x == 0) {
-        const int *f = flags + (blockIdx.x % kFlagCopies) * kFlagStride;
-        int spins = 0;
-        while (__hip_atomic_load(const_cast<int *>(f), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) == 0) {
-            if (++spins > kSpinLimit) {
-                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-        }
-    }
-    __syncthreads();
-}
-
-__host__ __device__ inline int slices(int M) { return (M + kSliceK - 1) / kSliceK; }
-__host__ __device__ inline int tiles(int n) { return (n + kTile - 1) / kTile; }
-
 // ---------------------------------------------------------------------------
-// Projection tiles.
-struct ProjSmem {
-    union {
-        struct {
-            float4 xs[kTile][kSliceK / 4 + 1];   // X rows of the slice (padded)
-            float4 ws[kSliceK][kTile / 4];       // W rows of the slice
-        };
-        float4 red[4][kTile][kTile / 4];         // per-wave partial tiles, after the products
-    };
-    int flag;
-};
-
-// Tile (tx, ty) and reduction slice z of Y = X . W for X [B x M], W [M x N]:
-// QKV: X = x scaled by w_rms, W = [W_Q | W_K | W_V]; WO: X = o, W = W_O.
-// Threads load row tid / 8 of X and rows tid / 8 + 32i of W; wave w takes
-// slice rows 32w .. 32w + 31, lane (rq, cq) = (lane / 8, lane % 8) rows
-// 4rq .. 4rq + 3 and columns 4cq .. 4cq + 3 of the tile.  FUSED: part of the
-// one-launch sublayer (WO waits for the merges; QKV's outputs are written
-// coherently and counted).
-template <bool QKV, bool FUSED>
-__device__ void proj_tile(const AttnArgs &a, int tx, int ty, int z, int ntx, int S, ProjSmem &sm) {
-    const int M = QKV ? a.d : a.qd, N = QKV ? a.qd + 2 * a.kd : a.d;
-    const int r0 = ty * kTile, c0 = tx * kTile, k0 = z * kSliceK;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-
-    float4 wv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int idx = tid + 256 * i, k = k0 + (idx >> 3), col = c0 + 4 * (idx & 7);
-        const float *src = nullptr;
-        if (k < M && col < N) {
-            if (!QKV)                     src = a.wo + (size_t)k * a.d + col;
-            else if (col < a.qd)          src = a.wq + (size_t)k * a.qd + col;
-            else if (col < a.qd + a.kd)   src = a.wk + (size_t)k * a.kd + (col - a.qd);
-            else                          src = a.wv + (size_t)k * a.kd + (col - a.qd - a.kd);
-        }
-        wv[i] = src ? *reinterpret_cast<const float4 *>(src) : zero;
-    }
-    if (FUSED && !QKV) wait_flag(a.sync + kSyncMergeFlags, a.err);   // every merge is done
-    const int xr = tid >> 3, xrow = r0 + xr;
-    float4 xv[4];
-    {
-        const float *X = QKV ? a.x : a.o;
-        const size_t rb = (size_t)(xrow < a.B ? xrow : 0) * M;
-        const CRead cx(X);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int k = k0 + 4 * ((tid & 7) + 8 * i);
-            const bool in = xrow < a.B && k < M;
-            if (FUSED && !QKV) xv[i] = cx.f4(in ? rb + k : 0);
-            else               xv[i] = in ? *reinterpret_cast<const float4 *>(X + rb + k) : zero;
-            if (!in) xv[i] = zero;
-        }
-    }
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int kq = (tid & 7) + 8 * i, k = k0 + 4 * kq;
-        float4 v = xv[i];
-        if (QKV && k < M) {
-            ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss);
-            ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
-            const float4 w = *reinterpret_cast<const float4 *>(a.rms_w + k);
-            v = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
-        }
-        sm.xs[xr][kq] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int idx = tid + 256 * i;
-        sm.ws[idx >> 3][idx & 7] = wv[i];
-    }
-    if (QKV) {
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 4);
-        if ((tid & 7) == 0 && xrow < a.B) cstore(a.sspart + (size_t)z * a.B + xrow, ss);
-    }
-    __syncthreads();
-
-    const int rq = lane >> 3, cq = lane & 7;
-    float acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[i][c] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kSliceK / 16; ++s) {
-        const int kq = wave * (kSliceK / 16) + s;
-        float4 xa[4], wb[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xa[i] = sm.xs[4 * rq + i][kq];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) wb[j] = sm.ws[4 * kq + j][cq];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float xij = comp(xa[i], j);
-                acc[i][0] = fmaf(xij, wb[j].x, acc[i][0]);
-                acc[i][1] = fmaf(xij, wb[j].y, acc[i][1]);
-                acc[i][2] = fmaf(xij, wb[j].z, acc[i][2]);
-                acc[i][3] = fmaf(xij, wb[j].w, acc[i][3]);
-            }
-    }
-    __syncthreads();   // (red overlays xs and ws)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        sm.red[wave][4 * rq + i][cq] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
-    __syncthreads();
-    const int orow = r0 + (tid >> 3), ocol = c0 + 4 * (tid & 7);
-    const bool owned = orow < a.B && ocol < N;
-    if (owned) {
-        const int r = tid >> 3, c = tid & 7;
-        const float4 v = add4(add4(sm.red[0][r][c], sm.red[1][r][c]),
-                              add4(sm.red[2][r][c], sm.red[3][r][c]));
-        cstore4(a.gpart + ((size_t)z * a.B + orow) * N + ocol, v);
-    }
-
-    // The last slice of this tile to finish adds the slices and writes out;
-    // what that epilogue needs besides the slices is fetched before arriving.
-    const int p = owned ? a.pos[orow] : -1;
-    const bool live = owned && p >= 0 && p < a.max_seq;
-    const int col = ocol < a.qd ? ocol : ocol < a.qd + a.kd ? ocol - a.qd : ocol - a.qd - a.kd;
-    const bool rope = QKV && live && ocol < a.qd + a.kd;
-    float4 cs = zero;   // (cos, sin) of the column's two RoPE pairs
-    if (rope) {
-        const int half = a.hd / 2, i0 = (col % a.hd) / 2;
-        const float *cr = a.cos_t + (size_t)p * half + i0, *sr = a.sin_t + (size_t)p * half + i0;
-        cs = make_float4(cr[0], sr[0], cr[1], sr[1]);
-    }
-    float4 xo = zero;
-    if (!QKV && live) xo = *reinterpret_cast<const float4 *>(a.x + (size_t)orow * a.d + ocol);
-
-    if (!arrive_last((QKV ? a.cnt_qkv : a.cnt_wo) + ty * ntx + tx, S, &sm.flag)) return;
-    if (live) {
-        const CRead gp(a.gpart), sp(a.sspart);
-        float4 y = zero;
-        float sq = 0.0f;
-        for (int z0 = 0; z0 < S; z0 += 4) {
-            float4 v[4];
-            float q2[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int zz = z0 + u < S ? z0 + u : 0;
-                v[u] = gp.f4(((size_t)zz * a.B + orow) * N + ocol);
-                q2[u] = QKV ? sp((size_t)zz * a.B + orow) : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (z0 + u < S) {
-                    y = add4(y, v[u]);
-                    sq += q2[u];
-                }
-        }
-        if (!QKV) {
-            *reinterpret_cast<float4 *>(a.x + (size_t)orow * a.d + ocol) = add4(xo, y);
-        } else {
-            const float inv = 1.0f / sqrtf(sq / (float)M + a.eps);
-            y = make_float4(y.x * inv, y.y * inv, y.z * inv, y.w * inv);
-            if (rope) {   // q or k: RoPE at p on both pairs
-                rope_pair(y.x, y.y, cs.x, cs.y);
-                rope_pair(y.z, y.w, cs.z, cs.w);
-            }
-            float *dst = ocol < a.qd ? a.q + (size_t)orow * a.qd
-                                     : (ocol < a.qd + a.kd ? a.kc : a.vc) +
-                                           ((size_t)orow * a.max_seq + p) * a.kd;
-            if (FUSED) cstore4(dst + col, y);
-            else       *reinterpret_cast<float4 *>(dst + col) = y;
-        }
-    }
-    if (FUSED && QKV) signal(a.sync, a.nqkv_tiles, a.sync + kSyncQkvFlags);   // q, k, v are out
-}
-
 // Projection tiles without a split reduction: one 1024-thread workgroup per
 // 16 x 16 output tile (tile column blockIdx.x, row blockIdx.y).  The X rows
 // and W columns of a 512-long reduction chunk are staged in LDS: thread t
@@ -298,8 +73,9 @@ __device__ void proj_tile(const AttnArgs &a, int tx, int ty, int z, int ntx, int
 // (rr, cq) = (lane / 4, lane % 4) row rr and columns 4cq .. 4cq + 3; the
 // sixteen waves' sums are added through LDS in wave order.  QKV: row r's
 // sum of x^2 is each thread's k-ordered share, summed over its wave and
-// then over the row's two waves; the epilogue (1/rms, RoPE, q and the cache
-// rows) as in proj_tile.  WO: x += the products.  One global round trip.
+// then over the row's two waves; the epilogue scales by 1/rms, applies RoPE
+// at the sequence's position to q and k and writes q and the cache rows at
+// pos.  WO: x += the products.  One global round trip.
 constexpr int kPT = 16, kPK = 512;
 struct Proj16Smem {
     union {
@@ -515,10 +291,8 @@ template <int HD, int G> struct ChunkSmem {
 // takes the chunk maximum m, p = exp(s - m) and l = sum p; the V sum uses
 // the V registers, then LDS across the R row groups.  The partial (m, l,
 // o[HD]) goes out coherently; the last of the pos / 128 + 1 chunks with
-// positions merges them into o.  FUSED: q and the row at pos come from the
-// QKV tiles of the same launch (waited for, read coherently); the merge is
-// counted, and a sequence without a valid position counts once (chunk 0).
-template <int HD, int G, bool FUSED>
+// positions merges them into o.
+template <int HD, int G>
 __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
     constexpr int L = HD / 4, R = 256 / L, NI = kChunkPos / R, CNT = NI * G, PER = CNT / L;
     static_assert(PER >= 1 && CNT % L == 0, "chunk layout");
@@ -534,51 +308,30 @@ __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
     const int j0 = c * kChunkPos, n = min(kChunkPos, p + 1 - j0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cq = tid % L, rg = tid / L;
-    if (n <= 0) {   // past the sequence (the merge reads chunks 0 .. pos / 128)
-        if (FUSED && p < 0 && c == 0) signal(a.sync + 1, a.B * a.nkv, a.sync + kSyncMergeFlags);
-        return;
-    }
+    if (n <= 0) return;   // past the sequence (the merge reads chunks 0 .. pos / 128)
     float *part = a.part + ((size_t)(b * a.nh + kvh * G) * nchunk + c) * (HD + 2);
     const size_t head_stride = (size_t)nchunk * (HD + 2);
-    const int prow = FUSED ? p - j0 : -1;   // the new row (in this chunk if < 128)
     const size_t base = ((size_t)b * a.max_seq + j0) * a.kd + kvh * HD + 4 * cq;
     float4 kv[NI], vv[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int row = i * R + rg;
-        const bool in = row < n && row != prow;
+        const bool in = row < n;
         const size_t off = base + (size_t)(in ? row : 0) * a.kd;
         kv[i] = in ? *reinterpret_cast<const float4 *>(a.kc + off) : make_float4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int row = i * R + rg;
-        const bool in = row < n && row != prow;
+        const bool in = row < n;
         const size_t off = base + (size_t)(in ? row : 0) * a.kd;
         vv[i] = in ? *reinterpret_cast<const float4 *>(a.vc + off) : make_float4(0, 0, 0, 0);
     }
     float4 q[G];
-    if (FUSED) {
-        wait_flag(a.sync + kSyncQkvFlags, a.err);   // q and the new k, v rows are out
-        const CRead qr(a.q + (size_t)b * a.qd + kvh * G * HD);
 #pragma unroll
-        for (int h = 0; h < G; ++h) q[h] = qr.f4(h * HD + 4 * cq);
-        if (prow < kChunkPos) {
-            const size_t rowoff = ((size_t)b * a.max_seq + p) * a.kd + kvh * HD;
-            const CRead kr(a.kc + rowoff), vr(a.vc + rowoff);
-#pragma unroll
-            for (int i = 0; i < NI; ++i)
-                if (i * R + rg == prow) {
-                    kv[i] = kr.f4(4 * cq);
-                    vv[i] = vr.f4(4 * cq);
-                }
-        }
-    } else {
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-            q[h] = *reinterpret_cast<const float4 *>(a.q + (size_t)b * a.qd + (kvh * G + h) * HD +
-                                                     4 * cq);
-    }
+    for (int h = 0; h < G; ++h)
+        q[h] = *reinterpret_cast<const float4 *>(a.q + (size_t)b * a.qd + (kvh * G + h) * HD +
+                                                 4 * cq);
     float v[CNT];
 #pragma unroll
     for (int i = 0; i < NI; ++i)
@@ -647,60 +400,17 @@ __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
     const CRead rd(a.part + ph0);
     float *ob = a.o + (size_t)b * a.qd + kvh * G * HD;
     for (int t = tid; t < G * HD; t += 256) {
-        const float ov = merge_head(rd, (size_t)(t / HD) * head_stride, nc, HD, t % HD);
-        if (FUSED) cstore(ob + t, ov);
-        else       ob[t] = ov;
+        ob[t] = merge_head(rd, (size_t)(t / HD) * head_stride, nc, HD, t % HD);
     }
-    if (FUSED) signal(a.sync + 1, a.B * a.nkv, a.sync + kSyncMergeFlags);
 }
 
 // ---------------------------------------------------------------------------
 // Kernels.
 
-// The whole sublayer in one launch: workgroups [0, nq) QKV tiles, [nq,
-// nq + nc) chunks, the rest W_O tiles.  The last workgroup to exit resets
-// the launch's counters.
-template <int HD, int G>
-__global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a, int nq, int nc) {
-    __shared__ union Smem {
-        ProjSmem p;
-        ChunkSmem<HD, G> c;
-    } sm;
-    const int bid = blockIdx.x;
-    if (bid < nq) {
-        const int S = slices(a.d), ntx = tiles(a.qd + 2 * a.kd), t = bid / S;
-        proj_tile<true, true>(a, t % ntx, t / ntx, bid % S, ntx, S, sm.p);
-    } else if (bid < nq + nc) {
-        chunk<HD, G, true>(a, bid - nq, sm.c);
-    } else {
-        const int r = bid - nq - nc, S = slices(a.qd), ntx = tiles(a.d), t = r / S;
-        proj_tile<false, true>(a, t % ntx, t / ntx, r % S, ntx, S, sm.p);
-    }
-    __syncthreads();
-    if (threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(a.sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            (int)gridDim.x - 1) {
-        for (int i = 0; i < 3; ++i)
-            __hip_atomic_store(a.sync + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int i = 0; i < kFlagCopies; ++i) {
-            __hip_atomic_store(a.sync + kSyncQkvFlags + i * kFlagStride, 0, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.sync + kSyncMergeFlags + i * kFlagStride, 0, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-}
-
-template <bool QKV>
-__global__ __launch_bounds__(256) void proj_tile_kernel(AttnArgs a) {
-    __shared__ ProjSmem sm;
-    proj_tile<QKV, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, gridDim.z, sm);
-}
-
 template <int HD, int G>
 __global__ __launch_bounds__(256) void attn_chunk_fast_kernel(AttnArgs a) {
     __shared__ ChunkSmem<HD, G> sm;
-    chunk<HD, G, false>(a, blockIdx.x, sm);
+    chunk<HD, G>(a, blockIdx.x, sm);
 }
 
 // Generic head shapes.  Workgroup (b, kv head, chunk c): positions j in
@@ -808,7 +518,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnArgs a) {
                           p / kChunkPos + 1, a.hd, t);
 }
 
-// Head shapes with a fast chunk kernel (and the one-launch sublayer).
+// Head shapes with a fast chunk kernel.
 template <class F> bool with_fast_shape(int hd, int g, F &&f) {
 #define MOE_ATTN_SHAPE(HD_, G_)                                     \
     if (hd == HD_ && g == G_) {                                     \
@@ -826,27 +536,6 @@ template <class F> bool with_fast_shape(int hd, int g, F &&f) {
 
 size_t attn_part_floats(int B, int nh, int hd, int max_seq) {
     return (size_t)B * nh * ((max_seq + kChunkPos - 1) / kChunkPos) * (hd + 2);
-}
-
-size_t attn_gpart_floats(int B, int d, int qd, int kd) {
-    const size_t qkv = (size_t)slices(d) * (qd + 2 * kd), wo = (size_t)slices(qd) * d;
-    return (size_t)B * (qkv > wo ? qkv : wo);
-}
-
-size_t attn_sspart_floats(int B, int d) { return (size_t)slices(d) * B; }
-
-int attn_sync_ints() { return kSyncMergeFlags + kFlagCopies * kFlagStride; }
-
-AttnCounters attn_counters(int B, int d, int qd, int kd, int nkv) {
-    AttnCounters c;
-    c.qkv = tiles(qd + 2 * kd) * tiles(B);
-    c.wo = tiles(d) * tiles(B);
-    c.merge = B * nkv;
-    return c;
-}
-
-bool attn_fused_supported(int hd, int nh, int nkv) {
-    return nkv > 0 && nh % nkv == 0 && with_fast_shape(hd, nh / nkv, [](auto, auto) {});
 }
 
 namespace {
@@ -870,7 +559,7 @@ hipError_t launch_pack_cols16(const float *src, float *dst, int K, int N, int co
     return hipGetLastError();
 }
 
-hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s) {
+hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) {
     if (a.B <= 0) return hipSuccess;
     const int gqa = a.nh / a.nkv;
     if (a.hd > 64 || a.hd % 8 || gqa > 8 || a.nh % a.nkv || a.d % 4 || a.qd % 4)
@@ -878,17 +567,7 @@ hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s) {
     const int N = a.qd + 2 * a.kd;
     const int nchunk = (a.max_seq + kChunkPos - 1) / kChunkPos;
     const int nc = a.B * a.nkv * nchunk;
-    if (fused) {
-        if (!a.sync || !a.err || a.nqkv_tiles != tiles(N) * tiles(a.B)) return hipErrorInvalidValue;
-        const int nq = tiles(N) * tiles(a.B) * slices(a.d);
-        const int no = tiles(a.d) * tiles(a.B) * slices(a.qd);
-        const bool ok = with_fast_shape(a.hd, gqa, [&](auto hd, auto g) {
-            hipLaunchKernelGGL((attn_fused_kernel<decltype(hd)::value, decltype(g)::value>),
-                               dim3((unsigned)(nq + nc + no)), dim3(256), 0, s, a, nq, nc);
-        });
-        if (!ok) return hipErrorInvalidValue;
-        return hipGetLastError();
-    }
+    if (!a.cnt_merge) return hipErrorInvalidValue;
     auto t16 = [](int n) { return (unsigned)((n + kPT - 1) / kPT); };
     hipLaunchKernelGGL(proj16_kernel<true>, dim3(t16(N), t16(a.B)), dim3(1024), 0, s, a);
     const bool fast = with_fast_shape(a.hd, gqa, [&](auto hd, auto g) {

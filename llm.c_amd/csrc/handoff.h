@@ -5,10 +5,6 @@
 namespace moe {
 namespace {
 
-// Bound of a device-side spin wait; past it the waiter raises an error flag
-// and goes on, so every wave always ends.
-constexpr int kSpinLimit = 1 << 20;
-
 // Data handed between workgroups of one launch is written with
 // device-scope relaxed atomic stores, which are coherent across the XCDs'
 // separate L2s, and read with loads of the same (sc1) cache policy.  The

@@ -134,11 +134,11 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, stage,
-        counters, xn, rmsw, aq, ao, apart, agpart, ass, acnt, bw, bwork;
+        counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
                          &tile_expert, &perm, &h, &ys, &stage, &counters, &xn, &rmsw,
-                         &aq, &ao, &apart, &agpart, &ass, &acnt, &bw, &bwork};
+                         &aq, &ao, &apart, &acnt, &bw, &bwork};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -146,9 +146,7 @@ Workspace g_ws;
 
 // Device ints that are zero between launches (each launch's last workgroup
 // resets what it counted), so they are cleared only when allocated: [0] the
-// fused route+dispatch launch's completion counter, [kLayerErr] the flag a
-// bounded device-side wait raises when it gives up.
-constexpr int kLayerErr = 12;
+// fused route+dispatch launch's completion counter.
 constexpr int kMaxCounters = 64;
 int ensure_counters() {
     if (g_ws.counters.bytes >= sizeof(int) * kMaxCounters) return MOE_HIP_OK;
@@ -177,24 +175,6 @@ int scratch_of(hipStream_t s, char **out) {
     }
     *out = g_scratch[dev];
     return MOE_HIP_OK;
-}
-
-// The host drop-ins read the bounded-wait flag back with their outputs (a
-// set flag: a device-side wait gave up and the call's results are invalid).
-int g_host_flag = 0;
-int queue_flag_read() {
-    g_host_flag = 0;
-    if (g_ws.counters.bytes < sizeof(int) * kMaxCounters) return MOE_HIP_OK;
-    HIP_TRY(hipMemcpyAsync(&g_host_flag, g_ws.counters.as<int>() + kLayerErr, sizeof(int),
-                           hipMemcpyDeviceToHost, g_stream));
-    return MOE_HIP_OK;
-}
-// After the library stream has synchronised.
-int take_flag() {
-    if (!g_host_flag) return MOE_HIP_OK;
-    g_host_flag = 0;
-    HIP_TRY(hipMemset(g_ws.counters.as<int>() + kLayerErr, 0, sizeof(int)));
-    return set_err(MOE_HIP_ERR_HIP, "a bounded device-side wait gave up (results invalid)");
 }
 
 // Norm: with x_raw set, the rows to route (x, written here) are first
@@ -430,20 +410,6 @@ static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float
 // ---------------------------------------------------------------------------
 // Attention of the decode step (src/inference.c:252-308): weights in the
 // reference layout, the block's rms_attn scale and the RoPE tables.
-// Decode attention as one launch where the head shape allows (1), or as
-// separate launches (0, the default: measured faster at the 64-sequence,
-// 1024-context decode step, where the one launch cannot keep every chunk
-// resident while the projections run).
-static int g_attn_fused = 0;
-
-int moe_hip_set_attn_path(int fused) {
-    g_attn_fused = fused ? 1 : 0;
-    return MOE_HIP_OK;
-}
-
-int moe_hip_get_attn_path(void) { return g_attn_fused; }
-
-
 struct MoeHipAttn {
     int d = 0, nh = 0, nkv = 0, hd = 0, max_seq = 0;
     float *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
@@ -535,36 +501,24 @@ static int attn_decode(MoeHipAttn *a, float *x, int B, const int *pos, float *k_
     TRY(g_ws.aq.reserve(sizeof(float) * (size_t)B * qd));
     TRY(g_ws.ao.reserve(sizeof(float) * (size_t)B * qd));
     TRY(g_ws.apart.reserve(sizeof(float) * moe::attn_part_floats(B, a->nh, a->hd, a->max_seq)));
-    TRY(g_ws.agpart.reserve(sizeof(float) * moe::attn_gpart_floats(B, a->d, qd, kd)));
-    TRY(g_ws.ass.reserve(sizeof(float) * moe::attn_sspart_floats(B, a->d)));
-    // Tile and merge counters, then the one-launch sublayer's three: zero
-    // when allocated, reset by the last workgroup of each launch that uses them.
-    const moe::AttnCounters nc = moe::attn_counters(B, a->d, qd, kd, a->nkv);
-    const size_t cnt_bytes =
-        sizeof(int) * (size_t)(moe::attn_sync_ints() + nc.qkv + nc.wo + nc.merge);
+    // Merge counters: zero when allocated, reset by the merging workgroup.
+    const size_t cnt_bytes = sizeof(int) * (size_t)moe::attn_merge_counters(B, a->nkv);
     if (g_ws.acnt.bytes < cnt_bytes) {
         TRY(g_ws.acnt.reserve(cnt_bytes));
         HIP_TRY(hipMemsetAsync(g_ws.acnt.p, 0, g_ws.acnt.bytes, g_stream));
         HIP_TRY(hipStreamSynchronize(g_stream));
     }
-    TRY(ensure_counters());
-    const bool fused = g_attn_fused && moe::attn_fused_supported(a->hd, a->nh, a->nkv);
     moe::AttnArgs aa{};
     aa.x = x; aa.rms_w = a->rms; aa.eps = eps;
     aa.wq = a->wq; aa.wk = a->wk; aa.wv = a->wv; aa.wo = a->wo;
     aa.wqkv_p = a->wqkv_p; aa.wo_p = a->wo_p;
     aa.cos_t = a->cos_t; aa.sin_t = a->sin_t; aa.kc = k_cache; aa.vc = v_cache; aa.pos = pos;
     aa.q = g_ws.aq.as<float>(); aa.o = g_ws.ao.as<float>(); aa.part = g_ws.apart.as<float>();
-    aa.gpart = g_ws.agpart.as<float>(); aa.sspart = g_ws.ass.as<float>();
-    aa.sync = g_ws.acnt.as<int>();   // (first: 128-byte aligned flag lines)
-    aa.cnt_qkv = aa.sync + moe::attn_sync_ints(); aa.cnt_wo = aa.cnt_qkv + nc.qkv;
-    aa.cnt_merge = aa.cnt_wo + nc.wo;
-    aa.err = g_ws.counters.as<int>() + kLayerErr;
-    aa.nqkv_tiles = nc.qkv;
+    aa.cnt_merge = g_ws.acnt.as<int>();
     aa.B = B; aa.d = a->d; aa.nh = a->nh; aa.nkv = a->nkv; aa.hd = a->hd; aa.qd = qd; aa.kd = kd;
     aa.max_seq = a->max_seq;
     aa.scale = 1.0f / sqrtf((float)a->hd);
-    HIP_TRY(moe::launch_attn_decode(aa, fused, s));
+    HIP_TRY(moe::launch_attn_decode(aa, s));
     return MOE_HIP_OK;
 }
 
@@ -1137,9 +1091,8 @@ int moe_hip_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg
                            hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
                            hipMemcpyDeviceToHost, g_stream));
-    TRY(queue_flag_read());
     HIP_TRY(hipStreamSynchronize(g_stream));
-    return take_flag();
+    return MOE_HIP_OK;
 }
 
 void moe_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg, ForwardCache *cache,
@@ -1165,9 +1118,8 @@ int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x
     HIP_TRY(hipMemcpyAsync(dx, x, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
     TRY(moe_hip_forward_dev(L, dxn, n_rows, dx, nullptr, nullptr, 1, g_stream));
     HIP_TRY(hipMemcpyAsync(x, dx, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
-    TRY(queue_flag_read());
     HIP_TRY(hipStreamSynchronize(g_stream));
-    return take_flag();
+    return MOE_HIP_OK;
 }
 
 void moe_decode_step(const MoEWeights *w, const ModelConfig *cfg, const float *x_norm, float *x) {
@@ -1302,9 +1254,7 @@ int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,
                            hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
                            hipMemcpyDeviceToHost, g_stream));
-    TRY(queue_flag_read());
     HIP_TRY(hipStreamSynchronize(g_stream));
-    TRY(take_flag());
     // Residual 2 (src/transformer.c:767, mat_add_inplace).
     for (size_t i = 0; i < xd; ++i) x->data[i] = x->data[i] + fo.data[i];
     return MOE_HIP_OK;
@@ -1403,25 +1353,4 @@ int moe_hip_graph_destroy(void *graph) {
     delete G;
     if (g_live_graphs > 0) --g_live_graphs;
     return MOE_HIP_OK;
-}
-
-int moe_hip_device_check(void) {
-    TRY(ensure_init());
-    HIP_TRY(hipStreamSynchronize(g_stream));
-    // The flag of the workspace's counters and of this device's scratch.
-    int *flags[2] = {g_ws.counters.bytes >= sizeof(int) * kMaxCounters
-                         ? g_ws.counters.as<int>() + kLayerErr : nullptr,
-                     g_scratch[g_device] ? reinterpret_cast<int *>(g_scratch[g_device]) + kLayerErr
-                                         : nullptr};
-    bool raised = false;
-    for (int *f : flags) {
-        if (!f) continue;
-        int flag = 0;
-        HIP_TRY(hipMemcpy(&flag, f, sizeof(int), hipMemcpyDeviceToHost));
-        if (!flag) continue;
-        raised = true;
-        HIP_TRY(hipMemset(f, 0, sizeof(int)));
-    }
-    if (!raised) return MOE_HIP_OK;
-    return set_err(MOE_HIP_ERR_HIP, "a bounded device-side wait gave up (results invalid)");
 }

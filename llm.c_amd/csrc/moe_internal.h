@@ -156,15 +156,7 @@ struct AttnArgs {
     float *q;               // [B x qd] workspace
     float *o;               // [B x qd] workspace (merged head outputs)
     float *part;            // attn_part_floats(...) workspace: chunk partials
-    float *gpart;           // attn_gpart_floats(...) workspace: projection slices
-    float *sspart;          // attn_sspart_floats(...) workspace: slice sums of x^2
-    int *cnt_qkv, *cnt_wo, *cnt_merge;   // attn_counters(...) device ints, zero between launches
-    // One-launch sublayer: attn_sync_ints() device ints, zero between
-    // launches (counts and readiness flags); err raised if a bounded wait
-    // gave up; nqkv_tiles = the QKV tile count.
-    int *sync;
-    int *err;
-    int nqkv_tiles;
+    int *cnt_merge;         // attn_merge_counters(B, nkv) device ints, zero between launches
     int B, d, nh, nkv, hd, qd, kd, max_seq;
     float scale;            // 1 / sqrt(hd)
     // Optional copies packed in 16-column tiles ([N/16][K][16], see
@@ -172,17 +164,10 @@ struct AttnArgs {
     // block per tile.  wqkv_p holds [wq | wk | wv] (K = d), wo_p wo (K = qd).
     const float *wqkv_p = nullptr, *wo_p = nullptr;
 };
-struct AttnCounters {
-    int qkv, wo, merge;
-};
 size_t attn_part_floats(int B, int nh, int hd, int max_seq);
-size_t attn_gpart_floats(int B, int d, int qd, int kd);
-size_t attn_sspart_floats(int B, int d);
-AttnCounters attn_counters(int B, int d, int qd, int kd, int nkv);
-int attn_sync_ints();
-// Head shapes for which the one-launch sublayer exists.
-bool attn_fused_supported(int hd, int nh, int nkv);
-hipError_t launch_attn_decode(const AttnArgs &a, bool fused, hipStream_t s);
+// Merge counters: one per (sequence, kv head).
+inline int attn_merge_counters(int B, int nkv) { return B * nkv; }
+hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s);
 // Columns col0 .. col0 + N of a K-row matrix packed in 16-column tiles:
 // dst[((col0 + c) / 16) K 16 + k 16 + c % 16] = src[k N + c] (col0, N
 // multiples of 16).

@@ -78,13 +78,10 @@ SIGNATURES = {
     "moe_hip_set_timing": (C.c_int, [C.c_int]),
     "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
     "moe_hip_set_router_path": (C.c_int, [C.c_int]),
-    "moe_hip_set_attn_path": (C.c_int, [C.c_int]),
     "moe_hip_backward_dev": (C.c_int, [_P, _P, C.c_int, _P, C.c_float, _P, _P, _P, _P, _P, _P,
                                        C.c_int, _P]),
     "moe_hip_decode_block_dev": (C.c_int, [_P, _P, _P, _P, C.c_int, _P, _P, _P, C.c_float, _P,
                                            _P, _P]),
-    "moe_hip_get_attn_path": (C.c_int, []),
-    "moe_hip_device_check": (C.c_int, []),
     "moe_hip_timer_start": (C.c_int, []),
     "moe_hip_timer_stop": (C.c_int, [_F]),
     "moe_hip_timer_mark": (C.c_int, [C.c_int]),
@@ -419,29 +416,6 @@ def set_expert_path(mode):
     """0 automatic, 1 grouped GEMMs, 2 decode GEMVs (gate/up fused with a
     split-K down projection), 3 decode GEMVs as two launches."""
     check(lib().moe_hip_set_expert_path(int(mode)))
-
-
-def device_check():
-    """Raises if a bounded device-side wait gave up since the last check."""
-    check(lib().moe_hip_device_check())
-
-
-_attn_path = [None]
-
-
-def set_attn_path(fused):
-    """Decode attention as one launch (1, where the head shape allows) or as
-    separate launches (0)."""
-    check(lib().moe_hip_set_attn_path(int(fused)))
-    _attn_path[0] = int(bool(fused))
-
-
-def attn_path():
-    """The decode attention arrangement set last (the library default if
-    none was set)."""
-    if _attn_path[0] is None:
-        _attn_path[0] = int(lib().moe_hip_get_attn_path())
-    return _attn_path[0]
 
 
 def set_router_path(mode):

@@ -125,40 +125,35 @@ def test_rope_table_identity_at_position_zero():
 
 
 # ---------------------------------------------------------------- GPU
-def run_device(x, w, kc, vc, pos, c, s, nh=NH, nkv=NKV, hd=HD, fused=1):
+def run_device(x, w, kc, vc, pos, c, s, nh=NH, nkv=NKV, hd=HD):
     B, d = x.shape
     max_seq = kc.shape[1]
     at = mh.Attn(d, nh, nkv, hd, max_seq)
-    prev = mh.attn_path()
-    mh.set_attn_path(fused)
     try:
         at.load(w["wq"], w["wk"], w["wv"], w["wo"], w["rms"])
         at.set_rope(c, s)
         dx, dk, dv = (mh.DeviceArray.from_host(np.ascontiguousarray(a)) for a in (x, kc, vc))
         dp = mh.DeviceArray.from_host(np.ascontiguousarray(pos, np.int32))
         at.decode_dev(dx.ptr, B, dp.ptr, dk.ptr, dv.ptr, 1e-5)
-        mh.device_check()   # no bounded device-side wait gave up
         return dx.to_host(), dk.to_host(), dv.to_host()
     finally:
-        mh.set_attn_path(prev)
         at.close()
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fused", [1, 0], ids=["one-launch", "launches"])
 @pytest.mark.parametrize("shape", [(128, 8, 2, 16, 600), (512, 8, 2, 64, 1100),
                                    (256, 8, 1, 32, 300), (64, 4, 4, 16, 300),
                                    (64, 2, 1, 8, 300)],
                          ids=["small", "config4", "g8", "mha-generic", "hd8-unpacked"])
-def test_attn_decode_device(shape, fused):
+def test_attn_decode_device(shape):
     """Outputs within the layer tolerance of the oracle; the new k, v rows
     within it too, every other cache row bit-for-bit unchanged.  mha-generic
     (one query head per kv head) runs the generic chunk kernels."""
     d, nh, nkv, hd, max_seq = shape
     pos = [0, 1, 2, 127, 128, 129, 255, 256, max_seq - 1, 100, min(300, max_seq - 2), 37]
     x, w, kc, vc, pos, c, s = make_case(len(pos), max_seq, pos, 5, d, nh, nkv, hd)
-    print(f"[gpu-test] attention {shape} fused={fused}", flush=True)
-    xg, kg, vg = run_device(x, w, kc, vc, pos, c, s, nh, nkv, hd, fused)
+    print(f"[gpu-test] attention {shape}", flush=True)
+    xg, kg, vg = run_device(x, w, kc, vc, pos, c, s, nh, nkv, hd)
     xo, ko, vo = run_oracle(x, w, kc, vc, pos, c, s, nh, nkv, hd)
     rel = orc.rel_l2(xg, xo)
     mabs = float(np.abs(xg - xo).max())
@@ -172,8 +167,8 @@ def test_attn_decode_device(shape, fused):
 
 @pytest.mark.gpu
 def test_attn_decode_repeatable_and_batch_sizes():
-    """The one-launch path gives the same bits on a repeat (its counters are
-    back at zero) and at other batch sizes (ragged row tiles)."""
+    """The same bits on a repeat (the merge counters are back at zero) and at
+    other batch sizes (ragged row tiles)."""
     for B in (1, 33, 64, 70):
         pos = np.arange(B, dtype=np.int32) * 7 % 200
         x, w, kc, vc, pos, c, s = make_case(B, 200, pos, 8)
@@ -186,12 +181,11 @@ def test_attn_decode_repeatable_and_batch_sizes():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fused", [1, 0], ids=["one-launch", "launches"])
-def test_attn_decode_position_out_of_range(fused):
+def test_attn_decode_position_out_of_range():
     """A position outside [0, max_seq) leaves that sequence untouched."""
     x, w, kc, vc, _, c, s = make_case(3, 64, [0, 0, 0], 6)
     pos = np.array([5, 64, -1], np.int32)
-    xg, kg, vg = run_device(x, w, kc, vc, pos, c, s, fused=fused)
+    xg, kg, vg = run_device(x, w, kc, vc, pos, c, s)
     for b in (1, 2):
         assert np.array_equal(xg[b], x[b])
         assert np.array_equal(kg[b], kc[b]) and np.array_equal(vg[b], vc[b])
@@ -200,8 +194,7 @@ def test_attn_decode_position_out_of_range(fused):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fused", [1, 0], ids=["one-launch", "launches"])
-def test_decode_block_device(fused):
+def test_decode_block_device():
     """moe_hip_decode_block_dev: x += Attn(rms_norm(x)), then x += MoE(
     rms_norm(x; rms_ffn)).  The FFN's normalised rows (made by the MoE
     router's first step) are bit-identical to rms_norm of the attention
@@ -216,14 +209,12 @@ def test_decode_block_device(fused):
     pos[3] = max_seq          # out of range: attention skipped, FFN still applied
     x, w, kc, vc, pos, cs, sn = make_case(B, max_seq, pos, 12, d, nh, nkv, hd)
     rms_ffn = (1.0 + 0.1 * np.random.default_rng(13).standard_normal(d)).astype(np.float32)
-    x_attn, _, _ = run_device(x, w, kc, vc, pos, cs, sn, nh, nkv, hd, fused)
+    x_attn, _, _ = run_device(x, w, kc, vc, pos, cs, sn, nh, nkv, hd)
 
     layer = mh.Layer(d, F, E, k)
     layer.fill_synthetic(11, c["std_router"], c["std_expert"])
     hw = host_layer(d, F, E, k, 11, c["std_router"], c["std_expert"])
     at = mh.Attn(d, nh, nkv, hd, max_seq)
-    prev = mh.attn_path()
-    mh.set_attn_path(fused)
     try:
         at.load(w["wq"], w["wk"], w["wv"], w["wo"], w["rms"])
         at.set_rope(cs, sn)
@@ -232,17 +223,15 @@ def test_decode_block_device(fused):
         dw = mh.DeviceArray.from_host(rms_ffn)
         dxn = mh.DeviceArray((B, d))
         dids = mh.DeviceArray((B, k), np.int32)
-        print(f"[gpu-test] decode block fused={fused} B={B}", flush=True)
+        print(f"[gpu-test] decode block B={B}", flush=True)
         at.decode_block_dev(layer, dw.ptr, dx.ptr, B, dp.ptr, dk.ptr, dv.ptr, 1e-5, dxn.ptr,
                             dids.ptr)
-        mh.device_check()
         xn_ref = orc.rms_norm(x_attn, rms_ffn, 1e-5)
         assert np.array_equal(bits(dxn.to_host()), bits(xn_ref))
         o_ref, _, i_ref = orc.moe_forward(xn_ref, hw, nthreads=16)
         assert np.array_equal(dids.to_host(), i_ref)
         assert_close(dx.to_host(), x_attn + o_ref, "decode block")
     finally:
-        mh.set_attn_path(prev)
         at.close()
         layer.close()
 

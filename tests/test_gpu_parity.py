@@ -448,7 +448,6 @@ def test_graph_replay(path):
             for i in ids:
                 i.zero()
             g.launch()
-            mh.device_check()
             assert np.array_equal(bits(out.to_host()), bits(ref)), f"replay {rep}: output differs"
             for i, r in zip(ids, ref_ids):
                 assert np.array_equal(i.to_host(), r), f"replay {rep}: expert ids differ"
@@ -577,7 +576,6 @@ def test_forced_expert_paths(name, T, d, F, E, k, path):
     mh.set_expert_path(path)
     try:
         out, probs, ids = mh.moe_forward(x, hw)
-        mh.device_check()
     finally:
         mh.set_expert_path(0)
     o_ref, p_ref, i_ref = orc.moe_forward(x, hw)
