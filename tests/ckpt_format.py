@@ -11,6 +11,7 @@ block is MoE when n_experts > 1, src/transformer.c:437); then rms_final [d]
 and lm_head [d x vocab].  fp32, row-major, no padding.
 """
 import struct
+import zlib
 
 import numpy as np
 
@@ -74,3 +75,25 @@ def write(path, cfg, seed=0):
             arrays[name] = a
             f.write(np.ascontiguousarray(a).tobytes())
     return arrays
+
+
+# The small MoE model whose checkpoint tests/golden/ckpt_moe_ref.bin was
+# written by the reference's own model_save (tests/golden/make_moe_ckpt.py).
+REF_MOE_CFG = dict(vocab_size=16, max_seq_len=8, d_model=64, n_layers=2, n_heads=2,
+                   n_kv_heads=1, head_dim=32, window_size=0, ffn_hidden=32, n_experts=3,
+                   top_k_experts=2, rms_norm_eps=1e-5, rope_theta=10000.0)
+
+
+def named_arrays(cfg, seed):
+    """{name: array} for every tensor of cfg, each from its own stream of
+    numpy's generator (seed, crc32 of the name), so a tensor's values do not
+    depend on where any file layout puts it.  Norm scales N(1, 0.1), the rest
+    N(0, 1/sqrt(d))."""
+    out = {}
+    for name, shape in layout(cfg):
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        if name.split(".")[-1].startswith("rms"):
+            out[name] = (1.0 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
+        else:
+            out[name] = (rng.standard_normal(shape) / np.sqrt(cfg["d_model"])).astype(np.float32)
+    return out

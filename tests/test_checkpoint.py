@@ -1,7 +1,9 @@
 """Checkpoint format (model_save, src/transformer.c:573-616): the layout
-restated in tests/ckpt_format.py against a checkpoint the reference ships,
-and the library's loader (moe_hip_model_load) against synthetic MoE and
-dense checkpoints written in that layout."""
+restated in tests/ckpt_format.py against a dense checkpoint the reference
+ships and a MoE checkpoint the reference's own model_save wrote
+(tests/golden/ckpt_moe_ref.bin), and the library's loader
+(moe_hip_model_load) against that file and synthetic MoE and dense
+checkpoints written in the restated layout."""
 import os
 
 import numpy as np
@@ -63,6 +65,51 @@ def test_writer_roundtrip(tmp_path):
     for name, (at, shape) in offs.items():
         got = np.frombuffer(blob, np.float32, count=int(np.prod(shape)), offset=at).reshape(shape)
         assert np.array_equal(got, arrays[name]), name
+
+
+REF_MOE_CKPT = os.path.join(GOLDEN, "ckpt_moe_ref.bin")
+
+
+def test_layout_matches_reference_written_moe_checkpoint():
+    """tests/golden/ckpt_moe_ref.bin was written by the reference's own
+    model_save (tests/golden/make_moe_ckpt.py) from named tensors: its
+    config, its size and every section (each block's router and every
+    expert's gate, up and down matrices included) sit where the restated
+    layout puts them, holding the tensor of that name."""
+    blob = open(REF_MOE_CKPT, "rb").read()
+    cfg = cf.read_config(blob)
+    assert cfg == {**cf.REF_MOE_CFG, "rms_norm_eps": np.float32(1e-5).item()}
+    offs, total = cf.offsets(cf.REF_MOE_CFG)
+    assert total == len(blob)
+    arrays = cf.named_arrays(cf.REF_MOE_CFG, 11)
+    for name, (at, shape) in offs.items():
+        got = np.frombuffer(blob, np.float32, count=int(np.prod(shape)), offset=at).reshape(shape)
+        assert np.array_equal(got, arrays[name]), name
+
+
+@pytest.mark.gpu
+def test_model_load_reference_written_moe_checkpoint():
+    """moe_hip_model_load on the checkpoint the reference's model_save wrote:
+    every block's router, experts and rms_ffn come back bit for bit."""
+    cfg = cf.REF_MOE_CFG
+    arrays = cf.named_arrays(cfg, 11)
+    m = mh.Model(REF_MOE_CKPT)
+    try:
+        assert m.config()["n_experts"] == cfg["n_experts"]
+        d, E = cfg["d_model"], cfg["n_experts"]
+        for l in range(cfg["n_layers"]):
+            L = m.layer(l)
+            assert np.array_equal(bits(L.get_router()), bits(arrays[f"{l}.W_router"]))
+            for e in range(E):
+                g, u, dn = L.get_expert(e)
+                assert np.array_equal(bits(g), bits(arrays[f"{l}.{e}.W_gate"]))
+                assert np.array_equal(bits(u), bits(arrays[f"{l}.{e}.W_up"]))
+                assert np.array_equal(bits(dn), bits(arrays[f"{l}.{e}.W_down"]))
+            rw = mh.DeviceArray((d,))
+            mh.check(mh.lib().moe_hip_memcpy(rw.ptr, m.rms_ffn_ptr(l), 4 * d, 3))
+            assert np.array_equal(bits(rw.to_host()), bits(arrays[f"{l}.rms_ffn"]))
+    finally:
+        m.close()
 
 
 # ---------------------------------------------------------------- the loader (GPU)
