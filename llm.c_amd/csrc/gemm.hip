@@ -452,32 +452,48 @@ __global__ __launch_bounds__(256) void zero_ints_kernel(int *p, int n) {
 
 }  // namespace
 
+// Compute units of the current device (cached; 256 on MI355X).
+static int device_cus() {
+    static int cus = 0;
+    if (cus <= 0) {
+        int dev = 0, n = 0;
+        cus = hipGetDevice(&dev) == hipSuccess &&
+                      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                          hipSuccess && n > 0
+                  ? n : 256;
+    }
+    return cus;
+}
+
 GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split) {
-    // Waves in flight for tile width bn (bn / 32 waves per workgroup) and
-    // split ks; aim for ~4 per SIMD.  Wider tiles reuse each loaded tile
-    // across more waves, so they shrink only to 128 columns, and only tiny
-    // grids go to 64; splits (whose partials the combine adds) stop at 4.
-    constexpr size_t kTarget = 1024;
-    auto waves = [&](int bn, int ks) { return (size_t)max_mtiles * (N / bn) * ks * (bn / 32); };
     GemmPlan p{0, 1};
     if (N % 256 == 0) p.bn = 256;
     else if (N % 128 == 0) p.bn = 128;
     else if (N % 64 == 0) p.bn = 64;
     else return p;
-    while (p.bn > 128 && waves(p.bn, 1) < kTarget) p.bn /= 2;
-    auto split = [&](int bn) {
-        int ks = 1;
-        if (allow_split)
-            while (ks < 4 && waves(bn, ks) < kTarget && K % (2 * ks * KT) == 0 &&
-                   K / (2 * ks) >= 128)
-                ks *= 2;
-        return ks;
-    };
-    p.ksplit = split(p.bn);
-    if (p.bn > 64 && waves(p.bn, p.ksplit) < kTarget / 4 && N % 64 == 0) {
-        p.bn = 64;
-        p.ksplit = split(64);
+    if (allow_split) {
+        // Down projection: the widest tile, and the reduction split (its
+        // partials are added by the combine) until the workgroups cover the
+        // CUs once: blocks of 256 columns hold a CU each, narrower ones share
+        // it 2 or 3 ways.  A split keeps >= 512 reduction elements (16 LDS
+        // slices) unless the grid is tiny.  Measured at T=4096, d=512,
+        // F=2048, E=8: no split 0.568 ms per layer, 2 splits 0.489, 4 0.501.
+        const long slots = (long)device_cus() * (p.bn == 256 ? 1 : p.bn == 128 ? 2 : 3);
+        const long blocks = (long)max_mtiles * (N / p.bn);
+        const int min_k = blocks * 4 < slots ? 128 : 512;
+        while (p.ksplit < 4 && blocks * p.ksplit < slots && K % (2 * p.ksplit * KT) == 0 &&
+               K / (2 * p.ksplit) >= min_k)
+            p.ksplit *= 2;
+        return p;
     }
+    // Without a split: waves in flight for tile width bn (bn / 32 waves per
+    // workgroup); aim for ~4 per SIMD.  Wider tiles reuse each loaded tile
+    // across more waves, so they shrink only to 128 columns, and only tiny
+    // grids go to 64.
+    constexpr size_t kTarget = 1024;
+    auto waves = [&](int bn) { return (size_t)max_mtiles * (N / bn) * (bn / 32); };
+    while (p.bn > 128 && waves(p.bn) < kTarget) p.bn /= 2;
+    if (p.bn > 64 && waves(p.bn) < kTarget / 4 && N % 64 == 0) p.bn = 64;
     return p;
 }
 
