@@ -325,8 +325,11 @@ int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed,
 int moe_hip_set_expert_path(int mode);
 
 /* Routing kernel selection: 0 = automatic, 1 = token x expert tiles,
- * 2 = 16-token row blocks with every expert in one workgroup.  Process-wide;
- * both give the same bits. */
+ * 2 = 16-token row blocks with every expert in one workgroup, in their own
+ * launch.  Automatic routes a decode step of up to 64 tokens (up to 16
+ * experts, d_model 256 or 512, finite router weights) inside the fused
+ * expert kernel, with the row blocks' arithmetic.  Process-wide; every
+ * choice gives the same bits. */
 int moe_hip_set_router_path(int mode);
 
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,

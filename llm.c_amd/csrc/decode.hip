@@ -23,22 +23,6 @@
 namespace moe {
 namespace {
 
-// Item (expert e, feature block fb) of workgroup b.  With E a multiple of 8
-// an expert's items are the workgroups b = x + 8 j of one x, i.e. (as the
-// hardware hands workgroups to the 8 XCDs in turn) all on one XCD, which
-// shares the expert's staged activation rows in that XCD's L2 (measured 1.1-
-// 1.6 us faster per 64-token, E = 16 layer than experts spread over XCDs).
-__device__ inline void item_of(int b, int E, int nfb, int &e, int &fb) {
-    if (E % 8 == 0) {
-        const int x = b % 8, j = b / 8;
-        e = x + 8 * (j / nfb);
-        fb = j % nfb;
-    } else {
-        e = b / nfb;
-        fb = b % nfb;
-    }
-}
-
 // grid = E x (F/(16*NW)): one gate/up item of NW waves per workgroup (NW =
 // 8: one workgroup per CU, two waves per SIMD).  The fused items store their
 // split-K partials write-through (coherent stores): none are left dirty in an
@@ -89,9 +73,9 @@ __global__ __launch_bounds__(256) void decode_down_kernel(DecodeArgs a) {
             WAIT_VMCNT(2 * Unroll<1>::kU);   // the rows, not the weights behind them
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
             dma_landed(hs);
-            const float *as = hs + j * kLd + 4 * h;
-            if (rows > 16) gemv_loop<1, 2>(ws, ow + 64 * k0, 0, as, kc / 16, acc, wa, wb);
-            else           gemv_loop<1, 1>(ws, ow + 64 * k0, 0, as, kc / 16, acc, wa, wb);
+            const float *as0 = hs + j * kLd + 4 * h, *as1 = as0 + 16 * kLd;
+            if (rows > 16) gemv_loop<1, 2>(ws, ow + 64 * k0, 0, as0, as1, kc / 16, acc, wa, wb);
+            else           gemv_loop<1, 1>(ws, ow + 64 * k0, 0, as0, as1, kc / 16, acc, wa, wb);
         }
 #pragma unroll
         for (int b = 0; b < 2; ++b)

@@ -170,14 +170,16 @@ __device__ inline void gemv_prime(const WSrc &s, int o0, int o1, int nq, WGroup<
     wload<NB>(s, ob, group_step<NB>(1, g0, ng), nq - 1, wb);
 }
 
+// as0 / as1: the lane's activation row of 16-row block 0 / 1 (as1 is read
+// only when RB == 2).
 template <int NB, int RB>
-__device__ inline void gemv_group(const float *as, int q, const WGroup<NB> &w,
+__device__ inline void gemv_group(const float *as0, const float *as1, int q, const WGroup<NB> &w,
                                   floatx4 (&acc)[2][NB]) {
 #pragma unroll
     for (int u = 0; u < Unroll<NB>::kU; ++u) {
-        floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 16 * (q + u));
+        floatx4 a0 = *reinterpret_cast<const floatx4 *>(as0 + 16 * (q + u));
         floatx4 a1;
-        if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as + 16 * kLd + 16 * (q + u));
+        if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as1 + 16 * (q + u));
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -215,7 +217,8 @@ struct DownHead {
 // the stream (requires nq = kU * ng).
 // HEAD: also issues the first two down groups into wa and wb (NB = 2 only).
 template <int NB, int RB, bool HEAD = false, int NW = 4>
-__device__ inline void gemv_loop(const WSrc &s, int o0, int o1, const float *as, int nq,
+__device__ inline void gemv_loop(const WSrc &s, int o0, int o1, const float *as0, const float *as1,
+                                 int nq,
                                  floatx4 (&acc)[2][NB], WGroup<NB> &wa, WGroup<NB> &wb,
                                  const DownHead<NW> &dh = DownHead<NW>{}, int g0 = 0) {
     constexpr int kU = Unroll<NB>::kU;
@@ -233,44 +236,44 @@ __device__ inline void gemv_loop(const WSrc &s, int o0, int o1, const float *as,
     // (Scheduling barriers keep each group's loads right after the MFMAs
     // that free its registers.)
     for (; g + 4 <= ng; g += 2) {
-        gemv_group<NB, RB>(as, qg(g), wa, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g), wa, acc);
         __builtin_amdgcn_sched_barrier(0);
         wload<NB, false>(s, ob, qg(g + 2), nq - 1, wa);
         __builtin_amdgcn_sched_barrier(0);
-        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g + 1), wb, acc);
         __builtin_amdgcn_sched_barrier(0);
         wload<NB, false>(s, ob, qg(g + 3), nq - 1, wb);
         __builtin_amdgcn_sched_barrier(0);
     }
     const int left = ng - g;   // 0 .. 3 groups, the first two already loaded
     if (left == 3) {
-        gemv_group<NB, RB>(as, qg(g), wa, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g), wa, acc);
         wload<NB>(s, ob, qg(g + 2), nq - 1, wa);
-        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
-        gemv_group<NB, RB>(as, qg(g + 2), wa, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g + 1), wb, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g + 2), wa, acc);
     } else if (left == 2 && nq == kU * ng) {
         // (the common case: each down group goes out as its registers free)
-        gemv_group<NB, RB>(as, qg(g), wa, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g), wa, acc);
         __builtin_amdgcn_sched_barrier(0);
         head(0, wa);
         __builtin_amdgcn_sched_barrier(0);
-        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g + 1), wb, acc);
         __builtin_amdgcn_sched_barrier(0);
         head(1, wb);
         return;
     } else if (left == 2) {
-        gemv_group<NB, RB>(as, qg(g), wa, acc);
-        gemv_group<NB, RB>(as, qg(g + 1), wb, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g), wa, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g + 1), wb, acc);
     } else if (left == 1) {
-        gemv_group<NB, RB>(as, qg(g), wa, acc);
+        gemv_group<NB, RB>(as0, as1, qg(g), wa, acc);
     }
     for (int q = kU * ng; q < nq; ++q) {
         floatx4 w[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) w[b] = ldw(s, ob[b] + kUnitBytes * q);
-        floatx4 a0 = *reinterpret_cast<const floatx4 *>(as + 16 * q);
+        floatx4 a0 = *reinterpret_cast<const floatx4 *>(as0 + 16 * q);
         floatx4 a1;
-        if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as + 16 * kLd + 16 * q);
+        if (RB == 2) a1 = *reinterpret_cast<const floatx4 *>(as1 + 16 * q);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -326,6 +329,141 @@ __device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int
     }
 }
 
+// Item (expert e, feature block fb) of workgroup b.  With E a multiple of 8
+// an expert's items are the workgroups b = x + 8 j of one x, i.e. (as the
+// hardware hands workgroups to the 8 XCDs in turn) all on one XCD, which
+// shares the expert's staged activation rows in that XCD's L2 (measured 1.1-
+// 1.6 us faster per 64-token, E = 16 layer than experts spread over XCDs).
+__device__ inline void item_of(int b, int E, int nfb, int &e, int &fb) {
+    if (E % 8 == 0) {
+        const int x = b % 8, j = b / 8;
+        e = x + 8 * (j / nfb);
+        fb = j % nfb;
+    } else {
+        e = b / nfb;
+        fb = b % nfb;
+    }
+}
+
+// Where one gate/up item of NW waves reads its weights: expert e, features
+// 16*NW*fb .. + 16*NW - 1 (16 per wave).  (e, fb and the wave index are
+// uniform: weight addresses keep their common part in SGPRs, the lane's
+// 16-byte column in lo.)
+template <int NW>
+struct ItemGeo {
+    int lane, wave, j, h, f;
+    WSrc gs, ds;
+    int og, ou;           // gate / up rows of the wave's feature block
+    int fq, nbw, last, ngd, od;
+    int spread;
+    DownHead<NW> dh;
+    // Rotation of a gate/up chunk of nq steps: each wave starts its streams
+    // at its own group (chunks of whole groups only), spreading the
+    // concurrent reads over the memory system.
+    __device__ int rot_of(int nq) const {
+        const int ng = nq / Unroll<2>::kU;
+        return nq % Unroll<2>::kU == 0 && ng >= 2 ? (5 * spread) % ng : 0;
+    }
+};
+
+template <bool FUSED, int NW>
+__device__ __forceinline__ ItemGeo<NW> item_geo(const DecodeArgs &a, int e, int fb) {
+    static_assert(NW == 4 || NW == 8, "an item is 4 or 8 waves of 16 features");
+    ItemGeo<NW> g;
+    e = __builtin_amdgcn_readfirstlane(e);
+    fb = __builtin_amdgcn_readfirstlane(fb);
+    g.lane = threadIdx.x & 63;
+    g.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const unsigned lo = 16u * g.lane;
+    g.j = g.lane & 15;
+    g.h = g.lane >> 4;
+    const int m = NW * fb + g.wave;                 // this wave's 16-feature block
+    g.f = 16 * m + g.j;
+    // Gate rows of feature block m form unit row nbg (packed rows interleave
+    // 32 gate and 32 up rows); up rows are 2 unit rows further.
+    const int nbg = 4 * (m >> 1) + (m & 1);
+    g.gs = wsrc(a.w + (size_t)e * 2 * a.F * a.d, (size_t)2 * a.F * a.d, lo);
+    g.og = kUnitBytes * nbg * (a.d / 16);
+    g.ou = g.og + kUnitBytes * 2 * (a.d / 16);
+    // Down weights (FUSED): wave w's 16-column blocks w*nbw .. of the
+    // expert's W_down, this item's NW feature units.
+    g.fq = a.F / 16;
+    g.nbw = a.d / (16 * NW);                        // 16-column blocks per wave
+    g.last = NW * g.nbw - 1;
+    g.ngd = (NW * g.nbw + 7) / 8;
+    g.ds = wsrc(FUSED ? a.w2 + (size_t)e * a.d * a.F : a.w, (size_t)a.d * a.F, lo);
+    g.od = kUnitBytes * ((g.wave * g.nbw) * g.fq + NW * fb);
+    g.spread = NW * (e * (a.F / (16 * NW)) + fb) + g.wave;
+    g.dh = DownHead<NW>{g.ds, g.od, g.fq, g.last, g.ngd >= 2 ? (3 * g.spread) % g.ngd : 0, g.ngd};
+    return g;
+}
+
+// The fused item's down projection for one pass of rows list[r0 ..
+// r0 + rows): the gate/up accumulators become the H block [rows][16 * NW] in
+// LDS at hs, which multiplies the matching rows of W_down; the split-K
+// partial goes to Yp[fb][a][0 .. d) by assignment a (CS: write-through
+// stores).  wa / wb arrive holding the down stream's first two groups.
+template <int NW, bool CS>
+__device__ __forceinline__ void fused_down_pass(const DecodeArgs &a, const ItemGeo<NW> &g, int fb,
+                                       const floatx4 (&acc)[2][2], int rows, const int *list,
+                                       int r0, float *hs, WGroup<2> &wa, WGroup<2> &wb) {
+    const int j = g.j, h = g.h;
+    // The gate/up weight registers carry the down stream.
+    floatx4 (&da)[8] = reinterpret_cast<floatx4 (&)[8]>(wa);
+    floatx4 (&db)[8] = reinterpret_cast<floatx4 (&)[8]>(wb);
+    // (every wave is past the activation rows, which hs may overlay)
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            hs[(b * 16 + 4 * h + r) * hld<NW>() + g.wave * 16 + j] =
+                swiglu_fast(acc[b][0][r], acc[b][1][r]);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    const float *as = hs + j * hld<NW>() + 4 * h;
+    // Partial offsets fit in 32 bits: the host caps the partial buffer.
+    int yoff[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = b * 16 + 4 * h + r;
+            yoff[b][r] = row < rows ? (fb * a.nslots + list[r0 + row]) * a.d : -1;
+        }
+    const int cb0 = g.wave * g.nbw, nbw = g.nbw, ngd = g.ngd;
+    const DownHead<NW> &dh = g.dh;
+    auto run = [&](auto rb) {
+        constexpr int RB = decltype(rb)::value;
+        int q = 0;
+        for (; q + 4 <= ngd; q += 2) {
+            dgroup<RB, NW, CS>(da, as, dh.rot(q), nbw, cb0, yoff, a.out, j);
+            __builtin_amdgcn_sched_barrier(0);
+            dload<NW>(g.ds, g.od, g.fq, dh.rot(q + 2), g.last, da);
+            __builtin_amdgcn_sched_barrier(0);
+            dgroup<RB, NW, CS>(db, as, dh.rot(q + 1), nbw, cb0, yoff, a.out, j);
+            __builtin_amdgcn_sched_barrier(0);
+            dload<NW>(g.ds, g.od, g.fq, dh.rot(q + 3), g.last, db);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const int left = ngd - q;
+        if (left == 3) {
+            dgroup<RB, NW, CS>(da, as, dh.rot(q), nbw, cb0, yoff, a.out, j);
+            dload<NW>(g.ds, g.od, g.fq, dh.rot(q + 2), g.last, da);
+            dgroup<RB, NW, CS>(db, as, dh.rot(q + 1), nbw, cb0, yoff, a.out, j);
+            dgroup<RB, NW, CS>(da, as, dh.rot(q + 2), nbw, cb0, yoff, a.out, j);
+        } else if (left == 2) {
+            dgroup<RB, NW, CS>(da, as, dh.rot(q), nbw, cb0, yoff, a.out, j);
+            dgroup<RB, NW, CS>(db, as, dh.rot(q + 1), nbw, cb0, yoff, a.out, j);
+        } else if (left == 1) {
+            dgroup<RB, NW, CS>(da, as, dh.rot(q), nbw, cb0, yoff, a.out, j);
+        }
+    };
+    if (rows > 16) run(std::integral_constant<int, 2>{});
+    else           run(std::integral_constant<int, 1>{});
+}
+
 // One gate/up item of NW waves: expert e, features 16*NW*fb .. + 16*NW - 1
 // (16 per wave).  FUSED = false: writes H [n x F] by assignment.  FUSED =
 // true: keeps the item's H columns in LDS and multiplies them by the matching
@@ -335,45 +473,14 @@ __device__ inline void dgroup(const floatx4 (&w)[8], const float *as, int g, int
 // coherent (write-through) stores.
 template <bool FUSED, int NW = 4, bool CS = false>
 __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *wcnt) {
-    static_assert(NW == 4 || NW == 8, "an item is 4 or 8 waves of 16 features");
     int *list = reinterpret_cast<int *>(xs + kRows * kLd);
     int *tok = list + a.nslots;
-    // (e, fb and the wave index are uniform: weight addresses keep their
-    // common part in SGPRs, the lane's 16-byte column in lo)
-    e = __builtin_amdgcn_readfirstlane(e);
-    fb = __builtin_amdgcn_readfirstlane(fb);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const unsigned lo = 16u * lane;
-    const int j = lane & 15, h = lane >> 4;
-    const int m = NW * fb + wave;                 // this wave's 16-feature block
-    const int f = 16 * m + j;
-    // Gate rows of feature block m form unit row nbg (packed rows interleave
-    // 32 gate and 32 up rows); up rows are 2 unit rows further.
-    const int nbg = 4 * (m >> 1) + (m & 1);
-    const WSrc gs = wsrc(a.w + (size_t)e * 2 * a.F * a.d, (size_t)2 * a.F * a.d, lo);
-    const int og = kUnitBytes * nbg * (a.d / 16);
-    const int ou = og + kUnitBytes * 2 * (a.d / 16);
+    const ItemGeo<NW> g = item_geo<FUSED, NW>(a, e, fb);
+    const int j = g.j, h = g.h;
 
     // The slot list first (its loads are not queued behind weight loads),
     // then per chunk the activation rows (DMA), the first two weight groups
     // and a wait for the rows only.
-    // Down weights (FUSED): wave w's 16-column blocks w*nbw .. of the
-    // expert's W_down, this item's NW feature units.
-    const int fq = a.F / 16;
-    const int nbw = a.d / (16 * NW);               // 16-column blocks per wave
-    const int last = NW * nbw - 1;
-    const int ngd = (NW * nbw + 7) / 8;
-    const WSrc ds = wsrc(FUSED ? a.w2 + (size_t)e * a.d * a.F : a.w, (size_t)a.d * a.F, lo);
-    const int od = kUnitBytes * ((wave * nbw) * fq + NW * fb);
-    // Each wave starts its streams at its own group (gate/up: chunks of whole
-    // groups only), spreading the concurrent reads over the memory system.
-    const int spread = NW * (e * (a.F / (16 * NW)) + fb) + wave;
-    auto rot_of = [&](int nq) {   // rotation of a gate/up chunk of nq steps
-        const int ng = nq / Unroll<2>::kU;
-        return nq % Unroll<2>::kU == 0 && ng >= 2 ? (5 * spread) % ng : 0;
-    };
-    const DownHead<NW> dh{ds, od, fq, last, ngd >= 2 ? (3 * spread) % ngd : 0, ngd};
     WGroup<2> wa, wb;
     const int id0 = (int)threadIdx.x < a.nslots ? a.ids[threadIdx.x] : -1;
     const int cnt = expert_slots<NW>(a.ids, a.nslots, e, id0, a.topk, list, tok, wcnt);
@@ -384,7 +491,7 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int g = 0; g < 2; ++g) acc[b][g] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int q = 0; q < 2; ++q) acc[b][q] = floatx4{0.f, 0.f, 0.f, 0.f};
         for (int k0 = 0; k0 < a.d; k0 += kChunk) {
             const int kc = min(kChunk, a.d - k0);
             __syncthreads();   // every wave is done with the previous rows
@@ -393,23 +500,23 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
             // weight loads, and other waves read those rows after the barrier:
             // keep the compiler from moving weight loads above the DMA.
             __builtin_amdgcn_sched_barrier(0);
-            gemv_prime<2>(gs, og + 64 * k0, ou + 64 * k0, kc / 16, wa, wb, rot_of(kc / 16));
+            const int g0 = g.rot_of(kc / 16);
+            gemv_prime<2>(g.gs, g.og + 64 * k0, g.ou + 64 * k0, kc / 16, wa, wb, g0);
             WAIT_VMCNT(4 * Unroll<2>::kU);   // the rows, not the weights behind them
             __builtin_amdgcn_s_barrier();   // (a fence here would wait for the weights too)
             dma_landed(xs);
-            const float *as = xs + j * kLd + 4 * h;
-            const int go = og + 64 * k0, uo = ou + 64 * k0;   // (16 floats per K column)
-            const int g0 = rot_of(kc / 16);
+            const float *as0 = xs + j * kLd + 4 * h, *as1 = as0 + 16 * kLd;
+            const int go = g.og + 64 * k0, uo = g.ou + 64 * k0;   // (16 floats per K column)
             if (FUSED && k0 + kc == a.d) {   // last chunk: hand over to the down stream
                 if (rows > 16)
-                    gemv_loop<2, 2, true, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                    gemv_loop<2, 2, true, NW>(g.gs, go, uo, as0, as1, kc / 16, acc, wa, wb, g.dh, g0);
                 else
-                    gemv_loop<2, 1, true, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                    gemv_loop<2, 1, true, NW>(g.gs, go, uo, as0, as1, kc / 16, acc, wa, wb, g.dh, g0);
             } else {
                 if (rows > 16)
-                    gemv_loop<2, 2, false, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                    gemv_loop<2, 2, false, NW>(g.gs, go, uo, as0, as1, kc / 16, acc, wa, wb, g.dh, g0);
                 else
-                    gemv_loop<2, 1, false, NW>(gs, go, uo, as, kc / 16, acc, wa, wb, dh, g0);
+                    gemv_loop<2, 1, false, NW>(g.gs, go, uo, as0, as1, kc / 16, acc, wa, wb, g.dh, g0);
             }
         }
         // 16x16 accumulator: lane holds rows 4*(lane/16) + r, column lane%16.
@@ -420,68 +527,13 @@ __device__ void gateup_item(const DecodeArgs &a, int e, int fb, float *xs, int *
                 for (int r = 0; r < 4; ++r) {
                     const int row = b * 16 + 4 * h + r;
                     if (row < rows)
-                        a.out[(size_t)list[r0 + row] * a.F + f] =
+                        a.out[(size_t)list[r0 + row] * a.F + g.f] =
                             swiglu_fast(acc[b][0][r], acc[b][1][r]);
                 }
             continue;
         }
-        // The gate/up weight registers carry the down stream, whose first
-        // two groups the last chunk's loop issued (the next pass, if any,
-        // primes them again).
-        floatx4 (&da)[8] = reinterpret_cast<floatx4 (&)[8]>(wa);
-        floatx4 (&db)[8] = reinterpret_cast<floatx4 (&)[8]>(wb);
-        // H block [rows][16 * NW] in LDS over the x rows (every wave is past
-        // them).
-        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0) only
-        __builtin_amdgcn_s_barrier();
-        float *hs = xs;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                hs[(b * 16 + 4 * h + r) * hld<NW>() + wave * 16 + j] =
-                    swiglu_fast(acc[b][0][r], acc[b][1][r]);
-        __builtin_amdgcn_s_waitcnt(0xC07F);
-        __builtin_amdgcn_s_barrier();
-        const float *as = hs + j * hld<NW>() + 4 * h;
-        // Partial offsets fit in 32 bits: the host caps the partial buffer.
-        int yoff[2][4];
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = b * 16 + 4 * h + r;
-                yoff[b][r] = row < rows ? (fb * a.nslots + list[r0 + row]) * a.d : -1;
-            }
-        const int cb0 = wave * nbw;
-        auto run = [&](auto rb) {
-            constexpr int RB = decltype(rb)::value;
-            int g = 0;
-            for (; g + 4 <= ngd; g += 2) {
-                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
-                __builtin_amdgcn_sched_barrier(0);
-                dload<NW>(ds, od, fq, dh.rot(g + 2), last, da);
-                __builtin_amdgcn_sched_barrier(0);
-                dgroup<RB, NW, CS>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
-                __builtin_amdgcn_sched_barrier(0);
-                dload<NW>(ds, od, fq, dh.rot(g + 3), last, db);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            const int left = ngd - g;
-            if (left == 3) {
-                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
-                dload<NW>(ds, od, fq, dh.rot(g + 2), last, da);
-                dgroup<RB, NW, CS>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
-                dgroup<RB, NW, CS>(da, as, dh.rot(g + 2), nbw, cb0, yoff, a.out, j);
-            } else if (left == 2) {
-                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
-                dgroup<RB, NW, CS>(db, as, dh.rot(g + 1), nbw, cb0, yoff, a.out, j);
-            } else if (left == 1) {
-                dgroup<RB, NW, CS>(da, as, dh.rot(g), nbw, cb0, yoff, a.out, j);
-            }
-        };
-        if (rows > 16) run(std::integral_constant<int, 2>{});
-        else           run(std::integral_constant<int, 1>{});
+        // (the next pass, if any, primes the gate/up groups again)
+        fused_down_pass<NW, CS>(a, g, fb, acc, rows, list, r0, xs, wa, wb);
     }
 }
 

@@ -924,9 +924,35 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
     const int d = L->d, F = L->F, E = L->E, k = L->k;
     const size_t n = p.n;
     int *ids_d = ids ? ids : b.ids;
-    TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
-                   b.tile_expert, b.counters, s, !p.use_decode, nm));
-    if (p.use_decode) {
+    // Decode steps small enough route inside the fused expert kernel (same
+    // routing bits as the row-block router, no routing launch).
+    const bool routed = p.fused && g_rpath == 0 && L->wrT && !L->wr_nonfinite &&
+                        moe::decode_routed_ok(T, d, F, E, k);
+    if (routed) {
+        moe::RouteArgs ra{x, L->wr, L->bias, T, d, E, k, probs, ids_d, b.gw};
+        ra.wrT = L->wrT;
+        ra.no_dispatch = 1;
+        if (nm.x_raw) {
+            ra.x_raw = nm.x_raw; ra.rms_w = nm.rms_w; ra.rms_eps = nm.eps;
+            ra.rms_rcp = 1.0f / (float)d; ra.xn_out = const_cast<float *>(x);
+        }
+        moe::DecodeArgs gu{};
+        gu.x = x; gu.ids = ids_d; gu.topk = k; gu.w = L->wgu; gu.w2 = L->wdT; gu.out = b.ys;
+        gu.d = d; gu.F = F; gu.E = E; gu.ksplit = 1; gu.nslots = (int)n;
+        if (g_timing)
+            for (int i = 0; i < 3; ++i) HIP_TRY(hipEventRecord(g_ev[i], s));
+        HIP_TRY(moe::launch_decode_routed(gu, ra, s));
+        if (g_timing) {
+            HIP_TRY(hipEventRecord(g_ev[3], s));
+            HIP_TRY(hipEventRecord(g_ev[4], s));
+        }
+    } else {
+        TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
+                       b.tile_expert, b.counters, s, !p.use_decode, nm));
+    }
+    if (routed) {
+        // (the expert products ran with the routing)
+    } else if (p.use_decode) {
         // Fused gate/up + split-K down while its partials stay small, else
         // gate/up then down.
         moe::DecodeArgs gu{};

@@ -126,6 +126,13 @@ hipError_t launch_transpose_units(const float *src, float *dst, int R, int C, in
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
 hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s);
+// The fused decode kernel with the routing inside (every workgroup routes
+// all T tokens, then runs its item on the rows it holds): T <= 64, E <= 16,
+// d of 256 or 512, F % 128 == 0 (decode_routed_ok).  ra: the routing of the
+// same rows (row-block router arguments: wrT, optional bias and rms_norm);
+// a: the fused kernel's (out = the split-K partials, w2 = wdT).
+bool decode_routed_ok(int T, int d, int F, int E, int k);
+hipError_t launch_decode_routed(const DecodeArgs &a, const RouteArgs &ra, hipStream_t s);
 // Waves per item of the fused decode kernel (8 when d and F allow, else 4);
 // its split-K partials number F / (16 * waves).
 int decode_fused_waves(int d, int F);

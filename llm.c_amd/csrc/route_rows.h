@@ -51,6 +51,97 @@ __device__ inline void chain16_dpp(float &acc, float w, const float (&x)[16]) {
         : "v"(w), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]));
 }
 
+// The same chain with the router row held as float4s: lane c of a 16-lane
+// row holds k = 4c .. 4c + 3 of a 64-wide k block, so the sixteen steps of
+// quarter Q (k = 16Q + J) take component J % 4 of lane 4Q + J / 4.  x[J] is
+// x at k = 16Q + J of that block.
+#define MOE_CHAIN_DPP4(L0, L1, L2, L3)                                                        \
+    asm("s_nop 4\n\t"                                                                         \
+        "v_fmac_f32_dpp %0, %1, %5 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_fmac_f32_dpp %0, %2, %6 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_fmac_f32_dpp %0, %3, %7 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_fmac_f32_dpp %0, %4, %8 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_fmac_f32_dpp %0, %1, %9 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"       \
+        "v_fmac_f32_dpp %0, %2, %10 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %3, %11 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %4, %12 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %1, %13 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %2, %14 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %3, %15 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %4, %16 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %1, %17 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %2, %18 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %3, %19 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %4, %20 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        : "+v"(acc)                                                                           \
+        : "v"(w.x), "v"(w.y), "v"(w.z), "v"(w.w), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), \
+          "v"(x[4]), "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]),       \
+          "v"(x[11]), "v"(x[12]), "v"(x[13]), "v"(x[14]), "v"(x[15]))
+
+// Two chains of the same x (two experts of one token) interleaved step by
+// step, so that each FMA's predecessor in its chain is two instructions back.
+#define MOE_CHAIN2_DPP4(L0, L1, L2, L3)                                                       \
+    asm("s_nop 4\n\t"                                                                         \
+        "v_fmac_f32_dpp %0, %2, %10 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %6, %10 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %3, %11 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %7, %11 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %4, %12 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %8, %12 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %5, %13 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %9, %13 row_newbcast:" #L0 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %2, %14 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %6, %14 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %3, %15 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %7, %15 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %4, %16 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %8, %16 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %5, %17 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %9, %17 row_newbcast:" #L1 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %2, %18 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %6, %18 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %3, %19 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %7, %19 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %4, %20 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %8, %20 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %5, %21 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %9, %21 row_newbcast:" #L2 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %2, %22 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %6, %22 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %3, %23 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %7, %23 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %4, %24 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %8, %24 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %0, %5, %25 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        "v_fmac_f32_dpp %1, %9, %25 row_newbcast:" #L3 " row_mask:0xf bank_mask:0xf\n\t"      \
+        : "+v"(a0), "+v"(a1)                                                                  \
+        : "v"(w0.x), "v"(w0.y), "v"(w0.z), "v"(w0.w), "v"(w1.x), "v"(w1.y), "v"(w1.z),       \
+          "v"(w1.w), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]), "v"(x[5]),        \
+          "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]),     \
+          "v"(x[13]), "v"(x[14]), "v"(x[15]))
+
+// chain16_dpp4 on two accumulators (router rows w0 and w1) at once.
+template <int Q>
+__device__ inline void chain16x2_dpp4(float &a0, float &a1, const float4 &w0, const float4 &w1,
+                                      const float (&x)[16]) {
+    static_assert(Q >= 0 && Q < 4, "a quarter of a 64-wide k block");
+    if constexpr (Q == 0) MOE_CHAIN2_DPP4(0, 1, 2, 3);
+    else if constexpr (Q == 1) MOE_CHAIN2_DPP4(4, 5, 6, 7);
+    else if constexpr (Q == 2) MOE_CHAIN2_DPP4(8, 9, 10, 11);
+    else MOE_CHAIN2_DPP4(12, 13, 14, 15);
+}
+#undef MOE_CHAIN2_DPP4
+
+template <int Q>
+__device__ inline void chain16_dpp4(float &acc, const float4 &w, const float (&x)[16]) {
+    static_assert(Q >= 0 && Q < 4, "a quarter of a 64-wide k block");
+    if constexpr (Q == 0) MOE_CHAIN_DPP4(0, 1, 2, 3);
+    else if constexpr (Q == 1) MOE_CHAIN_DPP4(4, 5, 6, 7);
+    else if constexpr (Q == 2) MOE_CHAIN_DPP4(8, 9, 10, 11);
+    else MOE_CHAIN_DPP4(12, 13, 14, 15);
+}
+#undef MOE_CHAIN_DPP4
+
 template <int J>
 __device__ inline float row_bcast(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xF, 0xF, true));

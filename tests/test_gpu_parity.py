@@ -415,13 +415,15 @@ def test_block_ffn_dropin_c1():
     assert np.array_equal(bits(x1), bits(x + fo))
 
 
-@pytest.mark.parametrize("path", [2, 3, 1], ids=["gemv", "gemv2", "gemm"])
-def test_graph_replay(path):
+@pytest.mark.parametrize("path,rpath", [(2, 0), (2, 2), (3, 0), (1, 0)],
+                         ids=["gemv_routed", "gemv", "gemv2", "gemm"])
+def test_graph_replay(path, rpath):
     """A captured forward (two layers, accumulating) replays to the same bits
     as the eager calls, replay after replay, with eager work and
     synchronisations in between."""
     T, d, F, E, k = 64, 512, 2048, 16, 2
     mh.set_expert_path(path)
+    mh.set_router_path(rpath)
     layers = [mh.Layer(d, F, E, k) for _ in range(2)]
     try:
         for i, L in enumerate(layers):
@@ -457,6 +459,7 @@ def test_graph_replay(path):
         g.close()
     finally:
         mh.set_expert_path(0)
+        mh.set_router_path(0)
         for L in layers:
             L.close()
 
