@@ -119,29 +119,32 @@ __global__ __launch_bounds__(1024) void proj16_kernel(AttnArgs a) {
     float ss[2] = {0.0f, 0.0f};
     for (int k0 = 0; k0 < M; k0 += kPK) {
         const int k = k0 + 4 * xq;
+        // Every load reads a valid address (out-of-range elements read the
+        // tile's first element) and is masked after: a select between the
+        // load and a constant keeps all of them in flight together.
         float4 xv[2], wv[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int row = r0 + xr0 + 8 * i;
-            xv[i] = row < a.B && k < M ? *reinterpret_cast<const float4 *>(X + (size_t)row * M + k)
-                                       : zero;
+            const bool in = row < a.B && k < M;
+            xv[i] = masked4(in, *reinterpret_cast<const float4 *>(X + (in ? (size_t)row * M + k : 0)));
         }
+        const float *wp = QKV ? a.wqkv_p : a.wo_p;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 1024 * i, kk = k0 + idx / (kPT / 4), cc = c0 + 4 * (idx % (kPT / 4));
-            const float *src = nullptr;
-            const float *wp = QKV ? a.wqkv_p : a.wo_p;
-            if (kk < M && cc < N) {
-                if (wp)                      src = wp + ((size_t)(cc >> 4) * M + kk) * 16 + (cc & 15);
-                else if (!QKV)               src = a.wo + (size_t)kk * a.d + cc;
-                else if (cc < a.qd)          src = a.wq + (size_t)kk * a.qd + cc;
-                else if (cc < a.qd + a.kd)   src = a.wk + (size_t)kk * a.kd + (cc - a.qd);
-                else                         src = a.wv + (size_t)kk * a.kd + (cc - a.qd - a.kd);
-            }
-            wv[i] = src ? *reinterpret_cast<const float4 *>(src) : zero;
+            const bool in = kk < M && cc < N;
+            const int kr = in ? kk : 0, cr = in ? cc : 0;
+            const float *src;
+            if (wp)                      src = wp + ((size_t)(cr >> 4) * M + kr) * 16 + (cr & 15);
+            else if (!QKV)               src = a.wo + (size_t)kr * a.d + cr;
+            else if (cr < a.qd)          src = a.wq + (size_t)kr * a.qd + cr;
+            else if (cr < a.qd + a.kd)   src = a.wk + (size_t)kr * a.kd + (cr - a.qd);
+            else                         src = a.wv + (size_t)kr * a.kd + (cr - a.qd - a.kd);
+            wv[i] = masked4(in, *reinterpret_cast<const float4 *>(src));
         }
         float4 wr = zero;
-        if (QKV && k < M) wr = *reinterpret_cast<const float4 *>(a.rms_w + k);
+        if (QKV) wr = masked4(k < M, *reinterpret_cast<const float4 *>(a.rms_w + (k < M ? k : 0)));
         if (k0 > 0) __syncthreads();   // the previous chunk's products are done
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -318,14 +321,14 @@ __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
         const int row = i * R + rg;
         const bool in = row < n;
         const size_t off = base + (size_t)(in ? row : 0) * a.kd;
-        kv[i] = in ? *reinterpret_cast<const float4 *>(a.kc + off) : make_float4(0, 0, 0, 0);
+        kv[i] = masked4(in, *reinterpret_cast<const float4 *>(a.kc + off));
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int row = i * R + rg;
         const bool in = row < n;
         const size_t off = base + (size_t)(in ? row : 0) * a.kd;
-        vv[i] = in ? *reinterpret_cast<const float4 *>(a.vc + off) : make_float4(0, 0, 0, 0);
+        vv[i] = masked4(in, *reinterpret_cast<const float4 *>(a.vc + off));
     }
     float4 q[G];
 #pragma unroll

@@ -61,7 +61,6 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(RowsGemm g) {
     const int rows = min(kRM, g.offsets[e + 1] - row0);
     const int n0 = nt * kRN;
     const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
-    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
 
     const float *arow[2];
 #pragma unroll
@@ -85,15 +84,15 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(RowsGemm g) {
         if (!BT) {   // 16 k rows x 16 column quads
             bk = tid >> 4;
             bn = 4 * (tid & 15);
-            bv = n0 + bn < g.N
-                     ? *reinterpret_cast<const float4 *>(bb + (size_t)(k0 + bk) * g.ldb + n0 + bn)
-                     : zero;
+            const bool in = n0 + bn < g.N;
+            bv = masked4(in, *reinterpret_cast<const float4 *>(bb + (size_t)(k0 + bk) * g.ldb +
+                                                              (in ? n0 + bn : 0)));
         } else {     // 64 columns x 4 k quads
             bn = tid >> 2;
             bk = 4 * (tid & 3);
-            bv = n0 + bn < g.N
-                     ? *reinterpret_cast<const float4 *>(bb + (size_t)(n0 + bn) * g.ldb + k0 + bk)
-                     : zero;
+            const bool in = n0 + bn < g.N;
+            bv = masked4(in, *reinterpret_cast<const float4 *>(bb + (size_t)(in ? n0 + bn : 0) * g.ldb +
+                                                              k0 + bk));
         }
         __syncthreads();   // the previous slice is consumed
 #pragma unroll

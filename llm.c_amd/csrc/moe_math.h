@@ -9,6 +9,13 @@
 
 namespace moe {
 
+// v where in, else zeros, component by component (a select between whole
+// float4 structs is lowered through private memory, with flat loads that
+// wait one by one).
+__device__ inline float4 masked4(bool in, float4 v) {
+    return make_float4(in ? v.x : 0.0f, in ? v.y : 0.0f, in ? v.z : 0.0f, in ? v.w : 0.0f);
+}
+
 __device__ inline float ftz_f(float x) {
     uint32_t u = __float_as_uint(x);
     return ((u & 0x7f800000u) == 0u) ? __uint_as_float(u & 0x80000000u) : x;
