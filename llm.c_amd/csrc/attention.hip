@@ -315,6 +315,14 @@ __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
     float *part = a.part + ((size_t)(b * a.nh + kvh * G) * nchunk + c) * (HD + 2);
     const size_t head_stride = (size_t)nchunk * (HD + 2);
     const size_t base = ((size_t)b * a.max_seq + j0) * a.kd + kvh * HD + 4 * cq;
+    // q, then the K rows, then the V rows, all issued before anything waits
+    // (the scheduling barrier keeps the compiler from sinking the V loads
+    // below the scores, which would cost a second memory round trip).
+    float4 q[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+        q[h] = *reinterpret_cast<const float4 *>(a.q + (size_t)b * a.qd + (kvh * G + h) * HD +
+                                                 4 * cq);
     float4 kv[NI], vv[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -330,11 +338,7 @@ __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
         const size_t off = base + (size_t)(in ? row : 0) * a.kd;
         vv[i] = masked4(in, *reinterpret_cast<const float4 *>(a.vc + off));
     }
-    float4 q[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-        q[h] = *reinterpret_cast<const float4 *>(a.q + (size_t)b * a.qd + (kvh * G + h) * HD +
-                                                 4 * cq);
+    __builtin_amdgcn_sched_barrier(0);
     float v[CNT];
 #pragma unroll
     for (int i = 0; i < NI; ++i)
