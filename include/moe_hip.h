@@ -188,10 +188,10 @@ int moe_hip_forward_dev(MoeHipLayer *layer, const float *x, int T, float *out,
  * reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Every
  * temporary (routing, dispatch, expert activations, partial products,
- * completion counters) lives in a fixed 64 MiB device array of the library,
+ * completion counters) lives in a fixed 128 MiB device array of the library,
  * one per GPU, held until the process ends; the layer's weights and the
  * caller's x, out, probs and ids are the only other memory touched.  A call
- * whose temporaries exceed 64 MiB fails with MOE_HIP_ERR_UNSUPPORTED (the
+ * whose temporaries exceed 128 MiB fails with MOE_HIP_ERR_UNSUPPORTED (the
  * message gives the need): at d_model 256, ffn_hidden 1024 that is above
  * about 10k tokens at top-2; the 64-sequence decode layer of d_model 512,
  * ffn_hidden 2048, E=16 takes 4.2 MB.  The library must be initialised

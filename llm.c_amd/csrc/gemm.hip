@@ -38,6 +38,7 @@
 #include "moe_internal.h"
 #include "moe_math.h"
 #include "synth.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace moe {
@@ -58,22 +59,18 @@ __device__ __forceinline__ void gemm_dma16(const float *g, float *lds) {
 // s_waitcnt limiting only the vector-memory count (expcnt, lgkmcnt at max).
 #define GEMM_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | 0x0F70)
 
+// One tile (m-tile mtg, n-tile nt) over the nk K slices from element kb;
+// the down projection writes its partial to slot `slot` (c + slot *
+// split_stride) and, with npieces > 0, records npieces for the tile's rows.
+// Every thread of the workgroup calls this together.
 template <int MODE, int WN>
-__global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mtg, int nt, int kb,
+                                          int nk, int slot, int npieces) {
     constexpr int BN = 64 * WN;
-    extern __shared__ __align__(16) float smem[];
     // Two buffers each: A as 128 rows of 32 swizzled floats, B as
     // (BN/16) x 2 packed 1 KB units (BN rows of 32 floats' worth).
     float *As = smem;
     float *Bs = smem + 2 * BM * KT;
-
-    const int ntiles = a.N / BN;
-    const int per_split = a.max_mtiles * ntiles;
-    const int ks = blockIdx.x / per_split;       // reduction split (down projection)
-    const int nt = (blockIdx.x % per_split) % ntiles;
-    const int mtg = (blockIdx.x % per_split) / ntiles;
-    const int total = a.tile_off[a.E];
-    if (mtg >= total) return;
     const int e = a.tile_expert[mtg];
     const int row0 = a.offsets[e] + (mtg - a.tile_off[e]) * BM;
     const int rows = min(BM, a.offsets[e + 1] - row0);
@@ -139,8 +136,6 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.0f;
 
-    const int nk = K / KT / a.ksplit;   // K steps of this split
-    const int kb = ks * nk * KT;
     adma(kb, 0);
     bdma(kb, 0);
     GEMM_WAIT_VMCNT(0);
@@ -243,7 +238,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                 }
             }
     } else {
-        float *c = a.c + (size_t)ks * a.split_stride;
+        float *c = a.c + (size_t)slot * a.split_stride;
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -256,7 +251,52 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
                         c[dst + nt * BN + wn * 64 + n * 32 + li] = acc[m][n][r];
                 }
             }
+        if (npieces > 0)
+            for (int r = tid; r < rows; r += 128 * WN)
+                a.pieces[(size_t)a.perm[row0 + r] * (a.N / BN) + nt] = npieces;
     }
+}
+
+// Grid: the (m-tile, n-tile) pairs, times the reduction splits.  Down
+// projection in stream-K form (a.streamk): workgroup g takes units
+// [g per, (g + 1) per) of the flat list of (live tile, K slice) units, per =
+// ceil(units / grid); each tile it touches is a piece whose index within
+// the tile (0 for the workgroup holding the tile's first slice) is the
+// partial slot it writes, and piece 0 records the tile's piece count for
+// the combine.  Slots, pieces and counts follow from the live tile count
+// alone, so results are deterministic.
+template <int MODE, int WN>
+__global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
+    constexpr int BN = 64 * WN;
+    extern __shared__ __align__(16) float smem[];
+    const int ntiles = a.N / BN;
+    const int nks = a.K / KT;
+    if (MODE == 1 && a.streamk) {
+        const long units = (long)a.tile_off[a.E] * ntiles * nks;
+        const long per = (units + gridDim.x - 1) / gridDim.x;
+        long u = (long)blockIdx.x * per;
+        const long uend = u + per < units ? u + per : units;
+        while (u < uend) {
+            const int tile = (int)(u / nks);
+            const int k0 = (int)(u - (long)tile * nks);
+            const int k1 = (int)(k0 + (uend - u) < nks ? k0 + (uend - u) : nks);
+            const long tstart = (long)tile * nks;
+            const int first = (int)(tstart / per);   // workgroup of the tile's first slice
+            const int slot = (int)blockIdx.x - first;
+            const int npieces = (int)((tstart + nks - 1) / per) - first + 1;
+            gemm_tile<MODE, WN>(a, smem, tile / ntiles, tile % ntiles, k0 * KT, k1 - k0, slot,
+                                slot == 0 ? npieces : 0);
+            u += k1 - k0;
+        }
+        return;
+    }
+    const int per_split = a.max_mtiles * ntiles;
+    const int ks = blockIdx.x / per_split;       // reduction split (down projection)
+    const int nt = (blockIdx.x % per_split) % ntiles;
+    const int mtg = (blockIdx.x % per_split) / ntiles;
+    if (mtg >= a.tile_off[a.E]) return;
+    const int nk = nks / a.ksplit;   // K steps of this split
+    gemm_tile<MODE, WN>(a, smem, mtg, nt, ks * nk * KT, nk, ks, 0);
 }
 
 template <int MODE, int WN>
@@ -292,7 +332,7 @@ hipError_t launch_mode(const GemmArgs &a, hipStream_t s) {
 // out[t] = sum over slots of gw * y, one FMA per slot in slot order
 // (src/transformer.c:355-358 after contraction), optionally added into out.
 // With ksplit > 1 each slot's y is the sum of its split partials, added in
-// split order.
+// split order (with pieces: as many as its column block's tile had).
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
     const int d4 = a.d >> 2;
     const size_t total = (size_t)a.T * d4;
@@ -303,7 +343,10 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
             const float w = a.gw[(size_t)t * a.k + ki];
             const float *yp = a.ys + ((size_t)t * a.k + ki) * a.d + 4 * c;
             floatx4 y = *reinterpret_cast<const floatx4 *>(yp);
-            for (int sp = 1; sp < a.ksplit; ++sp) {
+            const int np = a.pieces ? a.pieces[((size_t)t * a.k + ki) * (a.d / a.pieces_cols) +
+                                               4 * c / a.pieces_cols]
+                                    : a.ksplit;
+            for (int sp = 1; sp < np; ++sp) {
                 const floatx4 p = *reinterpret_cast<const floatx4 *>(yp + sp * a.split_stride);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) y[j] = y[j] + p[j];
@@ -497,8 +540,45 @@ GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split) {
     return p;
 }
 
+DownPlan down_plan(int N, int K, int max_mtiles, size_t n) {
+    const GemmPlan g = gemm_plan(N, K, max_mtiles, true);
+    DownPlan p{g.bn, g.ksplit, 0, 0};
+    if (g.bn != 256 || K % KT) return p;
+    // Stream-K when the tiles make fewer than ~4 rounds of one workgroup per
+    // CU: every CU gets the same number of K slices, where whole tiles (or
+    // tiles split a fixed 2 or 4 ways) leave a partial last round.
+    const long cus = device_cus();
+    const long tiles_max = (long)max_mtiles * (N / 256);
+    if (tiles_max >= 4 * cus) return p;
+    const long nks = K / KT;
+    // The fewest live tiles n rows can make (all rows in full m-tiles) set
+    // the shortest run per workgroup, hence the most pieces a tile can have.
+    const long tiles_min = (long)((n + BM - 1) / BM) * (N / 256);
+    const long units_min = tiles_min * nks;
+    // At least 4 slices per workgroup on small problems.
+    const long groups = std::max(1L, std::min(cus, units_min / 4));
+    const long per_min = (units_min + groups - 1) / groups;
+    p.streamk = 1;
+    p.groups = (int)groups;
+    p.slots = (int)((nks - 1 + per_min - 1) / per_min + 1);
+    return p;
+}
+
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) { return launch_mode<0>(a, s); }
-hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) { return launch_mode<1>(a, s); }
+hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) {
+    if (!a.streamk) return launch_mode<1>(a, s);
+    if (!a.pieces || a.sk_groups <= 0 || a.N % 256 || a.K % KT) return hipErrorInvalidValue;
+    constexpr size_t lds = (size_t)(2 * BM + 2 * 256) * KT * sizeof(float);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void *>(&grouped_gemm_kernel<1, 4>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (err != hipSuccess) return err;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((grouped_gemm_kernel<1, 4>), dim3((unsigned)a.sk_groups), dim3(512), lds, s, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm_bwd(const GemmArgs &a, int mode, hipStream_t s) {
     if (a.ksplit != 1) return hipErrorInvalidValue;
@@ -517,7 +597,9 @@ hipError_t launch_gemm_bwd(const GemmArgs &a, int mode, hipStream_t s) {
 }
 
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
-    if (a.ksplit > 8 && a.ksplit <= 128) {
+    if (a.pieces && (a.pieces_cols <= 0 || a.pieces_cols % 4 || a.d % a.pieces_cols))
+        return hipErrorInvalidValue;
+    if (!a.pieces && a.ksplit > 8 && a.ksplit <= 128) {
         const int groups = (a.ksplit + 7) / 8;
         const size_t n = (size_t)a.T * (a.d >> 2);
         if (n == 0) return hipSuccess;

@@ -29,7 +29,7 @@ struct MoeHipLayer {
 // a fixed device array, one copy per GPU the library runs on, held until the
 // process ends.  In host code its name is not a device address: host code
 // uses the per-device address hipGetSymbolAddress returns (scratch_of).
-constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr size_t kScratchBytes = (size_t)128 << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
@@ -133,11 +133,11 @@ struct DevBuf {
 
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
-    DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, stage,
-        counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork;
+    DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, pieces,
+        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
-                         &tile_expert, &perm, &h, &ys, &stage, &counters, &xn, &rmsw,
+                         &tile_expert, &perm, &h, &ys, &pieces, &stage, &counters, &xn, &rmsw,
                          &aq, &ao, &apart, &acnt, &bw, &bwork};
         for (DevBuf *b : all) b->release();
     }
@@ -809,9 +809,11 @@ struct FwdPlan {
     size_t n = 0;           // T * k assignments
     int max_mtiles = 0;     // grouped GEMM m-tile bound
     bool use_decode = false, fused = false;
-    int ksplit = 1;         // partial products per slot the combine adds
+    int ksplit = 1;         // partial products per slot the combine adds (at most, stream-K)
+    int streamk = 0, sk_groups = 0;   // down projection in stream-K form (moe::down_plan)
     size_t h_floats = 0;    // H [n x F] (grouped GEMMs, unfused decode)
     size_t ys_floats = 0;   // per-slot products / split-K partials
+    size_t pieces_ints = 0; // stream-K piece counts [n][d / 256]
 };
 
 // The device buffers of one forward.
@@ -821,6 +823,7 @@ struct FwdBufs {
     int *counts = nullptr, *offsets = nullptr, *tile_off = nullptr, *tile_expert = nullptr;
     int *perm = nullptr;    // [n]
     float *h = nullptr, *ys = nullptr;
+    int *pieces = nullptr;     // [n][d / 256] (stream-K down projection)
     int *counters = nullptr;   // kMaxCounters ints, zero between launches
 };
 
@@ -853,9 +856,13 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
         p->h_floats = n * F;
         p->ys_floats = n * d * p->ksplit;
     } else {
-        // Small grids split the down projection's reduction; the combine adds
-        // the splits in order.
-        p->ksplit = moe::gemm_plan(d, F, p->max_mtiles, true).ksplit;
+        // Small grids split the down projection's reduction (a fixed split,
+        // or stream-K pieces); the combine adds the partials in order.
+        const moe::DownPlan dp = moe::down_plan(d, F, p->max_mtiles, n);
+        p->ksplit = dp.slots;
+        p->streamk = dp.streamk;
+        p->sk_groups = dp.groups;
+        p->pieces_ints = dp.streamk ? n * (size_t)(d / 256) : 0;
         p->h_floats = n * F;
         p->ys_floats = (size_t)p->ksplit * n * d;
     }
@@ -873,11 +880,13 @@ int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
     TRY(g_ws.perm.reserve(sizeof(int) * p.n));
     if (p.h_floats) TRY(g_ws.h.reserve(sizeof(float) * p.h_floats));
     TRY(g_ws.ys.reserve(sizeof(float) * p.ys_floats));
+    if (p.pieces_ints) TRY(g_ws.pieces.reserve(sizeof(int) * p.pieces_ints));
     TRY(ensure_counters());
     b->ids = g_ws.ids.as<int>(); b->gw = g_ws.gw.as<float>();
     b->counts = g_ws.counts.as<int>(); b->offsets = g_ws.offsets.as<int>();
     b->tile_off = g_ws.tile_off.as<int>(); b->tile_expert = g_ws.tile_expert.as<int>();
     b->perm = g_ws.perm.as<int>(); b->h = g_ws.h.as<float>(); b->ys = g_ws.ys.as<float>();
+    b->pieces = p.pieces_ints ? g_ws.pieces.as<int>() : nullptr;
     b->counters = g_ws.counters.as<int>();
     return MOE_HIP_OK;
 }
@@ -904,6 +913,7 @@ void carve_bufs(const MoeHipLayer *L, const FwdPlan &p, char *base, size_t cap, 
     c.perm = static_cast<int *>(take(sizeof(int) * p.n));
     c.h = p.h_floats ? static_cast<float *>(take(sizeof(float) * p.h_floats)) : nullptr;
     c.ys = static_cast<float *>(take(sizeof(float) * p.ys_floats));
+    c.pieces = p.pieces_ints ? static_cast<int *>(take(sizeof(int) * p.pieces_ints)) : nullptr;
     *need = off;
     if (off <= cap) *b = c;
 }
@@ -986,10 +996,17 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
                          d, d, p.max_mtiles};
         dn.ksplit = p.ksplit;
         dn.split_stride = n * (size_t)d;
+        dn.streamk = p.streamk;
+        dn.sk_groups = p.sk_groups;
+        dn.pieces = b.pieces;
         HIP_TRY(moe::launch_gemm_down(dn, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
     }
     moe::CombineArgs ca{b.ys, b.gw, out, T, d, k, accumulate, p.ksplit, n * (size_t)d};
+    if (p.streamk) {
+        ca.pieces = b.pieces;
+        ca.pieces_cols = 256;
+    }
     HIP_TRY(moe::launch_combine(ca, s));
     if (g_timing) {
         HIP_TRY(hipEventRecord(g_ev[5], s));

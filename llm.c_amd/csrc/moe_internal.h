@@ -75,6 +75,12 @@ struct GemmArgs {
     // split s writing its partial to c + s * split_stride.
     int ksplit = 1;
     size_t split_stride = 0;
+    // Down projection in stream-K form (down_plan): sk_groups workgroups
+    // share the (tile, K slice) units equally; piece s of a tile writes slot
+    // s, and pieces[row][n-tile] receives the tile's piece count.
+    int streamk = 0;
+    int sk_groups = 0;
+    int *pieces = nullptr;
     // Backward epilogues: mode 2 also writes H = swiglu(G, U) to c2.
     float *c2 = nullptr;
     int ldc2 = 0;
@@ -88,6 +94,10 @@ struct CombineArgs {
     int accumulate;      // out += combined instead of out = combined
     int ksplit;          // partial products per slot (1 for the GEMM path)
     size_t split_stride; // floats between consecutive partials
+    // With pieces: slot a's columns [pieces_cols j, pieces_cols (j + 1)) add
+    // pieces[a * (d / pieces_cols) + j] partials instead of ksplit.
+    const int *pieces = nullptr;
+    int pieces_cols = 0;
 };
 
 struct DecodeArgs {
@@ -232,5 +242,13 @@ struct GemmPlan {
     int bn, ksplit;
 };
 GemmPlan gemm_plan(int N, int K, int max_mtiles, bool allow_split);
+
+// The forward's down projection: classic (the gemm_plan split) or, for
+// grids of a few rounds, stream-K over `groups` workgroups with at most
+// `slots` partials per tile.  n: the routed rows (T * k).
+struct DownPlan {
+    int bn, slots, streamk, groups;
+};
+DownPlan down_plan(int N, int K, int max_mtiles, size_t n);
 
 }  // namespace moe

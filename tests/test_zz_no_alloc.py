@@ -127,7 +127,7 @@ def test_noalloc_in_graph_replays():
 def test_noalloc_refuses_oversized_call():
     """Temporaries above the fixed array: MOE_HIP_ERR_UNSUPPORTED, before any
     kernel runs."""
-    d, F, E, k, T = 256, 1024, 8, 2, 16384   # H alone is 128 MiB
+    d, F, E, k, T = 256, 1024, 8, 2, 16384   # H alone fills the 128 MiB array
     layer = mh.Layer(d, F, E, k)
     try:
         x = mh.DeviceArray((T, d))
