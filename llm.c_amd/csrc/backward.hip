@@ -456,14 +456,22 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(float *G, float *U, con
 
 // Where an expert GEMM left its [T k x d] rows: by dispatch position, or by
 // slot as ns partials ys apart (summed in order).
+// With pieces (a stream-K GEMM): slot a's columns [pcols j, pcols (j + 1))
+// hold pieces[a * (d / pcols) + j] partials instead of ns.
 struct SlotRows {
     const float *p;
     int by_slot, ns;
     size_t ys;
+    const int *pieces = nullptr;
+    int pcols = 0;
+    __device__ int count(int a, int d, int c) const {
+        return pieces ? pieces[(size_t)a * (d / pcols) + c / pcols] : ns;
+    }
     __device__ float at(int pos, int a, int d, int c) const {
         const float *r = p + (size_t)(by_slot ? a : pos) * d + c;
         float v = r[0];
-        for (int s = 1; s < ns; ++s) v += r[(size_t)s * ys];
+        const int n = count(a, d, c);
+        for (int s = 1; s < n; ++s) v += r[(size_t)s * ys];
         return v;
     }
 };
@@ -535,7 +543,8 @@ __global__ __launch_bounds__(256) void dx_kernel(SlotRows dXr, const int *inv,
         const int a = t * k + s;
         const float *r = dXr.p + (size_t)(dXr.by_slot ? a : inv[a]) * d + c;
         fx4 y = *reinterpret_cast<const fx4 *>(r);
-        for (int z = 1; z < dXr.ns; ++z) y += *reinterpret_cast<const fx4 *>(r + (size_t)z * dXr.ys);
+        const int ns = dXr.count(a, d, c);
+        for (int z = 1; z < ns; ++z) y += *reinterpret_cast<const fx4 *>(r + (size_t)z * dXr.ys);
         v += y;
     }
     fx4 rr = {0.f, 0.f, 0.f, 0.f};
@@ -590,10 +599,9 @@ unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 25
 
 bool backward_engine_ok(int d, int F) { return d % 64 == 0 && F % 64 == 0; }
 
-int backward_slot_splits(int d, int F, int max_mtiles) {
+int backward_slot_splits(int d, int F, int max_mtiles, size_t n) {
     if (!backward_engine_ok(d, F)) return 1;
-    return std::max(gemm_plan(d, F, max_mtiles, true).ksplit,
-                    gemm_plan(d, 2 * F, max_mtiles, true).ksplit);
+    return std::max(down_plan(d, F, max_mtiles, n).slots, down_plan(d, 2 * F, max_mtiles, n).slots);
 }
 
 hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
@@ -632,24 +640,29 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         gu.a = b.x; gu.b = b.wgu; gu.c = GU; gu.K = d; gu.N = 2 * F; gu.ldc = 2 * F;
         gu.c2 = b.H; gu.ldc2 = F;
         BWD_TRY(launch_gemm_bwd(gu, 2, s));
-        const GemmPlan py = gemm_plan(d, F, b.max_mtiles, true);
+        // (Y and dX: down-projection shapes, by slot with split partials or
+        // stream-K pieces, moe::down_plan; one piece-count table serves both
+        // in turn.)
+        const DownPlan py = down_plan(d, F, b.max_mtiles, n);
         GemmArgs gy = g;
         gy.a = b.H; gy.b = b.wdT; gy.c = b.Y; gy.K = F; gy.N = d; gy.ldc = d;
-        gy.ksplit = py.ksplit; gy.split_stride = nd;
+        gy.ksplit = py.slots; gy.split_stride = nd;
+        gy.streamk = py.streamk; gy.sk_groups = py.groups; gy.pieces = b.pieces;
         BWD_TRY(launch_gemm_down(gy, s));
         hipLaunchKernelGGL(slot_kernel, dim3(slot_grid), dim3(256), 0, s,
-                           SlotRows{b.Y, 1, py.ksplit, nd}, b.dout, b.gw, b.perm, k, d, (int)n,
-                           b.dgw, b.dY, b.inv);
+                           SlotRows{b.Y, 1, py.slots, nd, py.streamk ? b.pieces : nullptr, 256},
+                           b.dout, b.gw, b.perm, k, d, (int)n, b.dgw, b.dY, b.inv);
         // dH -> dG, dU in place over GU; dXr = dGU wgu^T by slot (over Y).
         GemmArgs gh = g;
         gh.a = b.dY; gh.b = b.wdTT; gh.c = GU; gh.K = d; gh.N = F; gh.ldc = 2 * F;
         BWD_TRY(launch_gemm_bwd(gh, 3, s));
-        const GemmPlan px = gemm_plan(d, 2 * F, b.max_mtiles, true);
+        const DownPlan px = down_plan(d, 2 * F, b.max_mtiles, n);
         GemmArgs gx = g;
         gx.a = GU; gx.b = b.wguT; gx.c = b.Y; gx.K = 2 * F; gx.N = d; gx.ldc = d;
-        gx.ksplit = px.ksplit; gx.split_stride = nd;
+        gx.ksplit = px.slots; gx.split_stride = nd;
+        gx.streamk = px.streamk; gx.sk_groups = px.groups; gx.pieces = b.pieces;
         BWD_TRY(launch_gemm_down(gx, s));
-        dXr = SlotRows{b.Y, 1, px.ksplit, nd};
+        dXr = SlotRows{b.Y, 1, px.slots, nd, px.streamk ? b.pieces : nullptr, 256};
     } else {
         // Recompute: G, U (gathered x rows), H, Y.
         rows(T_{}, F_{}, b.x, d, b.wg, (size_t)d * F, F, b.G, d, F, 0);

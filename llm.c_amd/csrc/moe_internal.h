@@ -213,14 +213,16 @@ struct BackwardArgs {
     float aux_coef;
     float *G, *U, *H, *dH, *Y, *dY, *dgw, *dlogits;
     int *inv;
+    int *pieces = nullptr;   // [n][d / 256] when a down_plan is stream-K
     float *dx, *dwr, *dwg, *dwu, *dwd, *aux;
     int accumulate;
 };
 hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s);
 // The backward runs its row products on the grouped tile engine.
 bool backward_engine_ok(int d, int F);
-// Partial products per slot row the engine path leaves in Y (1 otherwise).
-int backward_slot_splits(int d, int F, int max_mtiles);
+// Partial products per slot row the engine path leaves in Y (1 otherwise);
+// n = T * k.
+int backward_slot_splits(int d, int F, int max_mtiles, size_t n);
 
 // rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,
