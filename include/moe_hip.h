@@ -103,7 +103,11 @@ enum {
  * [x->rows x d_model], writes cache->router_probs [T x E] and
  * cache->expert_ids [T x top_k].  Weights are uploaded on first use and kept
  * resident, keyed by the MoEWeights address and every matrix data pointer;
- * call moe_hip_invalidate() after changing weight values in place.
+ * call moe_hip_invalidate() after changing weight values in place.  Any
+ * d_model and ffn_hidden: widths the kernels do not tile are padded with
+ * zeros inside the resident layer (same routing bits, same outputs within
+ * the layer tolerance); n_experts <= 128 and top_k <= 16.  The same holds for
+ * moe_decode_step, moe_decode_batch and moe_block_ffn.
  * On error it prints the reason and aborts, as the reference does on OOM
  * (src/matrix.c:148-158). */
 void moe_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg,

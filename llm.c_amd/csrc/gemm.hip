@@ -626,6 +626,26 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// dst[r][c] = src[r][c] for c < min(sc, dc), 0 for sc <= c < dc: rows widened
+// with zeros, or cut to their first dc columns.
+__global__ __launch_bounds__(256) void copy_rows_kernel(const float *src, int rows, int sc,
+                                                        float *dst, int dc) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)rows * dc) return;
+    const size_t r = i / dc;
+    const int c = (int)(i - r * dc);
+    dst[i] = c < sc ? src[r * sc + c] : 0.0f;
+}
+
+hipError_t launch_copy_rows(const float *src, int rows, int src_cols, float *dst, int dst_cols,
+                            hipStream_t s) {
+    const size_t n = (size_t)rows * dst_cols;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src,
+                       rows, src_cols, dst, dst_cols);
+    return hipGetLastError();
+}
+
 hipError_t launch_pack_gateup(const float *wg, const float *wu, float *dst, int d, int F,
                               hipStream_t s) {
     dim3 grid(F / 32, d / 32);

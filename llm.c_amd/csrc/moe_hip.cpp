@@ -134,11 +134,11 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, pieces,
-        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork;
+        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork, xpad;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
                          &tile_expert, &perm, &h, &ys, &pieces, &stage, &counters, &xn, &rmsw,
-                         &aq, &ao, &apart, &acnt, &bw, &bwork};
+                         &aq, &ao, &apart, &acnt, &bw, &bwork, &xpad};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -185,9 +185,13 @@ struct Norm {
 };
 
 // Residency cache for the drop-in entry points.
+// A host drop-in's weights made resident.  d, F: the caller's widths; the
+// layer's own are rounded up (padded_dims) when they are not a multiple of
+// what the kernels tile.
 struct Resident {
     MoeHipLayer *layer = nullptr;
     std::vector<const void *> ptrs;
+    int d = 0, F = 0;
 };
 std::map<const MoEWeights *, Resident> g_resident;
 
@@ -202,7 +206,9 @@ std::vector<const void *> weight_ptrs(const MoEWeights *w) {
     return v;
 }
 
-int check_shapes(int d, int F, int E, int k) {
+// Shapes a device layer takes (widths = false: the host drop-ins, which pad
+// other widths themselves).
+int check_shapes(int d, int F, int E, int k, bool widths = true) {
     if (d <= 0 || F <= 0 || E <= 0 || k <= 0)
         return set_err(MOE_HIP_ERR_ARG, "bad MoE shape d=%d F=%d E=%d k=%d", d, F, E, k);
     if (k > E)
@@ -210,10 +216,21 @@ int check_shapes(int d, int F, int E, int k) {
     if (E > moe::kMaxExperts || k > moe::kMaxTopK)
         return set_err(MOE_HIP_ERR_UNSUPPORTED, "n_experts %d / top_k %d above the supported %d / %d",
                        E, k, moe::kMaxExperts, moe::kMaxTopK);
-    if (d % 64 != 0 || F % 32 != 0)
+    if (widths && (d % 64 != 0 || F % 32 != 0))
         return set_err(MOE_HIP_ERR_UNSUPPORTED,
                        "d_model %% 64 and ffn_hidden %% 32 must be 0 (got d=%d F=%d)", d, F);
     return MOE_HIP_OK;
+}
+
+// The widths a drop-in's resident layer uses: d_model rounded up to a
+// multiple of 64, ffn_hidden to 64 when it is not a multiple of 32.  The
+// padding holds zeros in x and in every weight, which leaves the layer
+// unchanged: the router's chains add exact zeros (a logit's sign of zero
+// aside, which no probability sees), a padded feature has gate = up = 0 and
+// so H = silu(0) * 0 = 0, and padded output columns are dropped.
+void padded_dims(int d, int F, int *dp, int *Fp) {
+    *dp = (d + 63) / 64 * 64;
+    *Fp = F % 32 == 0 ? F : (F + 63) / 64 * 64;
 }
 
 int validate_weights(const MoEWeights *w, int d, int F) {
@@ -232,29 +249,95 @@ int validate_weights(const MoEWeights *w, int d, int F) {
     return MOE_HIP_OK;
 }
 
+// Router [d x E] from host memory: device copy, its transpose, and the
+// non-finite check that selects the zero-skipping router.
+int upload_router(MoeHipLayer *L, const float *wr) {
+    HIP_TRY(hipMemcpyAsync(L->wr, wr, sizeof(float) * (size_t)L->d * L->E, hipMemcpyHostToDevice,
+                           g_stream));
+    HIP_TRY(moe::launch_transpose(L->wr, L->wrT, L->d, L->E, g_stream));
+    L->wr_nonfinite = 0;
+    for (size_t i = 0; i < (size_t)L->d * L->E; ++i)
+        if (!std::isfinite(wr[i])) { L->wr_nonfinite = 1; break; }
+    return MOE_HIP_OK;
+}
+
+// Expert e from host memory (reference layout) into the packed arrays,
+// through the device staging buffer (3 d F floats).
+int upload_expert(MoeHipLayer *L, int e, const float *wg, const float *wu, const float *wd) {
+    const size_t dF = (size_t)L->d * L->F;
+    TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
+    float *st = g_ws.stage.as<float>();
+    HIP_TRY(hipMemcpyAsync(st, wg, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipMemcpyAsync(st + dF, wu, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipMemcpyAsync(st + 2 * dF, wd, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(moe::launch_pack_gateup(st, st + dF, L->wgu + 2 * dF * e, L->d, L->F, g_stream));
+    HIP_TRY(moe::launch_pack_down(st + 2 * dF, L->wdT + dF * e, L->F, L->d, g_stream));
+    return MOE_HIP_OK;
+}
+
+// The weights zero-padded to the layer's widths, one expert at a time.
+int load_padded(MoeHipLayer *L, const MoEWeights *w, int d, int F) {
+    const int dp = L->d, Fp = L->F, E = L->E;
+    std::vector<float> wr((size_t)dp * E, 0.0f);
+    for (int r = 0; r < d; ++r)
+        std::copy_n(w->W_router.data + (size_t)r * E, E, wr.begin() + (size_t)r * E);
+    TRY(upload_router(L, wr.data()));
+    std::vector<float> g((size_t)dp * Fp, 0.0f), u((size_t)dp * Fp, 0.0f), dn((size_t)Fp * dp, 0.0f);
+    for (int e = 0; e < E; ++e) {
+        const FFNWeights &f = w->experts[e];
+        for (int r = 0; r < d; ++r) {
+            std::copy_n(f.W_gate.data + (size_t)r * F, F, g.begin() + (size_t)r * Fp);
+            std::copy_n(f.W_up.data + (size_t)r * F, F, u.begin() + (size_t)r * Fp);
+        }
+        for (int r = 0; r < F; ++r)
+            std::copy_n(f.W_down.data + (size_t)r * d, d, dn.begin() + (size_t)r * dp);
+        TRY(upload_expert(L, e, g.data(), u.data(), dn.data()));
+        HIP_TRY(hipStreamSynchronize(g_stream));   // (the host buffers are reused)
+    }
+    return MOE_HIP_OK;
+}
+
 int resident_layer(const MoEWeights *w, int d, int F, MoeHipLayer **out) {
     TRY(validate_weights(w, d, F));
     std::vector<const void *> ptrs = weight_ptrs(w);
     auto it = g_resident.find(w);
     if (it != g_resident.end()) {
         MoeHipLayer *L = it->second.layer;
-        if (it->second.ptrs == ptrs && L->d == d && L->F == F && L->E == w->n_experts &&
-            L->k == w->top_k) {
+        if (it->second.ptrs == ptrs && it->second.d == d && it->second.F == F &&
+            L->E == w->n_experts && L->k == w->top_k) {
             *out = L;
             return MOE_HIP_OK;
         }
         moe_hip_layer_destroy(L);
         g_resident.erase(it);
     }
+    int dp = d, Fp = F;
+    padded_dims(d, F, &dp, &Fp);
     MoeHipLayer *L = nullptr;
-    TRY(moe_hip_layer_create(d, F, w->n_experts, w->top_k, &L));
-    int rc = moe_hip_layer_load(L, w);
+    TRY(moe_hip_layer_create(dp, Fp, w->n_experts, w->top_k, &L));
+    int rc = dp == d && Fp == F ? moe_hip_layer_load(L, w) : load_padded(L, w, d, F);
     if (rc != MOE_HIP_OK) {
         moe_hip_layer_destroy(L);
         return rc;
     }
-    g_resident[w] = Resident{L, ptrs};
+    g_resident[w] = Resident{L, ptrs, d, F};
     *out = L;
+    return MOE_HIP_OK;
+}
+
+// A drop-in's forward of T rows of the caller's width d (x, and out when
+// accumulating, in device memory of that width), through a resident layer
+// that may be wider: rows are widened with zeros and the output cut back.
+int dropin_forward(MoeHipLayer *L, int d, const float *x, int T, float *out, float *probs,
+                   int *ids, int accumulate) {
+    if (L->d == d) return moe_hip_forward_dev(L, x, T, out, probs, ids, accumulate, g_stream);
+    const size_t np = (size_t)T * L->d;
+    TRY(g_ws.xpad.reserve(sizeof(float) * 2 * np));
+    float *xp = g_ws.xpad.as<float>(), *op = xp + np;
+    HIP_TRY(moe::launch_copy_rows(x, T, d, xp, L->d, g_stream));
+    if (accumulate) HIP_TRY(moe::launch_copy_rows(out, T, d, op, L->d, g_stream));
+    TRY(moe_hip_forward_dev(L, xp, T, op, probs, ids, accumulate, g_stream));
+    HIP_TRY(moe::launch_copy_rows(op, T, L->d, out, d, g_stream));
     return MOE_HIP_OK;
 }
 
@@ -360,33 +443,6 @@ int moe_hip_layer_destroy(MoeHipLayer *L) {
     if (L->wgu) (void)hipFree(L->wgu);
     if (L->wdT) (void)hipFree(L->wdT);
     delete L;
-    return MOE_HIP_OK;
-}
-
-// Router [d x E] from host memory: device copy, its transpose, and the
-// non-finite check that selects the zero-skipping router.
-static int upload_router(MoeHipLayer *L, const float *wr) {
-    HIP_TRY(hipMemcpyAsync(L->wr, wr, sizeof(float) * (size_t)L->d * L->E, hipMemcpyHostToDevice,
-                           g_stream));
-    HIP_TRY(moe::launch_transpose(L->wr, L->wrT, L->d, L->E, g_stream));
-    L->wr_nonfinite = 0;
-    for (size_t i = 0; i < (size_t)L->d * L->E; ++i)
-        if (!std::isfinite(wr[i])) { L->wr_nonfinite = 1; break; }
-    return MOE_HIP_OK;
-}
-
-// Expert e from host memory (reference layout) into the packed arrays,
-// through the device staging buffer (3 d F floats).
-static int upload_expert(MoeHipLayer *L, int e, const float *wg, const float *wu,
-                         const float *wd) {
-    const size_t dF = (size_t)L->d * L->F;
-    TRY(g_ws.stage.reserve(sizeof(float) * 3 * dF));
-    float *st = g_ws.stage.as<float>();
-    HIP_TRY(hipMemcpyAsync(st, wg, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
-    HIP_TRY(hipMemcpyAsync(st + dF, wu, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
-    HIP_TRY(hipMemcpyAsync(st + 2 * dF, wd, sizeof(float) * dF, hipMemcpyHostToDevice, g_stream));
-    HIP_TRY(moe::launch_pack_gateup(st, st + dF, L->wgu + 2 * dF * e, L->d, L->F, g_stream));
-    HIP_TRY(moe::launch_pack_down(st + 2 * dF, L->wdT + dF * e, L->F, L->d, g_stream));
     return MOE_HIP_OK;
 }
 
@@ -1113,7 +1169,7 @@ int moe_hip_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg
     const int T = x->rows, d = x->cols, F = cfg->ffn_hidden, E = w->n_experts, k = w->top_k;
     if (out->rows != T || out->cols != d)
         return set_err(MOE_HIP_ERR_ARG, "out is %dx%d, expected %dx%d", out->rows, out->cols, T, d);
-    TRY(check_shapes(d, F, E, k));
+    TRY(check_shapes(d, F, E, k, false));
     if (T == 0) return MOE_HIP_OK;
     if (!x->data || !out->data || !cache->router_probs || !cache->expert_ids)
         return set_err(MOE_HIP_ERR_ARG, "null data pointer");
@@ -1128,7 +1184,7 @@ int moe_hip_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg
     float *dx = g_ws.x.as<float>(), *dout = g_ws.out.as<float>(), *dprobs = g_ws.probs.as<float>();
     int *dids = g_ws.ids.as<int>();
     HIP_TRY(hipMemcpyAsync(dx, x->data, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
-    TRY(moe_hip_forward_dev(L, dx, T, dout, dprobs, dids, 0, g_stream));
+    TRY(dropin_forward(L, d, dx, T, dout, dprobs, dids, 0));
     HIP_TRY(hipMemcpyAsync(out->data, dout, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipMemcpyAsync(cache->router_probs, dprobs, sizeof(float) * (size_t)T * E,
                            hipMemcpyDeviceToHost, g_stream));
@@ -1148,7 +1204,7 @@ int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x
     if (!w || !cfg || n_rows < 0 || (n_rows > 0 && (!x_norm || !x)))
         return set_err(MOE_HIP_ERR_ARG, "bad decode arguments");
     const int d = cfg->d_model, F = cfg->ffn_hidden;
-    TRY(check_shapes(d, F, w->n_experts, w->top_k));
+    TRY(check_shapes(d, F, w->n_experts, w->top_k, false));
     if (n_rows == 0) return MOE_HIP_OK;
     TRY(ensure_init());
     MoeHipLayer *L = nullptr;
@@ -1159,7 +1215,7 @@ int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x
     float *dxn = g_ws.x.as<float>(), *dx = g_ws.out.as<float>();
     HIP_TRY(hipMemcpyAsync(dxn, x_norm, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
     HIP_TRY(hipMemcpyAsync(dx, x, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
-    TRY(moe_hip_forward_dev(L, dxn, n_rows, dx, nullptr, nullptr, 1, g_stream));
+    TRY(dropin_forward(L, d, dxn, n_rows, dx, nullptr, nullptr, 1));
     HIP_TRY(hipMemcpyAsync(x, dx, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipStreamSynchronize(g_stream));
     return MOE_HIP_OK;
@@ -1273,7 +1329,7 @@ int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,
     const Matrix &xn = cache->x_norm_ffn, &fo = cache->ffn_out;
     if (xn.rows != T || xn.cols != d || fo.rows != T || fo.cols != d)
         return set_err(MOE_HIP_ERR_ARG, "cache x_norm_ffn / ffn_out must be %dx%d", T, d);
-    TRY(check_shapes(d, F, E, k));
+    TRY(check_shapes(d, F, E, k, false));
     if (T == 0) return MOE_HIP_OK;
     if (!x->data || !xn.data || !fo.data || !cache->router_probs || !cache->expert_ids)
         return set_err(MOE_HIP_ERR_ARG, "null data pointer");
@@ -1293,7 +1349,7 @@ int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,
     HIP_TRY(hipMemcpyAsync(dx, x->data, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
     HIP_TRY(hipMemcpyAsync(dw, rms_ffn, sizeof(float) * d, hipMemcpyHostToDevice, g_stream));
     HIP_TRY(moe::launch_rms_norm(dx, dw, cfg->rms_norm_eps, T, d, dxn, g_stream));
-    TRY(moe_hip_forward_dev(L, dxn, T, dout, dprobs, dids, 0, g_stream));
+    TRY(dropin_forward(L, d, dxn, T, dout, dprobs, dids, 0));
     HIP_TRY(hipMemcpyAsync(xn.data, dxn, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipMemcpyAsync(fo.data, dout, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipMemcpyAsync(cache->router_probs, dprobs, sizeof(float) * (size_t)T * E,

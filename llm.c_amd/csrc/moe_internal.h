@@ -134,6 +134,10 @@ hipError_t launch_gemm_bwd(const GemmArgs &a, int mode, hipStream_t s);
 hipError_t launch_transpose_units(const float *src, float *dst, int R, int C, int E,
                                   hipStream_t s);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s);
+// Rows of src_cols floats into rows of dst_cols: zero-filled past src_cols,
+// or cut to the first dst_cols.
+hipError_t launch_copy_rows(const float *src, int rows, int src_cols, float *dst, int dst_cols,
+                            hipStream_t s);
 hipError_t launch_decode_gateup(const DecodeArgs &a, hipStream_t s);
 hipError_t launch_decode_down(const DecodeArgs &a, hipStream_t s);
 // The fused decode kernel with the routing inside (every workgroup routes

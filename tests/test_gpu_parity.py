@@ -545,9 +545,46 @@ def test_error_paths():
     x = orc.synth((4, 128), 0, 0, 1.0)
     with pytest.raises(mh.MoeHipError):
         mh.moe_forward(x, bad)
-    odd = host_layer(96, 512, 4, 2, 0, 0.02, 0.02)      # d_model % 64 != 0
+    many = host_layer(64, 32, 130, 2, 0, 0.02, 0.02)    # n_experts above the supported 128
     with pytest.raises(mh.MoeHipError):
-        mh.moe_forward(orc.synth((4, 96), 0, 0, 1.0), odd)
+        mh.moe_forward(orc.synth((4, 64), 0, 0, 1.0), many)
+
+
+# Widths the kernels do not tile, which the host drop-ins take by padding
+# (zeros in x and in every weight past d_model / ffn_hidden).
+ODD_WIDTHS = [
+    # name, T, d, F, E, k
+    ("d100_f70", 33, 100, 70, 5, 2),
+    ("d96", 64, 96, 512, 4, 2),         # d_model % 64 only
+    ("d130_k3", 7, 130, 96, 8, 3),      # ffn_hidden a multiple of 32: d only
+    ("f40_k1", 200, 64, 40, 6, 1),      # ffn_hidden only
+    ("d1_f1", 5, 1, 1, 3, 2),           # the narrowest layer
+]
+
+
+@pytest.mark.parametrize("name,T,d,F,E,k", ODD_WIDTHS, ids=[c[0] for c in ODD_WIDTHS])
+def test_dropins_odd_widths(name, T, d, F, E, k):
+    """moe_forward, moe_decode_batch and moe_block_ffn on widths the kernels do
+    not tile: routing bit-exact and the layer within the bars, like every
+    other shape."""
+    say(f"odd widths {name}: T={T} d={d} F={F} E={E} k={k}")
+    hw = host_layer(d, F, E, k, 17, 0.3, 0.05)
+    x = orc.synth((T, d), 17, 0, 1.0)
+    out, probs, ids = mh.moe_forward(x, hw)
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw)
+    assert np.array_equal(bits(probs), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    assert_close(out, o_ref, f"{name} moe_forward")
+    base = orc.synth((T, d), 17, 3, 1.0)
+    assert_close(mh.decode_batch(x, base, hw), base + o_ref, f"{name} moe_decode_batch")
+    w = orc.synth((d,), 17, 9, 0.1, mean=1.0)
+    x1, xn, fo, probs, ids = mh.block_ffn(x, w, hw)
+    xn_ref = orc.rms_norm(x, w, 1e-5)
+    assert np.array_equal(bits(xn), bits(xn_ref))
+    o2, p2, i2 = orc.moe_forward(xn_ref, hw)
+    assert np.array_equal(bits(probs), bits(p2))
+    assert np.array_equal(ids, i2)
+    assert_close(fo, o2, f"{name} moe_block_ffn")
 
 
 FORCED_PATH_CASES = [
