@@ -79,7 +79,7 @@ __device__ __forceinline__ void keep_regs(floatx4 a, floatx4 b, floatx4 c, float
 // Every thread of the workgroup calls this together.
 template <int MODE, int WN>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mtg, int nt, int kb,
-                                          int nk, int slot, int npieces) {
+                                          int nk, int slot, int npieces, float *part = nullptr) {
     constexpr int BN = 64 * WN;
     // Two buffers each: A as 128 rows of 32 swizzled floats, B as
     // (BN/16) x 2 packed 1 KB units (BN rows of 32 floats' worth).
@@ -268,7 +268,19 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
 
     // Accumulator layout of a 32x32 block: lane l, register r holds
     // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
-    if (MODE == 0) {
+    if (MODE == 0 && part) {
+        // A piece of a split tile: raw gate and up sums, [row][packed column].
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                int row = wm * 64 + m * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                if (row < rows)
+#pragma unroll
+                    for (int n = 0; n < 2; ++n)
+                        part[row * BN + wn * 64 + n * 32 + li] = acc[m][n][r];
+            }
+    } else if (MODE == 0) {
         const int f = ((nt * BN + wn * 64) >> 1) + li;   // feature index
 #pragma unroll
         for (int m = 0; m < 2; ++m)
@@ -336,6 +348,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
     }
 }
 
+// The split tail of a gate/up launch: whole tiles [0, dp); r tiles left over
+// (dp .. dp + r - 1), each in s pieces; r = s = 0 when the tail is not split.
+struct TailLayout { int dp, r, s; };
+__device__ __forceinline__ TailLayout tail_layout(const GemmArgs &a, int ntiles, int nks) {
+    const int live = a.tile_off[a.E] * ntiles;
+    const int g = a.tail_groups;
+    const int r = live % g;
+    const int sp = r ? min(min(nks, 4), g / r) : 0;
+    if (sp < 2) return TailLayout{live, 0, 0};
+    return TailLayout{live - r, r, sp};
+}
+
 // Grid: the (m-tile, n-tile) pairs, times the reduction splits.  Down
 // projection in stream-K form (a.streamk): workgroup g takes units
 // [g per, (g + 1) per) of the flat list of (live tile, K slice) units, per =
@@ -369,6 +393,26 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         }
         return;
     }
+    if (MODE == 0 && a.tail_groups > 0) {
+        // Whole tiles in the grid's first dp workgroups, then the pieces of
+        // the split tail: piece s of tail tile r covers K slices
+        // [s nks / S, (s + 1) nks / S).  (Grid: the m-tile bound's tiles plus
+        // tail_groups.)
+        const TailLayout tl = tail_layout(a, ntiles, nks);
+        const int b = blockIdx.x;
+        if (b < tl.dp) {
+            gemm_tile<MODE, WN>(a, smem, b / ntiles, b % ntiles, 0, nks, 0, 0);
+            return;
+        }
+        const int j = b - tl.dp;
+        if (j >= tl.r * tl.s) return;
+        const int r = j / tl.s, sp = j - r * tl.s;
+        const int tile = tl.dp + r;
+        const int k0 = sp * nks / tl.s, k1 = (sp + 1) * nks / tl.s;
+        gemm_tile<MODE, WN>(a, smem, tile / ntiles, tile % ntiles, k0 * KT, k1 - k0, 0, 0,
+                            a.tail_part + (size_t)j * BM * BN);
+        return;
+    }
     const int per_split = a.max_mtiles * ntiles;
     const int ks = blockIdx.x / per_split;       // reduction split (down projection)
     const int nt = (blockIdx.x % per_split) % ntiles;
@@ -391,7 +435,7 @@ hipError_t launch_grouped(const GemmArgs &a, hipStream_t s) {
         attr_set = true;
     }
     const int ntiles = a.N / BN;
-    dim3 grid((unsigned)(a.max_mtiles * ntiles * a.ksplit));
+    dim3 grid((unsigned)(a.max_mtiles * ntiles * a.ksplit + (MODE == 0 ? a.tail_groups : 0)));
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE, WN>), grid, dim3(128 * WN), lds, s, a);
     return hipGetLastError();
 }
@@ -572,6 +616,47 @@ __global__ __launch_bounds__(256) void zero_ints_kernel(int *p, int n) {
     for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
 }
 
+// Workgroup 8 r + q: rows 16 q .. 16 q + 15 of tail tile r of a gate/up
+// launch with a split tail, one thread per (row, 4 features).  The gate and
+// up sums are the tile's S pieces added in piece order (loads of four pieces
+// in flight at a time), then H = swiglu(gate, up).
+__global__ __launch_bounds__(512) void gateup_fixup_kernel(GemmArgs a) {
+    constexpr int BN = 256;
+    const int ntiles = a.N / BN;
+    const TailLayout tl = tail_layout(a, ntiles, a.K / KT);
+    const int r = blockIdx.x >> 3;
+    if (r >= tl.r) return;
+    const int tile = tl.dp + r, mtg = tile / ntiles, nt = tile - mtg * ntiles;
+    const int e = a.tile_expert[mtg];
+    const int row0 = a.offsets[e] + (mtg - a.tile_off[e]) * BM;
+    const int rows = min(BM, a.offsets[e + 1] - row0);
+    const int row = 16 * (blockIdx.x & 7) + (threadIdx.x >> 5);
+    if (row >= rows) return;
+    const int g = (threadIdx.x >> 3) & 3, c = (threadIdx.x & 7) * 4;
+    const float *src = a.tail_part + (size_t)r * tl.s * BM * BN + row * BN + 64 * g + c;
+    constexpr size_t PS = (size_t)BM * BN;   // floats per piece
+    floatx4 gs = {0.f, 0.f, 0.f, 0.f}, us = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < tl.s; s0 += 4) {
+        floatx4 gv[4], uv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (s0 + q < tl.s) {
+                gv[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS);
+                uv[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS + 32);
+            }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (s0 + q < tl.s) {
+                if (s0 + q == 0) { gs = gv[0]; us = uv[0]; }
+                else { gs += gv[q]; us += uv[q]; }
+            }
+    }
+    floatx4 h;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) h[q] = swiglu_fast(gs[q], us[q]);
+    *reinterpret_cast<floatx4 *>(a.c + (size_t)(row0 + row) * a.ldc + nt * (BN / 2) + 32 * g + c) = h;
+}
+
 }  // namespace
 
 // Compute units of the current device (cached; 256 on MI355X).
@@ -643,7 +728,26 @@ DownPlan down_plan(int N, int K, int max_mtiles, size_t n) {
     return p;
 }
 
-hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) { return launch_mode<0>(a, s); }
+int gateup_tail_groups(int N, int K, int max_mtiles) {
+    const GemmPlan g = gemm_plan(N, K, max_mtiles, false);
+    const long cus = device_cus();
+    if (g.bn != 256 || K % KT || K / KT < 2 || (long)max_mtiles * (N / 256) >= 4 * cus) return 0;
+    return (int)cus;
+}
+
+hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) {
+    if (a.tail_groups > 0 && (!a.tail_part || a.N % 256 || a.K % KT ||
+                              gemm_plan(a.N, a.K, a.max_mtiles, false).bn != 256))
+        return hipErrorInvalidValue;
+    return launch_mode<0>(a, s);
+}
+
+hipError_t launch_gateup_fixup(const GemmArgs &a, hipStream_t s) {
+    if (a.tail_groups <= 0) return hipSuccess;
+    if (!a.tail_part || a.N % 256 || a.ldc % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gateup_fixup_kernel, dim3((unsigned)a.tail_groups * 8), dim3(512), 0, s, a);
+    return hipGetLastError();
+}
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) {
     if (!a.streamk) return launch_mode<1>(a, s);
     if (!a.pieces || a.sk_groups <= 0 || a.N % 256 || a.K % KT) return hipErrorInvalidValue;

@@ -134,11 +134,11 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, pieces,
-        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork, xpad;
+        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork, xpad, gu_part;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
                          &tile_expert, &perm, &h, &ys, &pieces, &stage, &counters, &xn, &rmsw,
-                         &aq, &ao, &apart, &acnt, &bw, &bwork, &xpad};
+                         &aq, &ao, &apart, &acnt, &bw, &bwork, &xpad, &gu_part};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -870,6 +870,8 @@ struct FwdPlan {
     size_t h_floats = 0;    // H [n x F] (grouped GEMMs, unfused decode)
     size_t ys_floats = 0;   // per-slot products / split-K partials
     size_t pieces_ints = 0; // stream-K piece counts [n][d / 256]
+    int gu_tail = 0;        // gate/up split tail: workgroups per round (moe::gateup_tail_groups)
+    size_t gu_part_floats = 0;  // its pieces
 };
 
 // The device buffers of one forward.
@@ -880,6 +882,7 @@ struct FwdBufs {
     int *perm = nullptr;    // [n]
     float *h = nullptr, *ys = nullptr;
     int *pieces = nullptr;     // [n][d / 256] (stream-K down projection)
+    float *gu_part = nullptr;  // gate/up split-tail pieces
     int *counters = nullptr;   // kMaxCounters ints, zero between launches
 };
 
@@ -919,6 +922,8 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
         p->streamk = dp.streamk;
         p->sk_groups = dp.groups;
         p->pieces_ints = dp.streamk ? n * (size_t)(d / 256) : 0;
+        p->gu_tail = moe::gateup_tail_groups(2 * F, d, p->max_mtiles);
+        p->gu_part_floats = (size_t)p->gu_tail * moe::kGemmBM * 256;
         p->h_floats = n * F;
         p->ys_floats = (size_t)p->ksplit * n * d;
     }
@@ -937,12 +942,14 @@ int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
     if (p.h_floats) TRY(g_ws.h.reserve(sizeof(float) * p.h_floats));
     TRY(g_ws.ys.reserve(sizeof(float) * p.ys_floats));
     if (p.pieces_ints) TRY(g_ws.pieces.reserve(sizeof(int) * p.pieces_ints));
+    if (p.gu_part_floats) TRY(g_ws.gu_part.reserve(sizeof(float) * p.gu_part_floats));
     TRY(ensure_counters());
     b->ids = g_ws.ids.as<int>(); b->gw = g_ws.gw.as<float>();
     b->counts = g_ws.counts.as<int>(); b->offsets = g_ws.offsets.as<int>();
     b->tile_off = g_ws.tile_off.as<int>(); b->tile_expert = g_ws.tile_expert.as<int>();
     b->perm = g_ws.perm.as<int>(); b->h = g_ws.h.as<float>(); b->ys = g_ws.ys.as<float>();
     b->pieces = p.pieces_ints ? g_ws.pieces.as<int>() : nullptr;
+    b->gu_part = p.gu_part_floats ? g_ws.gu_part.as<float>() : nullptr;
     b->counters = g_ws.counters.as<int>();
     return MOE_HIP_OK;
 }
@@ -970,6 +977,7 @@ void carve_bufs(const MoeHipLayer *L, const FwdPlan &p, char *base, size_t cap, 
     c.h = p.h_floats ? static_cast<float *>(take(sizeof(float) * p.h_floats)) : nullptr;
     c.ys = static_cast<float *>(take(sizeof(float) * p.ys_floats));
     c.pieces = p.pieces_ints ? static_cast<int *>(take(sizeof(int) * p.pieces_ints)) : nullptr;
+    c.gu_part = p.gu_part_floats ? static_cast<float *>(take(sizeof(float) * p.gu_part_floats)) : nullptr;
     *need = off;
     if (off <= cap) *b = c;
 }
@@ -1046,7 +1054,10 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
     } else {
         moe::GemmArgs gu{x, b.perm, k, L->wgu, b.h, b.offsets, b.tile_off, b.tile_expert, E, d,
                          2 * F, F, p.max_mtiles};
+        gu.tail_groups = p.gu_tail;
+        gu.tail_part = b.gu_part;
         HIP_TRY(moe::launch_gemm_gateup(gu, s));
+        HIP_TRY(moe::launch_gateup_fixup(gu, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[3], s));
         moe::GemmArgs dn{b.h, b.perm, k, L->wdT, b.ys, b.offsets, b.tile_off, b.tile_expert, E, F,
                          d, d, p.max_mtiles};

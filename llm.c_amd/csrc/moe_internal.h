@@ -84,6 +84,14 @@ struct GemmArgs {
     // Backward epilogues: mode 2 also writes H = swiglu(G, U) to c2.
     float *c2 = nullptr;
     int ldc2 = 0;
+    // Gate/up with a split tail (gateup_tail_groups): the whole rounds of
+    // tail_groups workgroups take whole tiles; the R tiles left over are
+    // split along the reduction into S = min(K / 32, 4, tail_groups / R)
+    // pieces (when S >= 2), which write their raw gate and up sums to
+    // tail_part [R * S][128][256]; launch_gateup_fixup adds the pieces in
+    // order and writes H.
+    int tail_groups = 0;
+    float *tail_part = nullptr;
 };
 
 struct CombineArgs {
@@ -122,6 +130,9 @@ constexpr size_t kFusedPartialBytes = (size_t)32 << 20;
 
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);
+// The split tail's pieces of a gate/up launch with tail_groups > 0 added in
+// order, swiglu applied, written to H (same stream, after the gate/up).
+hipError_t launch_gateup_fixup(const GemmArgs &a, hipStream_t s);
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s);
 // The backward's tile epilogues (gemm.hip), no reduction split:
 //   mode 2  gate/up rows gathered like the forward: c = [G | U] per 32-feature
@@ -256,5 +267,10 @@ struct DownPlan {
     int bn, slots, streamk, groups;
 };
 DownPlan down_plan(int N, int K, int max_mtiles, size_t n);
+// Workgroups per round for a gate/up launch with a split tail (the CUs), or
+// 0 for whole tiles only: used when 256-column tiles make fewer than 4
+// rounds, where the last, partial round is a large share of the launch.
+// The pieces take at most kGemmBM * 256 * groups floats.
+int gateup_tail_groups(int N, int K, int max_mtiles);
 
 }  // namespace moe

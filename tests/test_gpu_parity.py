@@ -240,6 +240,55 @@ def test_forward_dev_configs(name):
     layer.close()
 
 
+def gateup_tail(ids, E, ntiles, nks, groups=256):
+    """The gate/up launch's split tail for these routes: (live tiles, tail
+    tiles R, pieces per tail tile S); R = S = 0 when it is not split."""
+    counts = np.bincount(ids.ravel(), minlength=E)
+    live = int(((counts + 127) // 128).sum()) * ntiles
+    r = live % groups
+    s = min(nks, 4, groups // r) if r else 0
+    return (live, r, s) if s >= 2 else (live, 0, 0)
+
+
+@pytest.mark.parametrize("T", [1500, 2000, 2500, 2600, 4096])
+def test_gateup_split_tail(T):
+    """Small layers (256-column tiles in fewer than 4 rounds of the CUs):
+    the tiles past the last whole round are split along d into 2-4 pieces
+    whose sums a second kernel adds in order.  Every tail layout the token
+    counts give (also none) matches the oracle."""
+    d, F, E, k = 256, 1024, 8, 2
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(17, 0.1, 0.02)
+    hw = host_layer(d, F, E, k, 17, 0.1, 0.02)
+    x = orc.synth((T, d), 17, 0, 1.0)
+    dx = mh.DeviceArray.from_host(x)
+    dout = mh.DeviceArray((T, d))
+    dprobs = mh.DeviceArray((T, E))
+    dids = mh.DeviceArray((T, k), np.int32)
+    layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+    mh.synchronize()
+    ids = dids.to_host()
+    say(f"split tail T={T}: (live tiles, tail tiles, pieces) = {gateup_tail(ids, E, 2 * F // 256, d // 32)}")
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw, nthreads=16)
+    assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    assert_close(dout.to_host(), o_ref, f"split tail T={T}")
+    layer.close()
+
+
+def test_gateup_split_tail_layouts_covered():
+    """The token counts of test_gateup_split_tail's cases (routes from the
+    oracle, no GPU work) give tails of 2, 3 and 4 pieces and one unsplit."""
+    d, F, E, k = 256, 1024, 8, 2
+    wr, _ = orc.synth_layer_host(d, F, E, k, 17, 0.1, 0.02)
+    seen = set()
+    for T in (1500, 2000, 2500, 2600, 4096):
+        _, ids, _ = orc.route(orc.synth((T, d), 17, 0, 1.0), wr, k)
+        seen.add(gateup_tail(ids, E, 2 * F // 256, d // 32)[2])
+    say(f"split tail piece counts seen: {sorted(seen)}")
+    assert {0, 2, 3, 4} <= seen
+
+
 @pytest.mark.parametrize("accumulate", [0, 1])
 def test_forward_large_skewed(accumulate):
     """A large layer (T k = 32768 routed rows), every token against the
