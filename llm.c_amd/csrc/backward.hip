@@ -599,6 +599,12 @@ unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 25
 
 bool backward_engine_ok(int d, int F) { return d % 64 == 0 && F % 64 == 0; }
 
+size_t backward_tail_floats(int d, int F, int max_mtiles) {
+    if (!backward_engine_ok(d, F)) return 0;
+    const int g = std::max(gateup_tail_groups(2 * F, d, max_mtiles), gateup_tail_groups(F, d, max_mtiles));
+    return (size_t)g * kGemmBM * 256;
+}
+
 int backward_slot_splits(int d, int F, int max_mtiles, size_t n) {
     if (!backward_engine_ok(d, F)) return 1;
     return std::max(down_plan(d, F, max_mtiles, n).slots, down_plan(d, 2 * F, max_mtiles, n).slots);
@@ -639,7 +645,12 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         GemmArgs gu = g;
         gu.a = b.x; gu.b = b.wgu; gu.c = GU; gu.K = d; gu.N = 2 * F; gu.ldc = 2 * F;
         gu.c2 = b.H; gu.ldc2 = F;
+        if (b.tail_part) {
+            gu.tail_groups = gateup_tail_groups(2 * F, d, b.max_mtiles);
+            gu.tail_part = b.tail_part;
+        }
         BWD_TRY(launch_gemm_bwd(gu, 2, s));
+        BWD_TRY(launch_tail_fixup(gu, 2, s));
         // (Y and dX: down-projection shapes, by slot with split partials or
         // stream-K pieces, moe::down_plan; one piece-count table serves both
         // in turn.)
@@ -655,7 +666,12 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         // dH -> dG, dU in place over GU; dXr = dGU wgu^T by slot (over Y).
         GemmArgs gh = g;
         gh.a = b.dY; gh.b = b.wdTT; gh.c = GU; gh.K = d; gh.N = F; gh.ldc = 2 * F;
+        if (b.tail_part) {
+            gh.tail_groups = gateup_tail_groups(F, d, b.max_mtiles);
+            gh.tail_part = b.tail_part;
+        }
         BWD_TRY(launch_gemm_bwd(gh, 3, s));
+        BWD_TRY(launch_tail_fixup(gh, 3, s));
         const DownPlan px = down_plan(d, 2 * F, b.max_mtiles, n);
         GemmArgs gx = g;
         gx.a = GU; gx.b = b.wguT; gx.c = b.Y; gx.K = 2 * F; gx.N = d; gx.ldc = d;

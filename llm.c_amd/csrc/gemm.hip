@@ -268,8 +268,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
 
     // Accumulator layout of a 32x32 block: lane l, register r holds
     // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
-    if (MODE == 0 && part) {
-        // A piece of a split tile: raw gate and up sums, [row][packed column].
+    if (MODE != 1 && part) {
+        // A piece of a split tile: raw sums, [row][tile column].
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -393,7 +393,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
         }
         return;
     }
-    if (MODE == 0 && a.tail_groups > 0) {
+    if (MODE != 1 && a.tail_groups > 0) {
         // Whole tiles in the grid's first dp workgroups, then the pieces of
         // the split tail: piece s of tail tile r covers K slices
         // [s nks / S, (s + 1) nks / S).  (Grid: the m-tile bound's tiles plus
@@ -435,7 +435,7 @@ hipError_t launch_grouped(const GemmArgs &a, hipStream_t s) {
         attr_set = true;
     }
     const int ntiles = a.N / BN;
-    dim3 grid((unsigned)(a.max_mtiles * ntiles * a.ksplit + (MODE == 0 ? a.tail_groups : 0)));
+    dim3 grid((unsigned)(a.max_mtiles * ntiles * a.ksplit + (MODE != 1 ? a.tail_groups : 0)));
     hipLaunchKernelGGL((grouped_gemm_kernel<MODE, WN>), grid, dim3(128 * WN), lds, s, a);
     return hipGetLastError();
 }
@@ -616,11 +616,13 @@ __global__ __launch_bounds__(256) void zero_ints_kernel(int *p, int n) {
     for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
 }
 
-// Workgroup 8 r + q: rows 16 q .. 16 q + 15 of tail tile r of a gate/up
-// launch with a split tail, one thread per (row, 4 features).  The gate and
-// up sums are the tile's S pieces added in piece order (loads of four pieces
-// in flight at a time), then H = swiglu(gate, up).
-__global__ __launch_bounds__(512) void gateup_fixup_kernel(GemmArgs a) {
+// Workgroup 8 r + q: rows 16 q .. 16 q + 15 of tail tile r of a launch with
+// a split tail, one thread per (row, 4 columns in each 32-column half of a
+// 64-column group).  The sums are the tile's S pieces added in piece order
+// (loads of four pieces in flight at a time); the tile engine's epilogue of
+// MODE then runs on them.
+template <int MODE>
+__global__ __launch_bounds__(512) void tail_fixup_kernel(GemmArgs a) {
     constexpr int BN = 256;
     const int ntiles = a.N / BN;
     const TailLayout tl = tail_layout(a, ntiles, a.K / KT);
@@ -635,26 +637,60 @@ __global__ __launch_bounds__(512) void gateup_fixup_kernel(GemmArgs a) {
     const int g = (threadIdx.x >> 3) & 3, c = (threadIdx.x & 7) * 4;
     const float *src = a.tail_part + (size_t)r * tl.s * BM * BN + row * BN + 64 * g + c;
     constexpr size_t PS = (size_t)BM * BN;   // floats per piece
-    floatx4 gs = {0.f, 0.f, 0.f, 0.f}, us = {0.f, 0.f, 0.f, 0.f};
+    // v0: columns 64 g + c .., v1: 32 further (gate and up, or dH of two
+    // feature runs for MODE 3).
+    floatx4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < tl.s; s0 += 4) {
-        floatx4 gv[4], uv[4];
+        floatx4 p0[4], p1[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (s0 + q < tl.s) {
-                gv[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS);
-                uv[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS + 32);
+                p0[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS);
+                p1[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS + 32);
             }
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (s0 + q < tl.s) {
-                if (s0 + q == 0) { gs = gv[0]; us = uv[0]; }
-                else { gs += gv[q]; us += uv[q]; }
+                if (s0 + q == 0) { v0 = p0[0]; v1 = p1[0]; }
+                else { v0 += p0[q]; v1 += p1[q]; }
             }
     }
-    floatx4 h;
+    const size_t p = (size_t)(row0 + row);
+    if (MODE == 0 || MODE == 2) {
+        // Gate (v0) and up (v1) of features 128 nt + 32 g + c ..
+        floatx4 h;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) h[q] = swiglu_fast(gs[q], us[q]);
-    *reinterpret_cast<floatx4 *>(a.c + (size_t)(row0 + row) * a.ldc + nt * (BN / 2) + 32 * g + c) = h;
+        for (int q = 0; q < 4; ++q) h[q] = swiglu_fast(v0[q], v1[q]);
+        if (MODE == 0) {
+            *reinterpret_cast<floatx4 *>(a.c + p * a.ldc + nt * (BN / 2) + 32 * g + c) = h;
+        } else {
+            float *gu = a.c + p * a.ldc + nt * BN + 64 * g + c;
+            *reinterpret_cast<floatx4 *>(gu) = v0;
+            *reinterpret_cast<floatx4 *>(gu + 32) = v1;
+            *reinterpret_cast<floatx4 *>(a.c2 + p * a.ldc2 + nt * (BN / 2) + 32 * g + c) = h;
+        }
+    } else {
+        // dH of features 256 nt + 64 g + 32 n + c .. (n = 0: v0, 1: v1); the
+        // gate and up values of feature f sit at packed columns
+        // 64 (f / 32) + f % 32 and 32 past it, replaced by dG and dU.
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            float *gu = a.c + p * a.ldc + 2 * (nt * BN + 64 * g) + 64 * n + c;
+            const floatx4 dhv = n ? v1 : v0;
+            floatx4 gv = *reinterpret_cast<const floatx4 *>(gu);
+            floatx4 uv = *reinterpret_cast<const floatx4 *>(gu + 32);
+            floatx4 dg, du;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float gq = gv[q], uq = uv[q], dh = dhv[q];
+                const float sg = 1.0f / (1.0f + expf(-gq));
+                dg[q] = dh * uq * fmaf(gq * sg, 1.0f - sg, sg);
+                du[q] = dh * gq * sg;
+            }
+            *reinterpret_cast<floatx4 *>(gu) = dg;
+            *reinterpret_cast<floatx4 *>(gu + 32) = du;
+        }
+    }
 }
 
 }  // namespace
@@ -742,12 +778,20 @@ hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s) {
     return launch_mode<0>(a, s);
 }
 
-hipError_t launch_gateup_fixup(const GemmArgs &a, hipStream_t s) {
+hipError_t launch_tail_fixup(const GemmArgs &a, int mode, hipStream_t s) {
     if (a.tail_groups <= 0) return hipSuccess;
-    if (!a.tail_part || a.N % 256 || a.ldc % 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gateup_fixup_kernel, dim3((unsigned)a.tail_groups * 8), dim3(512), 0, s, a);
+    if (!a.tail_part || a.N % 256 || a.ldc % 4 || (mode == 2 && a.ldc2 % 4)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)a.tail_groups * 8);
+    switch (mode) {
+        case 0: hipLaunchKernelGGL(tail_fixup_kernel<0>, grid, dim3(512), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(tail_fixup_kernel<2>, grid, dim3(512), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(tail_fixup_kernel<3>, grid, dim3(512), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
+
+hipError_t launch_gateup_fixup(const GemmArgs &a, hipStream_t s) { return launch_tail_fixup(a, 0, s); }
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) {
     if (!a.streamk) return launch_mode<1>(a, s);
     if (!a.pieces || a.sk_groups <= 0 || a.N % 256 || a.K % KT) return hipErrorInvalidValue;
@@ -767,6 +811,7 @@ hipError_t launch_gemm_bwd(const GemmArgs &a, int mode, hipStream_t s) {
     if (a.ksplit != 1) return hipErrorInvalidValue;
     const GemmPlan pl = gemm_plan(a.N, a.K, a.max_mtiles, false);
     if (a.K % KT || (mode != 2 && mode != 3)) return hipErrorInvalidValue;
+    if (a.tail_groups > 0 && (!a.tail_part || a.N % 256 || pl.bn != 256)) return hipErrorInvalidValue;
 #define MOE_BWD_CASE(M)                                              \
     switch (pl.bn) {                                                 \
         case 256: return launch_grouped<M, 4>(a, s);                 \

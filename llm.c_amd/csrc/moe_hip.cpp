@@ -1285,13 +1285,17 @@ int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dou
     const size_t nF = n * F, nd = n * d;
     const size_t ysplits = (size_t)moe::backward_slot_splits(d, F, max_mtiles, n);
     const size_t npieces = engine && d % 256 == 0 ? n * (size_t)(d / 256) : 0;
-    TRY(g_ws.bwork.reserve(sizeof(float) *
-                           (4 * nF + (ysplits + 1) * nd + 2 * n + (size_t)T * E + npieces)));
+    const size_t ntail = moe::backward_tail_floats(d, F, max_mtiles);
+    // (the split-tail pieces last, 256-byte aligned)
+    const size_t tail_off = (4 * nF + (ysplits + 1) * nd + 2 * n + (size_t)T * E + npieces + 63) &
+                            ~(size_t)63;
+    TRY(g_ws.bwork.reserve(sizeof(float) * (tail_off + ntail)));
     float *G = g_ws.bwork.as<float>(), *U = G + nF, *H = U + nF, *dH = H + nF;
     float *Y = dH + nF, *dY = Y + ysplits * nd, *dgw = dY + nd;
     int *inv = reinterpret_cast<int *>(dgw + n);
     float *dlogits = reinterpret_cast<float *>(inv + n);
     int *pieces = npieces ? reinterpret_cast<int *>(dlogits + (size_t)T * E) : nullptr;
+    float *tail = ntail ? G + tail_off : nullptr;
     moe::BackwardArgs b{};
     b.x = x; b.dout = dout; b.wr = L->wr; b.wrT = L->wrT;
     if (engine) {
@@ -1309,6 +1313,7 @@ int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dou
     b.G = G; b.U = U; b.H = H; b.dH = dH; b.Y = Y; b.dY = dY; b.dgw = dgw; b.dlogits = dlogits;
     b.inv = inv;
     b.pieces = pieces;
+    b.tail_part = tail;
     b.dx = dx; b.dwr = dw_router; b.dwg = dw_gate; b.dwu = dw_up; b.dwd = dw_down;
     b.aux = aux_loss; b.accumulate = accumulate ? 1 : 0;
     HIP_TRY(moe::launch_moe_backward(b, s));

@@ -133,6 +133,9 @@ hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);
 // The split tail's pieces of a gate/up launch with tail_groups > 0 added in
 // order, swiglu applied, written to H (same stream, after the gate/up).
 hipError_t launch_gateup_fixup(const GemmArgs &a, hipStream_t s);
+// The same for a tile-engine launch of mode 0, 2 or 3 (launch_gemm_bwd):
+// the pieces' sums go through that mode's epilogue.
+hipError_t launch_tail_fixup(const GemmArgs &a, int mode, hipStream_t s);
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s);
 // The backward's tile epilogues (gemm.hip), no reduction split:
 //   mode 2  gate/up rows gathered like the forward: c = [G | U] per 32-feature
@@ -229,6 +232,9 @@ struct BackwardArgs {
     float *G, *U, *H, *dH, *Y, *dY, *dgw, *dlogits;
     int *inv;
     int *pieces = nullptr;   // [n][d / 256] when a down_plan is stream-K
+    // Split-tail pieces of the GU recompute and dH products (engine path),
+    // backward_tail_floats(...) floats, or null for whole tiles only.
+    float *tail_part = nullptr;
     float *dx, *dwr, *dwg, *dwu, *dwd, *aux;
     int accumulate;
 };
@@ -238,6 +244,8 @@ bool backward_engine_ok(int d, int F);
 // Partial products per slot row the engine path leaves in Y (1 otherwise);
 // n = T * k.
 int backward_slot_splits(int d, int F, int max_mtiles, size_t n);
+// Floats of BackwardArgs::tail_part the engine path uses (0: none).
+size_t backward_tail_floats(int d, int F, int max_mtiles);
 
 // rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,

@@ -172,6 +172,24 @@ def test_backward_device_vs_oracle(shape, aux_coef):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T", [4096, 2500], ids=["t4096", "t2500"])
+def test_backward_device_split_tail(T):
+    """The batch-8x512 shape (256-column tiles in fewer than 4 rounds): the
+    GU recompute and the dH product split their last tiles along d into
+    pieces a fixup adds (GU, H, then dG, dU in place)."""
+    d, F, E, k = 256, 1024, 8, 2
+    print(f"[gpu-test] backward split tail d={d} F={F} E={E} k={k} T={T}", flush=True)
+    res, x, dout, wr, wg, wu, wd = run_device_backward(d, F, E, k, T, 41, 0.5)
+    hw_ids = orc.route(x, wr, k)[1]
+    g = mb.moe_backward64(x, wr, wg, wu, wd, hw_ids, dout, 0.5)
+    for name in ("dx", "dwr", "dwg", "dwu", "dwd"):
+        rel = orc.rel_l2(res[name], g[name])
+        print(f"[gpu-test]   {name}: rel-L2 {rel:.3e}", flush=True)
+        assert rel <= 1e-5, name
+    assert abs(res["aux"] - g["aux"]) <= 1e-5 * max(1.0, abs(g["aux"]))
+
+
+@pytest.mark.gpu
 def test_backward_deterministic_and_accumulates():
     """Same bits on a repeat; accumulate = 1 adds a second pass exactly."""
     a, *_ = run_device_backward(128, 256, 4, 2, 200, 5, 0.3)
