@@ -54,6 +54,10 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = kGemmBM;   // 128
 constexpr int KT = 32;
+// LDS buffers per operand: three for 256-column tiles (144 KB, one
+// workgroup per CU either way), two for narrower tiles (whose workgroups
+// share a CU).
+constexpr int gemm_stages(int wn) { return wn == 4 ? 3 : 2; }
 
 // One wave instruction of LDS DMA: lane i's 16 bytes at g go to LDS byte
 // address lds + 16 i (lds wave-uniform, passed in M0).  Written as asm: the
@@ -81,10 +85,11 @@ template <int MODE, int WN>
 __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mtg, int nt, int kb,
                                           int nk, int slot, int npieces, float *part = nullptr) {
     constexpr int BN = 64 * WN;
-    // Two buffers each: A as 128 rows of 32 swizzled floats, B as
+    constexpr int ST = gemm_stages(WN);
+    // ST buffers each: A as 128 rows of 32 swizzled floats, B as
     // (BN/16) x 2 packed 1 KB units (BN rows of 32 floats' worth).
     float *As = smem;
-    float *Bs = smem + 2 * BM * KT;
+    float *Bs = smem + ST * BM * KT;
     const int e = a.tile_expert[mtg];
     const int row0 = a.offsets[e] + (mtg - a.tile_off[e]) * BM;
     const int rows = min(BM, a.offsets[e + 1] - row0);
@@ -141,7 +146,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
 #pragma unroll
         for (int i = 0; i < BUW; ++i)
             gemm_dma16(b_src[i] + (size_t)16 * k0,
-                       lds0 + 4u * (2 * BM * KT + buf * BN * KT + (wu * BUW + i) * 256));
+                       lds0 + 4u * (ST * BM * KT + buf * BN * KT + (wu * BUW + i) * 256));
+    };
+    // Slice j of the tile into buffer j % ST.  With three buffers slice
+    // kt + 2 is issued during slice kt, so before the barrier that ends
+    // slice kt only the wave's newest NDMA transfers may still be in
+    // flight.
+    constexpr int NDMA = AUW + BUW;
+    auto dma = [&](int j, int buf) {
+        adma(kb + j * KT, buf);
+        bdma(kb + j * KT, buf);
+    };
+    auto wait_next = [&](int kt) {
+        if (ST == 3 && kt + 2 < nk) GEMM_WAIT_VMCNT(NDMA);
+        else GEMM_WAIT_VMCNT(0);
     };
 
     floatx16 acc[2][2];
@@ -152,9 +170,13 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[m][n][r] = 0.0f;
 
-    adma(kb, 0);
-    bdma(kb, 0);
-    GEMM_WAIT_VMCNT(0);
+    dma(0, 0);
+    if (ST == 3 && nk > 1) {
+        dma(1, 1);
+        GEMM_WAIT_VMCNT(NDMA);
+    } else {
+        GEMM_WAIT_VMCNT(0);
+    }
     __syncthreads();
     // Row (li) of this lane's A blocks has r % 8 = li % 8: the 16-byte chunk
     // 4 lh + q of K step q sits at 4 ((4 lh + q) ^ (li % 8)) floats.
@@ -165,10 +187,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
         // Set q holds quarter-step q's fragments (a0, a1 of the two 32-row
         // blocks, b0, b1 of the two 32-column blocks).  Order per slice:
         // read set 1, MFMAs of set 0, read set 2, MFMAs of set 1, read set 3,
-        // MFMAs of set 2, wait for the next slice, barrier, read the next
-        // slice's set 0, MFMAs of set 3.  keep() holds set q's registers
-        // until the following quarter's MFMAs have issued: they wait on set
-        // q's results, so by then no MFMA reads set q and it can be refilled.
+        // issue the DMA of slice kt + ST - 1, MFMAs of set 2, wait for the
+        // next slice, barrier, read the next slice's set 0, MFMAs of set 3.
+        // keep() holds set q's registers until the following quarter's
+        // MFMAs have issued: they wait on set q's results, so by then no
+        // MFMA reads set q and it can be refilled.  The DMA goes out after
+        // the slice's last fragment reads: LDS reads issued behind an LDS
+        // DMA of the same wave measured slower (the loop took 3 % longer
+        // with the DMA at the top of the slice).
         floatx4 fa0[4], fa1[4], fb0[4], fb1[4];
         const float *ap = As + (wm * 64 + li) * KT;
         const float *bp = Bs + ((wn * 4 + (li >> 4)) * 2 + lh) * 256 + (li & 15) * 4;
@@ -202,10 +228,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
         // barriers keep the reads ahead of the MFMAs they overlap.
         auto slice = [&](int kt, auto bufc) {
             constexpr int buf = decltype(bufc)::value;
-            if (kt + 1 < nk) {
-                adma(kb + (kt + 1) * KT, buf ^ 1);
-                bdma(kb + (kt + 1) * KT, buf ^ 1);
-            }
             rd(bufc, Q1{});
             __builtin_amdgcn_sched_barrier(0);
             mm(Q0{});
@@ -218,12 +240,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
             __builtin_amdgcn_sched_barrier(0);
             rd(bufc, Q3{});
             __builtin_amdgcn_sched_barrier(0);
+            if (kt + ST - 1 < nk) dma(kt + ST - 1, (buf + ST - 1) % ST);
+            __builtin_amdgcn_sched_barrier(0);
             mm(Q2{});
             keep(Q1{});
             __builtin_amdgcn_sched_barrier(0);
-            GEMM_WAIT_VMCNT(0);   // the next slice has landed
+            wait_next(kt);   // slice kt + 1 has landed
             __syncthreads();
-            if (kt + 1 < nk) rd(std::integral_constant<int, buf ^ 1>{}, Q0{});
+            if (kt + 1 < nk) rd(std::integral_constant<int, (buf + 1) % ST>{}, Q0{});
             __builtin_amdgcn_sched_barrier(0);
             mm(Q3{});
             keep(Q2{});
@@ -232,20 +256,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
 #pragma unroll
         for (int q = 1; q < 4; ++q) fa0[q] = fa1[q] = fb0[q] = fb1[q] = floatx4{0.f, 0.f, 0.f, 0.f};
         rd(Q0{}, Q0{});
-        for (int kt = 0; kt < nk; kt += 2) {
+        for (int kt = 0; kt < nk; kt += ST) {
             slice(kt, Q0{});
             if (kt + 1 < nk) slice(kt + 1, Q1{});
+            if (ST == 3 && kt + 2 < nk) slice(kt + 2, std::integral_constant<int, 2 % ST>{});
         }
     } else {
         // One 32-row block (the expert's last, short tile) or none.
         for (int kt = 0; kt < nk; ++kt) {
-            const int buf = kt & 1;
-            // The next slice into the other buffer (free since the barrier
-            // that ended step kt - 1), in flight while this one is multiplied.
-            if (kt + 1 < nk) {
-                adma(kb + (kt + 1) * KT, buf ^ 1);
-                bdma(kb + (kt + 1) * KT, buf ^ 1);
-            }
+            const int buf = kt % ST;
+            // Slice kt + ST - 1 into the buffer slice kt - 1 used (free since
+            // the barrier that ended slice kt - 1), in flight meanwhile.
+            if (kt + ST - 1 < nk) dma(kt + ST - 1, (kt + ST - 1) % ST);
             const float *as = As + buf * BM * KT + (wm * 64 + li) * KT;
             const float *bs = Bs + buf * BN * KT + ((wn * 4 + (li >> 4)) * 2 + lh) * 256 + (li & 15) * 4;
             if (nmb == 1) {
@@ -261,7 +283,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &a, float *smem, int mt
                     }
                 }
             }
-            GEMM_WAIT_VMCNT(0);   // the next slice has landed
+            wait_next(kt);   // slice kt + 1 has landed
             __syncthreads();
         }
     }
@@ -425,7 +447,7 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
 template <int MODE, int WN>
 hipError_t launch_grouped(const GemmArgs &a, hipStream_t s) {
     constexpr int BN = 64 * WN;
-    const size_t lds = (size_t)(2 * BM + 2 * BN) * KT * sizeof(float);
+    const size_t lds = (size_t)gemm_stages(WN) * (BM + BN) * KT * sizeof(float);
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t err = hipFuncSetAttribute(
@@ -795,7 +817,7 @@ hipError_t launch_gateup_fixup(const GemmArgs &a, hipStream_t s) { return launch
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) {
     if (!a.streamk) return launch_mode<1>(a, s);
     if (!a.pieces || a.sk_groups <= 0 || a.N % 256 || a.K % KT) return hipErrorInvalidValue;
-    constexpr size_t lds = (size_t)(2 * BM + 2 * 256) * KT * sizeof(float);
+    constexpr size_t lds = (size_t)gemm_stages(4) * (BM + 256) * KT * sizeof(float);
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void *>(&grouped_gemm_kernel<1, 4>),
