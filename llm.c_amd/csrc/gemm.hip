@@ -20,12 +20,13 @@
 //
 // Each workgroup computes a 128 x (64*WN) tile with 2 x WN waves of 64 x 64.
 // A wave issues v_mfma_f32_32x32x2f32 on 2 x 2 sub-tiles.  K is staged
-// through double-buffered LDS in 32-wide slices; a lane of half h (lane/32)
-// feeds the MFMA's k-row h with the slice's elements 16h..16h+15 in turn, so
-// both operands come from LDS as 128-bit reads.
+// through LDS in 32-wide slices (three buffers for 256-column tiles, two for
+// narrower ones); a lane of half h (lane/32) feeds the MFMA's k-row h with
+// the slice's elements 16h..16h+15 in turn, so both operands come from LDS
+// as 128-bit reads.
 // Both operands go global -> LDS by DMA (global_load_lds_dwordx4, one wave
-// instruction = 64 lanes x 16 bytes into 1 KB of LDS), one slice ahead of
-// the MFMAs: no registers or LDS store instructions carry the tiles.
+// instruction = 64 lanes x 16 bytes into 1 KB of LDS), one or two slices
+// ahead of the MFMAs: no registers or LDS store instructions carry the tiles.
 //   B  the packed 1 KB units are copied whole (unit layout in LDS);
 //   A  a unit is 8 whole gathered rows (128 B each, full cache lines), each
 //      row's eight 16-byte chunks permuted by XOR with row % 8 so the
