@@ -354,75 +354,173 @@ __global__ __launch_bounds__(256) void reduce_gemm_kernel(ReduceGemm g) {
     }
 }
 
-// The same product on the matrix cores for M, N multiples of 64 and the
-// experts' row ranges: a 64 x 64 tile per workgroup, 4 waves of 32 x 32
-// (v_mfma_f32_32x32x2f32; lane half h feeds rows 2i + h of the slice).  Rows
-// go through LDS in double-buffered slices of 32, the next slice's loads in
-// registers while the current one is multiplied; rows past the range load
-// as zeros.  Row stride 96: the two half-waves' rows fall in disjoint banks.
-constexpr int kMR = 32, kMT = 64, kMLD = 96;
+// The same product on the matrix cores for M, N multiples of 64 WM and
+// 64 WN over the experts' row ranges: a 64 WM x 64 WN tile per workgroup,
+// NWM x NWN waves of 32 x 32 blocks of v_mfma_f32_32x32x2f32 (lane half h
+// feeds rows 2i + h of the slice).  Rows go through LDS in
+// double-buffered slices of 32, the next two slices' loads in registers
+// while the current one is multiplied; rows past the range load as zeros.  Row
+// strides of 32 mod 64 floats: the two half-waves' rows fall in disjoint
+// banks.  The larger tiles read each operand row once per 128 columns
+// instead of once per 64.
+constexpr int kMR = 32;
 
-template <bool GATHER>
-__global__ __launch_bounds__(256) void reduce_mfma_kernel(ReduceGemm g) {
-    __shared__ __align__(16) float As[2][kMR][kMLD];
-    __shared__ __align__(16) float Bs[2][kMR][kMLD];
-    const int e = blockIdx.z, m0 = blockIdx.y * kMT, n0 = blockIdx.x * kMT;
+template <bool GATHER, int WM, int WN, int NWM, int NWN>
+__global__ __launch_bounds__(64 * NWM * NWN) void reduce_mfma_kernel(ReduceGemm g) {
+    // NWM x NWN waves, each BM x BN blocks of 32 x 32.
+    constexpr int NT = 64 * NWM * NWN, BM = 2 * WM / NWM, BN = 2 * WN / NWN;
+    static_assert(BM >= 1 && BN >= 1 && BM * NWM == 2 * WM && BN * NWN == 2 * WN, "wave layout");
+    constexpr int TM = 64 * WM, TN = 64 * WN, LDA = TM + 32, LDB = TN + 32;
+    constexpr int QA = TM / 4, QB = TN / 4;       // float4s per slice row
+    constexpr int RA = NT / QA, RB = NT / QB;     // rows per load pass
+    constexpr int PA = kMR / RA, PB = kMR / RB;   // load passes
+    // The wider tiles fill the CUs in about one round: unused rows past the
+    // slices take the LDS above half a CU's 160 KB, so that no two of these
+    // workgroups share a CU while another CU idles.
+    constexpr int kBase = 2 * kMR * (LDA + LDB) * 4, kHalf = 80 * 1024;
+    constexpr int XR = WM * WN > 1 && kBase <= kHalf ? (kHalf - kBase) / (2 * LDA * 4) + 1 : 0;
+    __shared__ __align__(16) float As[2][kMR + XR][LDA];
+    __shared__ __align__(16) float Bs[2][kMR][LDB];
+    const int e = blockIdx.z, m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
     const int r0 = g.offsets[e], r1 = g.offsets[e + 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1, li = lane & 31, lh = lane >> 5;
-    const int lr = tid >> 4, lq = 4 * (tid & 15);   // load rows lr, lr + 16; column quad
-    const int bcol = n0 + lq;
-    fx4 ra[2], rb[2];
-    auto gload = [&](int r) {
+    const int wm = wave / NWN, wn = wave % NWN, li = lane & 31, lh = lane >> 5;
+    const int la = tid / QA, qa = 4 * (tid % QA), lb = tid / QB, qb = 4 * (tid % QB);
+    // Two register sets take the loads of the next two slices, so each load
+    // has a slice and a half of MFMAs to arrive; the perm entries (GATHER)
+    // of a slice are loaded a slice earlier still, into a set of their own
+    // (pix, by slice parity; divided when used).  Every load is issued
+    // unconditionally, rows clamped to r1 - 1 (rows past the range are
+    // zeroed when stored to LDS), so the wait counts stay exact and no load
+    // waits for a younger one.
+    fx4 ra[2][PA], rb[2][PB];
+    int pix[2][PA];
+    auto pload = [&](auto set, int r) {
+        constexpr int S = decltype(set)::value;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int row = r + lr + 16 * i;
-            if (row < r1) {
-                const size_t arow = GATHER ? (size_t)(g.perm[row] / g.topk) : (size_t)row;
-                ra[i] = *reinterpret_cast<const fx4 *>(g.a + arow * g.lda + m0 + lq);
-                rb[i] = *reinterpret_cast<const fx4 *>(g.b + (size_t)row * g.ldb + bcol);
-            } else {
-                ra[i] = fx4{0.f, 0.f, 0.f, 0.f};
-                rb[i] = fx4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < PA; ++i) {
+            const int row = min(r + la + RA * i, r1 - 1);
+            pix[S][i] = GATHER ? g.perm[row] : row;
+        }
+    };
+    auto gload = [&](auto set, int r) {
+        constexpr int S = decltype(set)::value;
+#pragma unroll
+        for (int i = 0; i < PA; ++i)
+            ra[S][i] = *reinterpret_cast<const fx4 *>(
+                g.a + (size_t)(GATHER ? pix[S][i] / g.topk : pix[S][i]) * g.lda + m0 + qa);
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const int row = min(r + lb + RB * i, r1 - 1);
+            rb[S][i] = *reinterpret_cast<const fx4 *>(g.b + (size_t)row * g.ldb + n0 + qb);
+        }
+    };
+    // Store p (< PA + PB) of register set S as LDS rows of buffer buf, slice r.
+    auto sstore1 = [&](auto set, int p, int buf, int r) {
+        constexpr int S = decltype(set)::value;
+        const fx4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < PA; ++i)
+            if (p == i)
+                *reinterpret_cast<fx4 *>(&As[buf][la + RA * i][qa]) =
+                    r + la + RA * i < r1 ? ra[S][i] : z;
+#pragma unroll
+        for (int i = 0; i < PB; ++i)
+            if (p == PA + i)
+                *reinterpret_cast<fx4 *>(&Bs[buf][lb + RB * i][qb]) =
+                    r + lb + RB * i < r1 ? rb[S][i] : z;
+    };
+    auto sstore = [&](auto set, int buf, int r) {
+#pragma unroll
+        for (int p = 0; p < PA + PB; ++p) sstore1(set, p, buf, r);
+    };
+    fx16 acc[BM][BN];
+#pragma unroll
+    for (int i = 0; i < BM; ++i)
+#pragma unroll
+        for (int j = 0; j < BN; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+    const int am = wm * 32 * BM + li, bn = wn * 32 * BN + li;
+    // The slice in LDS buffer buf; operands of step kk + 2 are read while
+    // step kk multiplies.  mid(p) runs after step 2 + p's MFMAs have issued
+    // (the next slice's LDS stores, one per step under the MFMAs, so that no
+    // step waits for more than one of them).
+    static_assert(PA + PB + 2 <= kMR / 2, "stores per slice");
+    auto mm = [&](int buf, auto &&mid) {
+        float av[2][BM], bv[2][BN];
+        auto rd = [&](int st, int kk) {
+#pragma unroll
+            for (int i = 0; i < BM; ++i) av[st][i] = As[buf][kk + lh][am + 32 * i];
+#pragma unroll
+            for (int j = 0; j < BN; ++j) bv[st][j] = Bs[buf][kk + lh][bn + 32 * j];
+        };
+        rd(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < kMR; kk += 2) {
+            const int st = (kk >> 1) & 1;
+            if (kk + 2 < kMR) rd(st ^ 1, kk + 2);
+            __builtin_amdgcn_sched_barrier(0);   // (the reads go out before the MFMAs)
+#pragma unroll
+            for (int i = 0; i < BM; ++i)
+#pragma unroll
+                for (int j = 0; j < BN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[st][i], bv[st][j],
+                                                                     acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            const int p = kk / 2 - 2;
+            if (p >= 0 && p < PA + PB) {
+                mid(p);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            *reinterpret_cast<fx4 *>(&As[buf][lr + 16 * i][lq]) = ra[i];
-            *reinterpret_cast<fx4 *>(&Bs[buf][lr + 16 * i][lq]) = rb[i];
-        }
-    };
-    fx16 acc;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) acc[q] = 0.f;
-    if (r0 < r1) {
-        gload(r0);
-        sstore(0);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    // Slice r (parity S), held by register set S and already in LDS buffer
+    // S: the perm entries of slice r + 3 kMR go to pix set S ^ 1, register
+    // set S takes slice r + 2 kMR (perm entries in pix set S), buffer S is
+    // multiplied, and slice r + kMR (register set S ^ 1) goes to buffer
+    // S ^ 1, which every wave finished reading before the barrier that ended
+    // the previous slice.
+    auto step = [&](auto set, int r) {
+        constexpr int S = decltype(set)::value;
+        using O = std::integral_constant<int, S ^ 1>;
+        pload(O{}, r + 3 * kMR);
+        gload(set, r + 2 * kMR);
+        mm(S, [&](int p) { sstore1(O{}, p, S ^ 1, r + kMR); });
         __syncthreads();
-        int buf = 0;
-        for (int r = r0; r < r1; r += kMR, buf ^= 1) {
-            const bool more = r + kMR < r1;
-            if (more) gload(r + kMR);
-#pragma unroll
-            for (int kk = 0; kk < kMR; kk += 2)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[buf][kk + lh][wm * 32 + li],
-                                                           Bs[buf][kk + lh][wn * 32 + li], acc,
-                                                           0, 0, 0);
-            if (more) sstore(buf ^ 1);
-            __syncthreads();
+    };
+    if (r0 < r1) {
+        pload(S0{}, r0);
+        pload(S1{}, r0 + kMR);
+        gload(S0{}, r0);
+        pload(S0{}, r0 + 2 * kMR);
+        gload(S1{}, r0 + kMR);
+        sstore(S0{}, 0, r0);
+        __syncthreads();
+        int r = r0;
+        for (; r + kMR < r1; r += 2 * kMR) {
+            step(S0{}, r);
+            step(S1{}, r + kMR);
         }
+        if (r < r1) step(S0{}, r);   // an odd last slice
     }
-    // Lane l, register q: row 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32.
-    const int n = n0 + wn * 32 + li;
-    float *ce = (g.c_up && (n & 32) ? g.c_up : g.c) + (size_t)e * g.c_e;
-    const int col = g.c_up ? 32 * (n >> 6) + (n & 31) : n;
+    // Lane l, register q of a block: row 8 (q / 4) + 4 (l / 32) + q % 4,
+    // column l % 32.
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int m = m0 + wm * 32 + 8 * (q >> 2) + 4 * lh + (q & 3);
-        float *cp = ce + (size_t)m * g.ldc + col;
-        *cp = g.accumulate ? *cp + acc[q] : acc[q];
+    for (int j = 0; j < BN; ++j) {
+        const int n = n0 + bn + 32 * j;
+        float *ce = (g.c_up && (n & 32) ? g.c_up : g.c) + (size_t)e * g.c_e;
+        const int col = g.c_up ? 32 * (n >> 6) + (n & 31) : n;
+#pragma unroll
+        for (int i = 0; i < BM; ++i)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int m = m0 + wm * 32 * BM + 32 * i + 8 * (q >> 2) + 4 * lh + (q & 3);
+                float *cp = ce + (size_t)m * g.ldc + col;
+                *cp = g.accumulate ? *cp + acc[i][j][q] : acc[i][j][q];
+            }
     }
 }
 
@@ -718,9 +816,27 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
                         float *C_up, int M, int N, int ldc) {
             ReduceGemm g{A, lda, b.perm, k, B, ldb, C, (size_t)M * ldc, ldc, b.offsets, 0, 0, M,
                          N, b.accumulate, 1, 1, C_up};
-            hipLaunchKernelGGL((reduce_mfma_kernel<decltype(gather)::value>),
-                               dim3((unsigned)(N / kMT), (unsigned)(M / kMT), (unsigned)E),
-                               dim3(256), 0, s, g);
+            // The widest tile that still gives every CU a workgroup.
+            const long cus = device_cus();
+            auto tiles = [&](int wm, int wn) { return (long)(M / (64 * wm)) * (N / (64 * wn)) * E; };
+            // The wider tiles run 8 waves (two per SIMD): 128 x 128 as 64 x 32
+            // blocks 4 % faster than 4 waves of 64 x 64, 128 x 64 as 32 x 32
+            // blocks 8 % faster than 4 waves of 64 x 32.
+            auto go = [&](auto wm, auto wn) {
+                constexpr int WM = decltype(wm)::value, WN = decltype(wn)::value;
+                constexpr int NWM = WM == 2 && WN == 1 ? 4 : 2;
+                constexpr int NWN = WN == 2 ? 4 : 2;
+                hipLaunchKernelGGL((reduce_mfma_kernel<decltype(gather)::value, WM, WN, NWM, NWN>),
+                                   dim3((unsigned)(N / (64 * WN)), (unsigned)(M / (64 * WM)),
+                                        (unsigned)E),
+                                   dim3(64 * NWM * NWN), 0, s, g);
+            };
+            using I1 = std::integral_constant<int, 1>;
+            using I2 = std::integral_constant<int, 2>;
+            if (M % 128 == 0 && N % 128 == 0 && tiles(2, 2) >= cus) go(I2{}, I2{});
+            else if (M % 128 == 0 && tiles(2, 1) >= cus)           go(I2{}, I1{});
+            else if (N % 128 == 0 && tiles(1, 2) >= cus)           go(I1{}, I2{});
+            else                                                    go(I1{}, I1{});
         };
         mfma(F_{}, b.H, F, b.dY, d, b.dwd, nullptr, F, d, d);
         // dW_g and dW_u in one launch over GU's 2F packed columns.

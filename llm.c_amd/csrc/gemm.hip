@@ -719,7 +719,7 @@ __global__ __launch_bounds__(512) void tail_fixup_kernel(GemmArgs a) {
 }  // namespace
 
 // Compute units of the current device (cached; 256 on MI355X).
-static int device_cus() {
+int device_cus() {
     static int cus = 0;
     if (cus <= 0) {
         int dev = 0, n = 0;

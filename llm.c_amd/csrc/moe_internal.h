@@ -281,4 +281,7 @@ DownPlan down_plan(int N, int K, int max_mtiles, size_t n);
 // The pieces take at most kGemmBM * 256 * groups floats.
 int gateup_tail_groups(int N, int K, int max_mtiles);
 
+// Compute units of the current device (cached; 256 on MI355X).
+int device_cus();
+
 }  // namespace moe

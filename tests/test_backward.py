@@ -153,12 +153,16 @@ def run_device_backward(d, F, E, k, T, seed, aux_coef, accumulate_twice=False):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape", [(128, 512, 4, 2, 256), (256, 1024, 8, 2, 384),
-                                   (128, 256, 16, 4, 100), (64, 96, 4, 2, 150)],
-                         ids=["c1", "c2-rows", "e16-k4", "untiled"])
+                                   (128, 256, 16, 4, 100), (64, 96, 4, 2, 150),
+                                   (192, 1024, 8, 2, 600)],
+                         ids=["c1", "c2-rows", "e16-k4", "untiled", "d192"])
 @pytest.mark.parametrize("aux_coef", [0.0, 0.5])
 def test_backward_device_vs_oracle(shape, aux_coef):
     """The tile-engine path (d, F multiples of 64; split partials by slot at
-    c2-rows) and the untiled row products (F = 96)."""
+    c2-rows) and the untiled row products (F = 96).  The weight-gradient
+    tiles: 64 x 64 at the small shapes, 64 x 128 for dW_g/dW_u at d192 (d
+    not a multiple of 128), 128 x 128 and 128 x 64 at the batch-8x512 shape
+    (test_backward_device_split_tail)."""
     d, F, E, k, T = shape
     print(f"[gpu-test] backward d={d} F={F} E={E} k={k} T={T} aux={aux_coef}", flush=True)
     res, x, dout, wr, wg, wu, wd = run_device_backward(d, F, E, k, T, 31, aux_coef)
