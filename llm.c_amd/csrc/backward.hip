@@ -28,7 +28,6 @@ namespace {
 
 constexpr int kRM = 128, kRN = 64, kRK = 16;   // rows_gemm tile
 constexpr int kQM = 64, kQN = 64, kQR = 16;    // reduce_gemm tile
-constexpr int kRouterChunk = 256;              // token rows per router-gradient partial
 
 // C[pos][n] (+)= sum_kk A(pos, kk) B_e(kk, n) for the rows pos of each
 // 128-row tile (expert e).  A(pos, kk) = a[arow * lda + kk] with arow =
@@ -524,13 +523,108 @@ __global__ __launch_bounds__(64 * NWM * NWN) void reduce_mfma_kernel(ReduceGemm 
     }
 }
 
-// C (+)= sum over z (in order) of P[z] for nz partials of n floats.
-__global__ __launch_bounds__(256) void sum_partials_kernel(const float *P, int nz, size_t n,
-                                                           int accumulate, float *C) {
-    for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        float v = 0.f;
-        for (int z = 0; z < nz; ++z) v += P[(size_t)z * n + i];
-        C[i] = accumulate ? C[i] + v : v;
+// dW_r = X^T dlogits over all T rows, and (CS set) the column sums of
+// probs for the aux loss.  Workgroup (column block cb of 64 x columns, row
+// chunk z of R rows); thread (c, p) = (t % 64, t / 64) runs the FMA chains of
+// kRgEB experts at a time over rows zR + p, zR + p + 4, ..., and the 4 row
+// phases are added in phase order through LDS into P[z][d][E].  Every load
+// is unconditional (indices clamped, masked terms multiplied by zero).  The
+// workgroups of column block 0 also sum probs over their rows into CS[z][E].
+// router_grad_final_kernel adds the chunks in order.
+constexpr int kRgEB = 8;
+
+__global__ __launch_bounds__(256) void router_grad_kernel(const float *x, const float *dl,
+                                                          const float *probs, int T, int d,
+                                                          int E, int R, float *P, float *CS) {
+    __shared__ float red[4][64][kRgEB + 1];
+    const int cb = blockIdx.x, z = blockIdx.y;
+    const int t = threadIdx.x, c = t & 63, p = t >> 6;
+    const int col = min(cb * 64 + c, d - 1);
+    const int r0 = z * R, r1 = min(T, r0 + R);
+    for (int e0 = 0; e0 < E; e0 += kRgEB) {
+        float acc[kRgEB];
+#pragma unroll
+        for (int j = 0; j < kRgEB; ++j) acc[j] = 0.f;
+        // Rows in batches of 8 (every load of a batch in flight together).
+        for (int rb = r0 + p; rb < r1; rb += 32) {
+            float xv[8], w[8][kRgEB];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int r = min(rb + 4 * u, r1 - 1);
+                xv[u] = x[(size_t)r * d + col];
+#pragma unroll
+                for (int j = 0; j < kRgEB; ++j) w[u][j] = dl[(size_t)r * E + min(e0 + j, E - 1)];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+#pragma unroll
+                for (int j = 0; j < kRgEB; ++j)
+                    acc[j] = fmaf(rb + 4 * u < r1 ? xv[u] : 0.f, e0 + j < E ? w[u][j] : 0.f,
+                                  acc[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < kRgEB; ++j) red[p][c][j] = acc[j];
+        __syncthreads();
+        for (int i = t; i < 64 * kRgEB; i += 256) {
+            const int cc = i / kRgEB, j = i % kRgEB, oc = cb * 64 + cc;
+            if (oc < d && e0 + j < E)
+                P[((size_t)z * d + oc) * E + e0 + j] =
+                    ((red[0][cc][j] + red[1][cc][j]) + red[2][cc][j]) + red[3][cc][j];
+        }
+        __syncthreads();
+    }
+    if (CS && cb == 0)
+        for (int e = t; e < E; e += 256) {
+            float sum = 0.f;
+            for (int rb = r0; rb < r1; rb += 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) v[u] = probs[(size_t)min(rb + u, r1 - 1) * E + e];
+#pragma unroll
+                for (int u = 0; u < 16; ++u)
+                    if (rb + u < r1) sum += v[u];
+            }
+            CS[(size_t)z * E + e] = sum;
+        }
+}
+
+// base + sum over z < nz (in order) of P[z n + i], 16 chunks' loads in
+// flight at a time.
+__device__ inline float sum_chunks(const float *P, int nz, int n, int i, float base) {
+    float v = 0.f;
+    for (int z0 = 0; z0 < nz; z0 += 16) {
+        float q[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) q[u] = P[(size_t)min(z0 + u, nz - 1) * n + i];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            if (z0 + u < nz) v += q[u];
+    }
+    return base + v;
+}
+
+// dwr (+)= sum over z (in order) of P[z] (n = d E floats); with aux, one
+// more workgroup adds the column sums CS over z (in order) and takes
+// aux = E sum_e f_e P_e, f_e = counts[e] / (T k), P_e = colsum[e] / T.
+__global__ __launch_bounds__(256) void router_grad_final_kernel(const float *P, int nz, int n,
+                                                                int accumulate, float *dwr,
+                                                                const float *CS,
+                                                                const int *counts, int T, int E,
+                                                                int k, float *aux) {
+    __shared__ float cs[kMaxExperts];
+    const int nb = (n + 255) / 256;
+    if ((int)blockIdx.x < nb) {
+        const int i = blockIdx.x * 256 + threadIdx.x;
+        if (i < n) dwr[i] = sum_chunks(P, nz, n, i, accumulate ? dwr[i] : 0.f);
+        return;
+    }
+    for (int e = threadIdx.x; e < E; e += 256) cs[e] = sum_chunks(CS, nz, E, e, 0.f);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float total = 0.f;
+        for (int e = 0; e < E; ++e)
+            total = fmaf((float)counts[e] / ((float)T * (float)k), cs[e] / (float)T, total);
+        *aux = (float)E * total;
     }
 }
 
@@ -661,30 +755,6 @@ __global__ __launch_bounds__(256) void dx_kernel(SlotRows dXr, const int *inv,
 // aux = E * sum_e (counts[e] / (T k)) * (sum_t probs[t][e] / T): workgroup
 // e sums column e (thread-strided sums, then a fixed tree) into colsum[e];
 // aux_final adds the terms in expert order.
-__global__ __launch_bounds__(256) void aux_cols_kernel(const float *probs, int T, int E,
-                                                       float *colsum) {
-    __shared__ float red[256];
-    const int e = blockIdx.x;
-    float s = 0.f;
-    for (int t = threadIdx.x; t < T; t += 256) s += probs[(size_t)t * E + e];
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int w = 128; w >= 1; w >>= 1) {
-        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) colsum[e] = red[0];
-}
-
-__global__ __launch_bounds__(64) void aux_final_kernel(const float *colsum, const int *counts,
-                                                       int T, int E, int k, float *aux) {
-    if (threadIdx.x != 0) return;
-    float total = 0.f;
-    for (int e = 0; e < E; ++e)
-        total = fmaf((float)counts[e] / ((float)T * (float)k), colsum[e] / (float)T, total);
-    *aux = (float)E * total;
-}
-
 unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 16384); }
 
 #define BWD_TRY(x)                               \
@@ -849,22 +919,19 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         reduce(T_{}, b.x, d, b.U, F, b.dwu, (size_t)d * F, d, F, b.offsets, 0, 0, E,
                b.accumulate);
     }
-    // The router's over all tokens, in chunks of kRouterChunk rows whose
-    // partials (in dH, free by now) are then added in chunk order.
-    // (at most n F / (d E) partials fit in dH)
-    const size_t fit = std::max<size_t>(1, n * F / ((size_t)d * E));
-    const int chunk = (int)std::max<size_t>(kRouterChunk, (T + fit - 1) / fit);
-    const int nz = (T + chunk - 1) / chunk;
-    reduce(F_{}, b.x, d, b.dlogits, E, b.dH, (size_t)d * E, d, E, nullptr, T, chunk, nz, 0);
-    hipLaunchKernelGGL(sum_partials_kernel, dim3(blocks_for((size_t)d * E)), dim3(256), 0, s,
-                       b.dH, nz, (size_t)d * E, b.accumulate, b.dwr);
-    // (dlogits, consumed by now, holds the column sums)
-    if (b.aux) {
-        hipLaunchKernelGGL(aux_cols_kernel, dim3((unsigned)E), dim3(256), 0, s, b.probs, T, E,
-                           b.dlogits);
-        hipLaunchKernelGGL(aux_final_kernel, dim3(1), dim3(64), 0, s, b.dlogits, b.counts, T, E,
-                           k, b.aux);
-    }
+    // The router's over all tokens (and the aux loss's column sums), in row
+    // chunks whose partials (in dH, free by now) are then added in chunk
+    // order: enough chunks for about one workgroup per CU.
+    const int ncb = (d + 63) / 64;
+    int R = std::max(16, (int)((T + std::max(1, 256 / ncb) - 1) / std::max(1, 256 / ncb)));
+    while ((size_t)((T + R - 1) / R) * ((size_t)d * E + E) > n * F) R *= 2;
+    const int nz = (T + R - 1) / R;
+    float *P = b.dH, *CS = b.aux ? b.dH + (size_t)nz * d * E : nullptr;
+    hipLaunchKernelGGL(router_grad_kernel, dim3((unsigned)ncb, (unsigned)nz), dim3(256), 0, s,
+                       b.x, b.dlogits, b.probs, T, d, E, R, P, CS);
+    const int nb = (int)((d * E + 255) / 256);
+    hipLaunchKernelGGL(router_grad_final_kernel, dim3((unsigned)(nb + (b.aux ? 1 : 0))), dim3(256),
+                       0, s, P, nz, d * E, b.accumulate, b.dwr, CS, b.counts, T, E, k, b.aux);
     return hipGetLastError();
 }
 
