@@ -659,11 +659,33 @@ struct SlotRows {
     __device__ int count(int a, int d, int c) const {
         return pieces ? pieces[(size_t)a * (d / pcols) + c / pcols] : ns;
     }
+    // The partials of (row, column c) added in order; the first 8 are
+    // loaded together (clamped, masked), so none waits for another.
     __device__ float at(int pos, int a, int d, int c) const {
         const float *r = p + (size_t)(by_slot ? a : pos) * d + c;
-        float v = r[0];
-        const int n = count(a, d, c);
-        for (int s = 1; s < n; ++s) v += r[(size_t)s * ys];
+        const int n = max(count(a, d, c), 1);
+        float q[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[u] = r[(size_t)min(u, n - 1) * ys];
+        float v = q[0];
+#pragma unroll
+        for (int u = 1; u < 8; ++u)
+            if (u < n) v += q[u];
+        for (int s = 8; s < n; ++s) v += r[(size_t)s * ys];
+        return v;
+    }
+    // The same for the four columns c .. c + 3 (16-byte aligned).
+    __device__ fx4 at4(int row, int a, int d, int c) const {
+        const float *r = p + (size_t)row * d + c;
+        const int n = max(count(a, d, c), 1);
+        fx4 q[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[u] = *reinterpret_cast<const fx4 *>(r + (size_t)min(u, n - 1) * ys);
+        fx4 v = q[0];
+#pragma unroll
+        for (int u = 1; u < 8; ++u)
+            if (u < n) v += q[u];
+        for (int s = 8; s < n; ++s) v += *reinterpret_cast<const fx4 *>(r + (size_t)s * ys);
         return v;
     }
 };
@@ -681,10 +703,21 @@ __global__ __launch_bounds__(256) void slot_kernel(SlotRows Y, const float *dout
     const float *go = dout + (size_t)t * d;
     float *dy = dY + (size_t)pos * d;
     float s = 0.f;
-    for (int c = lane; c < d; c += 64) {
-        const float v = go[c];
-        s = fmaf(Y.at(pos, a, d, c), v, s);
-        dy[c] = w * v;
+    // Four columns per step, their loads issued together.
+    for (int c0 = lane; c0 < d; c0 += 256) {
+        float v[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = min(c0 + 64 * u, d - 1);
+            v[u] = go[c];
+            y[u] = Y.at(pos, a, d, c);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (c0 + 64 * u < d) {
+                s = fmaf(y[u], v[u], s);
+                dy[c0 + 64 * u] = w * v[u];
+            }
     }
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
     if (lane == 0) {
@@ -693,31 +726,72 @@ __global__ __launch_bounds__(256) void slot_kernel(SlotRows Y, const float *dout
     }
 }
 
-// One thread per token: dlogits [T x E] from dgw through the gate
-// renormalisation, the aux term and the softmax.
+// Eight lanes per token: dlogits [T x E] from dgw through the gate
+// renormalisation, the aux term and the softmax.  Every lane of a token
+// loads its ids, dgw and gw (kMaxTopK of each, clamped, masked) and the
+// probabilities of its experts e = g, g + 8, ... (g = lane % 8) at once, then
+// the selected probabilities; S, c and dp(e) are summed in slot order and
+// the dot over the experts in expert order (through shuffles), as one thread
+// per token would.
+constexpr int kRbG = 8, kRbJ = kMaxExperts / kRbG;
 __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, const int *ids,
                                                          const float *gw, const float *dgw,
                                                          const int *counts, int T, int E, int k,
                                                          float aux_coef, float *dlogits) {
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (t >= T) return;
-    const float *p = probs + (size_t)t * E;
-    const int *id = ids + (size_t)t * k;
-    float S = 0.f, c = 0.f;
-    for (int s = 0; s < k; ++s) {
-        S += p[id[s]];
-        c = fmaf(dgw[(size_t)t * k + s], gw[(size_t)t * k + s], c);
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    const int t = gid / kRbG, g = gid % kRbG;
+    const int tc = min(t, T - 1);
+    const float *p = probs + (size_t)tc * E;
+    int id[kMaxTopK];
+    float dg[kMaxTopK], w[kMaxTopK], ps[kMaxTopK];
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s) {
+        const size_t q = (size_t)tc * k + min(s, k - 1);
+        id[s] = ids[q];
+        dg[s] = dgw[q];
+        w[s] = gw[q];
     }
+    float pv[kRbJ], cn[kRbJ];
+#pragma unroll
+    for (int j = 0; j < kRbJ; ++j)
+        if (kRbG * j < E) {
+            const int e = min(g + kRbG * j, E - 1);
+            pv[j] = p[e];
+            cn[j] = (float)counts[e];
+        }
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s) ps[s] = p[id[s]];
+    float S = 0.f, c = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s)
+        if (s < k) {
+            S += ps[s];
+            c = fmaf(dg[s], w[s], c);
+        }
     const float aux_scale = aux_coef * (float)E / ((float)T * (float)T * (float)k);
-    auto dp = [&](int e) {
-        float v = aux_scale * (float)counts[e];
-        for (int s = 0; s < k; ++s)
-            if (id[s] == e) v += (dgw[(size_t)t * k + s] - c) / S;
-        return v;
-    };
+    float dpv[kRbJ];
+#pragma unroll
+    for (int j = 0; j < kRbJ; ++j)
+        if (kRbG * j < E) {
+            const int e = g + kRbG * j;
+            float v = aux_scale * cn[j];
+#pragma unroll
+            for (int s = 0; s < kMaxTopK; ++s)
+                if (s < k && id[s] == e) v += (dg[s] - c) / S;
+            dpv[j] = v;
+        }
     float dot = 0.f;
-    for (int e = 0; e < E; ++e) dot = fmaf(dp(e), p[e], dot);
-    for (int e = 0; e < E; ++e) dlogits[(size_t)t * E + e] = p[e] * (dp(e) - dot);
+#pragma unroll
+    for (int j = 0; j < kRbJ; ++j)
+        if (kRbG * j < E)
+#pragma unroll
+            for (int q = 0; q < kRbG; ++q)
+                if (kRbG * j + q < E)
+                    dot = fmaf(__shfl(dpv[j], q, kRbG), __shfl(pv[j], q, kRbG), dot);
+    if (t >= T) return;
+#pragma unroll
+    for (int j = 0; j < kRbJ; ++j)
+        if (g + kRbG * j < E) dlogits[(size_t)t * E + g + kRbG * j] = pv[j] * (dpv[j] - dot);
 }
 
 // dx[t][c..c+3] = sum over slots (in order) of dXr(t k + s), plus
@@ -733,28 +807,31 @@ __global__ __launch_bounds__(256) void dx_kernel(SlotRows dXr, const int *inv,
     fx4 v = {0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < k; ++s) {
         const int a = t * k + s;
-        const float *r = dXr.p + (size_t)(dXr.by_slot ? a : inv[a]) * d + c;
-        fx4 y = *reinterpret_cast<const fx4 *>(r);
-        const int ns = dXr.count(a, d, c);
-        for (int z = 1; z < ns; ++z) y += *reinterpret_cast<const fx4 *>(r + (size_t)z * dXr.ys);
-        v += y;
+        v += dXr.at4(dXr.by_slot ? a : inv[a], a, d, c);
     }
     fx4 rr = {0.f, 0.f, 0.f, 0.f};
     const float *dl = dlogits + (size_t)t * E;
-    for (int e = 0; e < E; ++e) {
-        const float g = dl[e];
-        const fx4 w = *reinterpret_cast<const fx4 *>(wrT + (size_t)e * d + c);
+    // Eight experts per step, their loads issued together.
+    for (int e0 = 0; e0 < E; e0 += 8) {
+        float gv[8];
+        fx4 wv[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) rr[j] = fmaf(g, w[j], rr[j]);
+        for (int u = 0; u < 8; ++u) {
+            const int e = min(e0 + u, E - 1);
+            gv[u] = dl[e];
+            wv[u] = *reinterpret_cast<const fx4 *>(wrT + (size_t)e * d + c);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (e0 + u < E)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rr[j] = fmaf(gv[u], wv[u][j], rr[j]);
     }
     v += rr;
     fx4 *o = reinterpret_cast<fx4 *>(dx + (size_t)t * d + c);
     *o = accumulate ? *o + v : v;
 }
 
-// aux = E * sum_e (counts[e] / (T k)) * (sum_t probs[t][e] / T): workgroup
-// e sums column e (thread-strided sums, then a fixed tree) into colsum[e];
-// aux_final adds the terms in expert order.
 unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 256, 16384); }
 
 #define BWD_TRY(x)                               \
@@ -865,8 +942,8 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         rows(F_{}, T_{}, b.U, F, b.wu, (size_t)d * F, F, b.Y, F, d, 1);
     }
     // Router and dx.
-    hipLaunchKernelGGL(router_bwd_kernel, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s,
-                       b.probs, b.ids, b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
+    hipLaunchKernelGGL(router_bwd_kernel, dim3((unsigned)(((size_t)T * kRbG + 255) / 256)),
+                       dim3(256), 0, s, b.probs, b.ids, b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
     hipLaunchKernelGGL(dx_kernel, dim3((unsigned)(((size_t)T * (d / 4) + 255) / 256)), dim3(256),
                        0, s, dXr, b.inv,
                        b.dlogits, b.wrT, T, d, E, k, b.accumulate, b.dx);
