@@ -176,13 +176,163 @@ __device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], i
     }
 }
 
-constexpr int kDispWaves = 16;
+constexpr int kDispWaves = 16, kDispMaxGroups = 32;
 
-__global__ __launch_bounds__(1024) void dispatch_kernel(DispatchArgs a) {
-    __shared__ int hist[kDispWaves][kMaxExperts];
-    __shared__ int offs[kMaxExperts + 1];
-    __shared__ int toff[kMaxExperts + 1];
-    dispatch_body<kDispWaves>(a, hist, offs, toff);
+// The same counting sort over G workgroups of 16 waves (dispatch_groups):
+// the assignments fall into G * 16 wave chunks of CH (a multiple of 64)
+// consecutive entries, chunk c = gg * 16 + w.  Every workgroup counts all
+// of them into per-range histograms (wave w taking chunks gg * 16 + w for
+// every gg), and its own range's chunks into per-wave ones.  Workgroup g
+// then places its own 16 chunks: a wave's running base per expert lives in
+// lane x, an entry's base comes from its expert's lane (a shuffle), its rank
+// among the group's earlier lanes from the expert bits' ballots, which also
+// give each lane x the group's count of expert x (and x + 64).  Workgroup 0
+// writes counts, offsets, tile_off and tile_expert.
+// (Both loops run to the largest bit count, 7 for 128 experts, with
+// constant indices, so the masks stay in registers.)
+struct GroupMasks {
+    uint64_t valid, bit[7];
+    // Lanes of the group whose expert is x.
+    __device__ uint64_t of(int x, int nbits) const {
+        uint64_t m = valid;
+#pragma unroll
+        for (int b = 0; b < 7; ++b)
+            if (b < nbits) m &= ((x >> b) & 1) ? bit[b] : ~bit[b];
+        return m;
+    }
+};
+__device__ inline GroupMasks group_masks(bool valid, int e, int nbits) {
+    GroupMasks g;
+    g.valid = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 7; ++b) g.bit[b] = __ballot(b < nbits && valid && ((e >> b) & 1));
+    return g;
+}
+
+__global__ __launch_bounds__(1024) void dispatch_groups_kernel(DispatchArgs a, int CH) {
+    __shared__ int hg[kDispMaxGroups][kMaxExperts];   // per-workgroup-range counts
+    __shared__ int hw[kDispWaves][kMaxExperts];       // this range's per-wave counts, then bases
+    __shared__ int tot[kMaxExperts], pre[kMaxExperts];
+    __shared__ int offs[kMaxExperts + 1], toff[kMaxExperts + 1];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int G = gridDim.x, g = blockIdx.x, E = a.E, n = a.n;
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+    for (int i = tid; i < kDispMaxGroups * kMaxExperts; i += 1024) (&hg[0][0])[i] = 0;
+    for (int i = tid; i < kDispWaves * kMaxExperts; i += 1024) (&hw[0][0])[i] = 0;
+    __syncthreads();
+
+    // Pass 1: wave w counts chunks gg * 16 + w, gg < G (LDS atomics per
+    // entry), 8 groups' loads at a time; (gg, sub) advance without
+    // divisions.
+    const int per = CH / 64, Q = G * per;
+    int gg_n = 0, sub_n = 0;   // the next group to load
+    for (int q0 = 0; q0 < Q; q0 += 8) {
+        int v[8], gq[8];
+        bool ok[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = (gg_n * kDispWaves + w) * CH + sub_n * 64 + lane;
+            ok[u] = q0 + u < Q && i < n;
+            gq[u] = gg_n;
+            v[u] = a.ids[min(i, n - 1)];
+            if (++sub_n == per) {
+                sub_n = 0;
+                ++gg_n;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (ok[u]) {
+                atomicAdd(&hg[gq[u]][v[u]], 1);
+                if (gq[u] == g) atomicAdd(&hw[w][v[u]], 1);
+            }
+    }
+    __syncthreads();
+
+    // Totals, the counts before this workgroup's range, offsets (a scan in
+    // expert order), then each wave's bases.
+    for (int x = tid; x < E; x += 1024) {
+        int t = 0, p = 0;
+        for (int gg = 0; gg < G; ++gg) {
+            const int c = hg[gg][x];
+            t += c;
+            if (gg < g) p += c;
+        }
+        tot[x] = t;
+        pre[x] = p;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int cs = 0, ms = 0;
+        for (int x = 0; x < E; ++x) {
+            offs[x] = cs;
+            toff[x] = ms;
+            cs += tot[x];
+            ms += (tot[x] + a.bm - 1) / a.bm;
+        }
+        offs[E] = cs;
+        toff[E] = ms;
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += 1024) {
+        int b = offs[x] + pre[x];
+        for (int ww = 0; ww < kDispWaves; ++ww) {
+            const int c = hw[ww][x];
+            hw[ww][x] = b;
+            b += c;
+        }
+    }
+    if (g == 0) {
+        for (int x = tid; x < E; x += 1024) a.counts[x] = tot[x];
+        for (int x = tid; x <= E; x += 1024) {
+            a.offsets[x] = offs[x];
+            a.tile_off[x] = toff[x];
+        }
+        if (a.tile_expert)
+            for (int x = tid; x < E; x += 1024)
+                for (int t = toff[x]; t < toff[x + 1]; ++t) a.tile_expert[t] = x;
+    }
+    __syncthreads();
+
+    // Pass 2: this workgroup's chunk g * 16 + w, in order.
+    int b0 = lane < E ? hw[w][lane] : 0, b1 = lane + 64 < E ? hw[w][lane + 64] : 0;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    const int beg = (g * kDispWaves + w) * CH;
+    for (int s0 = 0; s0 < per; s0 += 8) {
+        int v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = a.ids[min(beg + min(s0 + u, per - 1) * 64 + lane, n - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (s0 + u >= per) break;
+            const int i = beg + (s0 + u) * 64 + lane;
+            const bool valid = i < n;
+            const int e = v[u];
+            const GroupMasks m = group_masks(valid, e, nbits);
+            const uint64_t peers = m.of(e, nbits);
+            const int lo = __shfl(b0, e & 63), hi = __shfl(b1, e & 63);
+            if (valid) a.perm[(e < 64 ? lo : hi) + __popcll(peers & below)] = i;
+            b0 += __popcll(m.of(lane, nbits));
+            if (E > 64) b1 += __popcll(m.of(lane + 64, nbits));
+        }
+    }
+}
+
+// Workgroups of the grouped dispatch for n assignments (about one 64-entry
+// group per wave), and the chunk length CH.
+inline void dispatch_groups(int n, int &G, int &CH) {
+    G = std::max(1, std::min(kDispMaxGroups, (n + kDispWaves * 64 - 1) / (kDispWaves * 64)));
+    const int wc = G * kDispWaves;
+    CH = ((n + wc - 1) / wc + 63) / 64 * 64;
+}
+
+hipError_t launch_dispatch_groups(const DispatchArgs &da, hipStream_t s) {
+    if (da.n <= 0) return hipSuccess;
+    int G, CH;
+    dispatch_groups(da.n, G, CH);
+    hipLaunchKernelGGL(dispatch_groups_kernel, dim3((unsigned)G), dim3(1024), 0, s, da, CH);
+    return hipGetLastError();
 }
 
 // Softmax, top-k and gate weights of token t from its logits row (in LDS),
@@ -619,8 +769,8 @@ hipError_t launch_rows_router(const RouteArgs &a, const DispatchArgs &da, hipStr
 // kFusedDispatchMax assignments and kFusedDispatchMaxBlocks router
 // workgroups) the router's last workgroup sorts them in the same launch; its
 // device-scope fences write back and invalidate L2, which is cheap for a
-// handful of workgroups only.  Otherwise a separate 16-wave dispatch kernel
-// sorts them.
+// handful of workgroups only.  Otherwise dispatch_groups_kernel sorts them
+// (about one 64-entry group per wave, over up to 32 workgroups).
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
     if (a.rms_w && !(a.wrT && a.d % 16 == 0)) {
@@ -638,16 +788,14 @@ hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hip
         const bool fuse = da.counter && da.n <= kFusedDispatchMax && blocks <= kRowsFusedMaxBlocks;
         hipError_t e = fuse ? launch_rows_router<true>(a, da, s) : launch_rows_router<false>(a, da, s);
         if (e != hipSuccess || fuse) return e;
-        hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, da);
-        return hipGetLastError();
+        return launch_dispatch_groups(da, s);
     }
     const int grid = (a.T + (a.T >= 2048 ? 64 : 16) - 1) / (a.T >= 2048 ? 64 : 16);
     if (da.n <= kFusedDispatchMax && grid <= kFusedDispatchMaxBlocks && da.counter)
         return launch_router<true>(a, da, s);
     hipError_t e = launch_router<false>(a, da, s);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, da);
-    return hipGetLastError();
+    return launch_dispatch_groups(da, s);
 }
 
 
