@@ -125,6 +125,10 @@ ROUTE_CASES = [
     ("t1", 1, 256, 8, 2, 0.1),
     ("t65_d64", 65, 64, 16, 2, 0.1),
     ("t5000", 5000, 128, 16, 2, 0.1),
+    # the grouped dispatch: 128 experts over 6 workgroups; 40000 assignments
+    # over 32 workgroups, two 64-entry groups per wave
+    ("e128k2_g6", 3000, 64, 128, 2, 0.2),
+    ("t20000_g32", 20000, 64, 16, 2, 0.1),
 ]
 
 ROUTER_PATHS = [0, 1, 2]   # automatic, token x expert tiles, 16-token row blocks
