@@ -478,27 +478,56 @@ hipError_t launch_mode(const GemmArgs &a, hipStream_t s) {
 // out[t] = sum over slots of gw * y, one FMA per slot in slot order
 // (src/transformer.c:355-358 after contraction), optionally added into out.
 // With ksplit > 1 each slot's y is the sum of its split partials, added in
-// split order (with pieces: as many as its column block's tile had).
+// split order (with pieces: as many as its column block's tile had).  With
+// PARTS (ksplit > 1 or pieces) the first 8 partials of a slot are loaded
+// together (clamped, masked), and with KS > 0 (k = KS) every slot's loads
+// go out before the first sum, so no load waits for another.
+template <int KS, bool PARTS>
 __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
+    constexpr int KB = KS > 0 ? KS : 1;   // slots whose loads go out together
+    constexpr int NQ = PARTS ? 8 : 1;     // partials loaded together
     const int d4 = a.d >> 2;
     const size_t total = (size_t)a.T * d4;
+    const int k = KS > 0 ? KS : a.k;
     for (size_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
         const int t = (int)(i / d4), c = (int)(i % d4);
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int ki = 0; ki < a.k; ++ki) {
-            const float w = a.gw[(size_t)t * a.k + ki];
-            const float *yp = a.ys + ((size_t)t * a.k + ki) * a.d + 4 * c;
-            floatx4 y = *reinterpret_cast<const floatx4 *>(yp);
-            const int np = a.pieces ? a.pieces[((size_t)t * a.k + ki) * (a.d / a.pieces_cols) +
-                                               4 * c / a.pieces_cols]
-                                    : a.ksplit;
-            for (int sp = 1; sp < np; ++sp) {
-                const floatx4 p = *reinterpret_cast<const floatx4 *>(yp + sp * a.split_stride);
+        for (int k0 = 0; k0 < k; k0 += KB) {
+            floatx4 q[KB][NQ];
+            float w[KB];
+            int np[KB];
+            const float *yp[KB];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) y[j] = y[j] + p[j];
+            for (int kb = 0; kb < KB; ++kb) {
+                const size_t slot = (size_t)t * a.k + k0 + kb;
+                w[kb] = a.gw[slot];
+                yp[kb] = a.ys + slot * a.d + 4 * c;
+                np[kb] = !PARTS ? 1
+                         : a.pieces ? a.pieces[slot * (a.d / a.pieces_cols) + 4 * c / a.pieces_cols]
+                                    : a.ksplit;
+                np[kb] = max(np[kb], 1);
+#pragma unroll
+                for (int u = 0; u < NQ; ++u)
+                    q[kb][u] = *reinterpret_cast<const floatx4 *>(
+                        yp[kb] + (size_t)min(u, np[kb] - 1) * a.split_stride);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = fmaf(w, y[j], acc[j]);
+            for (int kb = 0; kb < KB; ++kb) {
+                floatx4 y = q[kb][0];
+#pragma unroll
+                for (int u = 1; u < NQ; ++u)
+                    if (u < np[kb])
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) y[j] = y[j] + q[kb][u][j];
+                for (int sp = NQ; sp < np[kb]; ++sp) {
+                    const floatx4 p = *reinterpret_cast<const floatx4 *>(
+                        yp[kb] + (size_t)sp * a.split_stride);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) y[j] = y[j] + p[j];
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] = fmaf(w[kb], y[j], acc[j]);
+            }
         }
         floatx4 *o = reinterpret_cast<floatx4 *>(a.out + (size_t)t * a.d + 4 * c);
         if (a.accumulate) {
@@ -873,7 +902,15 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
     size_t total = (size_t)a.T * (a.d >> 2);
     if (total == 0) return hipSuccess;
     unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
-    hipLaunchKernelGGL(combine_kernel, dim3(blocks), dim3(256), 0, s, a);
+    auto go = [&](auto parts) {
+        constexpr bool P = decltype(parts)::value;
+        if (a.k == 1)      hipLaunchKernelGGL((combine_kernel<1, P>), dim3(blocks), dim3(256), 0, s, a);
+        else if (a.k == 2) hipLaunchKernelGGL((combine_kernel<2, P>), dim3(blocks), dim3(256), 0, s, a);
+        else if (a.k == 4) hipLaunchKernelGGL((combine_kernel<4, P>), dim3(blocks), dim3(256), 0, s, a);
+        else               hipLaunchKernelGGL((combine_kernel<0, P>), dim3(blocks), dim3(256), 0, s, a);
+    };
+    if (a.pieces || a.ksplit > 1) go(std::true_type{});
+    else                          go(std::false_type{});
     return hipGetLastError();
 }
 
