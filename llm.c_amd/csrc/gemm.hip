@@ -695,11 +695,11 @@ __global__ __launch_bounds__(512) void tail_fixup_kernel(GemmArgs a) {
     for (int s0 = 0; s0 < tl.s; s0 += 4) {
         floatx4 p0[4], p1[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (s0 + q < tl.s) {
-                p0[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS);
-                p1[q] = *reinterpret_cast<const floatx4 *>(src + (s0 + q) * PS + 32);
-            }
+        for (int q = 0; q < 4; ++q) {   // (clamped: every load goes out together)
+            const size_t sq = (size_t)min(s0 + q, tl.s - 1) * PS;
+            p0[q] = *reinterpret_cast<const floatx4 *>(src + sq);
+            p1[q] = *reinterpret_cast<const floatx4 *>(src + sq + 32);
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (s0 + q < tl.s) {
