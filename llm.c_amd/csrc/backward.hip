@@ -358,7 +358,7 @@ __global__ __launch_bounds__(256) void reduce_gemm_kernel(ReduceGemm g) {
 // NWM x NWN waves of 32 x 32 blocks of v_mfma_f32_32x32x2f32 (lane half h
 // feeds rows 2i + h of the slice).  Rows go through LDS in
 // double-buffered slices of 32, the next two slices' loads in registers
-// while the current one is multiplied; rows past the range load as zeros.  Row
+// while the current one is multiplied; rows past the range enter LDS as zeros.  Row
 // strides of 32 mod 64 floats: the two half-waves' rows fall in disjoint
 // banks.  The larger tiles read each operand row once per 128 columns
 // instead of once per 64.
