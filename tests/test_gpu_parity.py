@@ -129,6 +129,7 @@ ROUTE_CASES = [
     # over 32 workgroups, two 64-entry groups per wave
     ("e128k2_g6", 3000, 64, 128, 2, 0.2),
     ("t20000_g32", 20000, 64, 16, 2, 0.1),
+    ("e128k16_g32", 8192, 64, 128, 16, 0.3),   # 131072 assignments, four groups per wave
 ]
 
 ROUTER_PATHS = [0, 1, 2]   # automatic, token x expert tiles, 16-token row blocks
