@@ -106,7 +106,7 @@ enum {
  * call moe_hip_invalidate() after changing weight values in place.  Any
  * d_model and ffn_hidden: widths the kernels do not tile are padded with
  * zeros inside the resident layer (same routing bits, same outputs within
- * the layer tolerance); n_experts <= 128 and top_k <= 16.  The same holds for
+ * the layer tolerance); n_experts <= 256 and top_k <= 16.  The same holds for
  * moe_decode_step, moe_decode_batch and moe_block_ffn.
  * On error it prints the reason and aborts, as the reference does on OOM
  * (src/matrix.c:148-158). */
@@ -332,8 +332,9 @@ int moe_hip_set_expert_path(int mode);
  * 2 = 16-token row blocks with every expert in one workgroup, in their own
  * launch.  Automatic routes a decode step of up to 64 tokens (up to 16
  * experts, d_model 256 or 512, finite router weights) inside the fused
- * expert kernel, with the row blocks' arithmetic.  Process-wide; every
- * choice gives the same bits. */
+ * expert kernel, with the row blocks' arithmetic.  The tiles take up to 128
+ * experts; with mode 1 a wider layer routes by row blocks.  Process-wide;
+ * every choice gives the same bits. */
 int moe_hip_set_router_path(int mode);
 
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,

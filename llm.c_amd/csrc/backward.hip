@@ -733,7 +733,9 @@ __global__ __launch_bounds__(256) void slot_kernel(SlotRows Y, const float *dout
 // the selected probabilities; S, c and dp(e) are summed in slot order and
 // the dot over the experts in expert order (through shuffles), as one thread
 // per token would.
-constexpr int kRbG = 8, kRbJ = kMaxExperts / kRbG;
+// JN experts per lane: 16 up to 128 experts, 32 up to 256.
+constexpr int kRbG = 8;
+template <int JN>
 __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, const int *ids,
                                                          const float *gw, const float *dgw,
                                                          const int *counts, int T, int E, int k,
@@ -751,9 +753,9 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, con
         dg[s] = dgw[q];
         w[s] = gw[q];
     }
-    float pv[kRbJ], cn[kRbJ];
+    float pv[JN], cn[JN];
 #pragma unroll
-    for (int j = 0; j < kRbJ; ++j)
+    for (int j = 0; j < JN; ++j)
         if (kRbG * j < E) {
             const int e = min(g + kRbG * j, E - 1);
             pv[j] = p[e];
@@ -769,9 +771,9 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, con
             c = fmaf(dg[s], w[s], c);
         }
     const float aux_scale = aux_coef * (float)E / ((float)T * (float)T * (float)k);
-    float dpv[kRbJ];
+    float dpv[JN];
 #pragma unroll
-    for (int j = 0; j < kRbJ; ++j)
+    for (int j = 0; j < JN; ++j)
         if (kRbG * j < E) {
             const int e = g + kRbG * j;
             float v = aux_scale * cn[j];
@@ -782,7 +784,7 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, con
         }
     float dot = 0.f;
 #pragma unroll
-    for (int j = 0; j < kRbJ; ++j)
+    for (int j = 0; j < JN; ++j)
         if (kRbG * j < E)
 #pragma unroll
             for (int q = 0; q < kRbG; ++q)
@@ -790,7 +792,7 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, con
                     dot = fmaf(__shfl(dpv[j], q, kRbG), __shfl(pv[j], q, kRbG), dot);
     if (t >= T) return;
 #pragma unroll
-    for (int j = 0; j < kRbJ; ++j)
+    for (int j = 0; j < JN; ++j)
         if (g + kRbG * j < E) dlogits[(size_t)t * E + g + kRbG * j] = pv[j] * (dpv[j] - dot);
 }
 
@@ -942,8 +944,15 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         rows(F_{}, T_{}, b.U, F, b.wu, (size_t)d * F, F, b.Y, F, d, 1);
     }
     // Router and dx.
-    hipLaunchKernelGGL(router_bwd_kernel, dim3((unsigned)(((size_t)T * kRbG + 255) / 256)),
-                       dim3(256), 0, s, b.probs, b.ids, b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
+    {
+        const dim3 grid((unsigned)(((size_t)T * kRbG + 255) / 256));
+        if (E <= 128)
+            hipLaunchKernelGGL(router_bwd_kernel<128 / kRbG>, grid, dim3(256), 0, s, b.probs, b.ids,
+                               b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
+        else
+            hipLaunchKernelGGL(router_bwd_kernel<kMaxExperts / kRbG>, grid, dim3(256), 0, s, b.probs,
+                               b.ids, b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
+    }
     hipLaunchKernelGGL(dx_kernel, dim3((unsigned)(((size_t)T * (d / 4) + 255) / 256)), dim3(256),
                        0, s, dXr, b.inv,
                        b.dlogits, b.wrT, T, d, E, k, b.accumulate, b.dx);

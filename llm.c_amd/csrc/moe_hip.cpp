@@ -819,7 +819,7 @@ static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *
         ra.x_raw = nm.x_raw; ra.rms_w = nm.rms_w; ra.rms_eps = nm.eps;
         ra.rms_rcp = 1.0f / (float)L->d; ra.xn_out = const_cast<float *>(x);
     }
-    if (g_rpath != 1) {
+    if (g_rpath != 1 || L->E > 128) {   // (the tile router takes up to 128 experts)
         ra.wrT = L->wrT;
         ra.wr_nonfinite = L->wr_nonfinite;
     }

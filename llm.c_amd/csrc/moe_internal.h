@@ -10,7 +10,7 @@ namespace moe {
 // per-expert tile schedule with the same value.
 constexpr int kGemmBM = 128;
 // Largest expert count the routing kernels support (LDS sizing).
-constexpr int kMaxExperts = 128;
+constexpr int kMaxExperts = 256;
 // Largest top-k the routing kernels support.
 constexpr int kMaxTopK = 16;
 

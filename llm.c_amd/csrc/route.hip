@@ -100,27 +100,36 @@ __device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], i
     }
     __syncthreads();
 
-    // Wave 0 scans counts and m-tiles over the (at most 128) experts, two
-    // per lane.
+    // Wave 0 scans counts and m-tiles over the experts, kEpl consecutive
+    // experts per lane.
     if (w == 0) {
-        const int e0 = 2 * lane, e1 = e0 + 1;
-        int c0 = 0, c1 = 0;
-        for (int ww = 0; ww < NW; ++ww) {
-            if (e0 < E) c0 += hist[ww][e0];
-            if (e1 < E) c1 += hist[ww][e1];
+        constexpr int kEpl = kMaxExperts / 64;
+        int c[kEpl], m[kEpl], cs = 0, ms = 0;
+#pragma unroll
+        for (int j = 0; j < kEpl; ++j) {
+            const int e = kEpl * lane + j;
+            c[j] = 0;
+            for (int ww = 0; ww < NW; ++ww)
+                if (e < E) c[j] += hist[ww][e];
+            if (e < E) a.counts[e] = c[j];
+            m[j] = (c[j] + a.bm - 1) / a.bm;
+            cs += c[j];
+            ms += m[j];
         }
-        if (e0 < E) a.counts[e0] = c0;
-        if (e1 < E) a.counts[e1] = c1;
-        const int m0 = (c0 + a.bm - 1) / a.bm, m1 = (c1 + a.bm - 1) / a.bm;
-        int cs = c0 + c1, ms = m0 + m1;
+        const int c_own = cs, m_own = ms;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int u = __shfl_up(cs, o), v = __shfl_up(ms, o);
             if (lane >= o) { cs += u; ms += v; }
         }
-        const int cb = cs - c0 - c1, mb = ms - m0 - m1;
-        if (e0 < E) { offs[e0] = cb; toff[e0] = mb; }
-        if (e1 < E) { offs[e1] = cb + c0; toff[e1] = mb + m0; }
+        int cb = cs - c_own, mb = ms - m_own;
+#pragma unroll
+        for (int j = 0; j < kEpl; ++j) {
+            const int e = kEpl * lane + j;
+            if (e < E) { offs[e] = cb; toff[e] = mb; }
+            cb += c[j];
+            mb += m[j];
+        }
         if (lane == 63) { offs[E] = cs; toff[E] = ms; }
     }
     __syncthreads();
@@ -186,17 +195,19 @@ constexpr int kDispWaves = 16, kDispMaxGroups = 32;
 // then places its own 16 chunks: a wave's running base per expert lives in
 // lane x, an entry's base comes from its expert's lane (a shuffle), its rank
 // among the group's earlier lanes from the expert bits' ballots, which also
-// give each lane x the group's count of expert x (and x + 64).  Workgroup 0
+// give each lane x the group's count of experts x, x + 64, ....  Workgroup 0
 // writes counts, offsets, tile_off and tile_expert.
-// (Both loops run to the largest bit count, 7 for 128 experts, with
+// (Both loops run to the largest bit count, 8 for 256 experts, with
 // constant indices, so the masks stay in registers.)
+constexpr int kExpertBits = 8;
+static_assert((1 << kExpertBits) >= kMaxExperts, "expert bits");
 struct GroupMasks {
-    uint64_t valid, bit[7];
+    uint64_t valid, bit[kExpertBits];
     // Lanes of the group whose expert is x.
     __device__ uint64_t of(int x, int nbits) const {
         uint64_t m = valid;
 #pragma unroll
-        for (int b = 0; b < 7; ++b)
+        for (int b = 0; b < kExpertBits; ++b)
             if (b < nbits) m &= ((x >> b) & 1) ? bit[b] : ~bit[b];
         return m;
     }
@@ -205,7 +216,7 @@ __device__ inline GroupMasks group_masks(bool valid, int e, int nbits) {
     GroupMasks g;
     g.valid = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 7; ++b) g.bit[b] = __ballot(b < nbits && valid && ((e >> b) & 1));
+    for (int b = 0; b < kExpertBits; ++b) g.bit[b] = __ballot(b < nbits && valid && ((e >> b) & 1));
     return g;
 }
 
@@ -296,7 +307,10 @@ __global__ __launch_bounds__(1024) void dispatch_groups_kernel(DispatchArgs a, i
     __syncthreads();
 
     // Pass 2: this workgroup's chunk g * 16 + w, in order.
-    int b0 = lane < E ? hw[w][lane] : 0, b1 = lane + 64 < E ? hw[w][lane + 64] : 0;
+    constexpr int kEpl = kMaxExperts / 64;   // running bases per lane: experts lane + 64 j
+    int bs[kEpl];
+#pragma unroll
+    for (int j = 0; j < kEpl; ++j) bs[j] = lane + 64 * j < E ? hw[w][lane + 64 * j] : 0;
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const int beg = (g * kDispWaves + w) * CH;
     for (int s0 = 0; s0 < per; s0 += 8) {
@@ -311,10 +325,17 @@ __global__ __launch_bounds__(1024) void dispatch_groups_kernel(DispatchArgs a, i
             const int e = v[u];
             const GroupMasks m = group_masks(valid, e, nbits);
             const uint64_t peers = m.of(e, nbits);
-            const int lo = __shfl(b0, e & 63), hi = __shfl(b1, e & 63);
-            if (valid) a.perm[(e < 64 ? lo : hi) + __popcll(peers & below)] = i;
-            b0 += __popcll(m.of(lane, nbits));
-            if (E > 64) b1 += __popcll(m.of(lane + 64, nbits));
+            int base = 0;
+#pragma unroll
+            for (int j = 0; j < kEpl; ++j)
+                if (64 * j < E) {
+                    const int bj = __shfl(bs[j], e & 63);
+                    if ((e >> 6) == j) base = bj;
+                }
+            if (valid) a.perm[base + __popcll(peers & below)] = i;
+#pragma unroll
+            for (int j = 0; j < kEpl; ++j)
+                if (64 * j < E) bs[j] += __popcll(m.of(lane + 64 * j, nbits));
         }
     }
 }
@@ -335,6 +356,10 @@ hipError_t launch_dispatch_groups(const DispatchArgs &da, hipStream_t s) {
     return hipGetLastError();
 }
 
+// The token x expert tile router (router_kernel) takes up to 128 experts;
+// wider layers route through the row-block router.
+constexpr int kTileRouterMaxExperts = 128;
+
 // Softmax, top-k and gate weights of token t from its logits row (in LDS),
 // which is left holding the probabilities.  The reference's "already chosen"
 // scan over ids[0..ki) (src/transformer.c:321-325) is a set membership test;
@@ -343,7 +368,7 @@ hipError_t launch_dispatch_groups(const DispatchArgs &da, hipStream_t s) {
 __device__ inline void finish_token(const RouteArgs &a, float *row, int t) {
     const int E = a.E, k = a.k;
     softmax_row(row, E);
-    uint64_t chosen[kMaxExperts / 64] = {};
+    uint64_t chosen[kTileRouterMaxExperts / 64] = {};
     float pk[kMaxTopK];
     int idk[kMaxTopK];
 #pragma unroll
@@ -549,7 +574,7 @@ __global__ __launch_bounds__(256) void router_kernel(RouteArgs a, DispatchArgs d
 
 template <int NWV, int RE, int KC, bool SKIP, bool FUSE>
 __global__ __launch_bounds__(64 * NWV) void router_rows_kernel(RouteArgs a, DispatchArgs da) {
-    __shared__ __align__(16) float smem[RowsSmem<KC>::kFloats];
+    __shared__ __align__(16) float smem[RowsSmem<KC, rows_lw(NWV, RE)>::kFloats];
     __shared__ int is_last;
     const int tid = threadIdx.x;
     route_rows_block<NWV, RE, KC, SKIP>(a, blockIdx.x, smem);
@@ -747,6 +772,7 @@ hipError_t launch_rows_kc(const RouteArgs &a, const DispatchArgs &da, hipStream_
         } else {
             if (a.E <= 64)       launch_rows<4, 4, KC, FUSE>(a, da, s);
             else if (a.E <= 128) launch_rows<4, 8, KC, FUSE>(a, da, s);
+            else if (a.E <= 256) launch_rows<8, 8, KC, FUSE>(a, da, s);
             else return hipErrorInvalidValue;
         }
     }

@@ -237,14 +237,25 @@ __device__ inline float finish_token8(const RouteArgs &a, float *row, int l, int
         row[8 * nb + l] = tv;
     }
 
-    uint64_t chosen0 = 0, chosen1 = 0;
+    // The chosen set: one bit per expert in NW words, every word index a
+    // constant after unrolling (a runtime index would put them in scratch).
+    constexpr int NW = (8 * NBM + 63) / 64;
+    uint64_t chosen[NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) chosen[q] = 0;
+    auto is_chosen = [&](int e) {
+        uint64_t bit = 0;
+#pragma unroll
+        for (int q = 0; q < NW; ++q)
+            if ((e >> 6) == q) bit = (chosen[q] >> (e & 63)) & 1ull;
+        return bit != 0;
+    };
     float s = 0.0f;
     for (int ki = 0; ki < k; ++ki) {
         float best = -1.0f;
         int be = 0x7fffffff;
         auto consider = [&](int e, float p) {
-            const uint64_t bit = e < 64 ? (chosen0 >> e) & 1ull : (chosen1 >> (e - 64)) & 1ull;
-            if (!bit && p > best) { best = p; be = e; }
+            if (!is_chosen(e) && p > best) { best = p; be = e; }
         };
 #pragma unroll
         for (int b = 0; b < NBM; ++b)
@@ -261,28 +272,34 @@ __device__ inline float finish_token8(const RouteArgs &a, float *row, int l, int
             be = 0;
             p = row[0];
         }
-        if (be < 64) chosen0 |= 1ull << be;
-        else         chosen1 |= 1ull << (be - 64);
+#pragma unroll
+        for (int q = 0; q < NW; ++q)
+            if ((be >> 6) == q) chosen[q] |= 1ull << (be & 63);
         s = s + p;
         if (l == 0) { id_out[ki] = be; p_out[ki] = p; }
     }
     return (s > 1e-9f) ? 1.0f / s : 0.0f;
 }
 
+// Logits row width of a router block covering 4 NWV RE experts: 129 floats
+// up to 128 experts, 257 up to 256.
+constexpr int rows_lw(int nwv, int re) { return 4 * nwv * re > 128 ? 257 : 129; }
+
 // LDS layout of route_rows_block (floats): x chunks, logits rows, chosen
 // probabilities and experts, renormalisation factors.
-template <int KC>
+template <int KC, int LW = 129>
 struct RowsSmem {
     static constexpr int kLd = KC + 4;
     static constexpr int kLg = 2 * 16 * kLd;
-    static constexpr int kPSel = kLg + 16 * (kMaxExperts + 1);
+    static constexpr int kLw = LW;   // logits row (floats): the experts + 1
+    static constexpr int kPSel = kLg + 16 * LW;
     static constexpr int kIdSel = kPSel + 16 * kMaxTopK;
     static constexpr int kInv = kIdSel + 16 * kMaxTopK;
     static constexpr int kFloats = kInv + 16;
 };
 
 // Routes token block tb (tokens 16*tb ..) with NWV waves; every thread of
-// the workgroup calls this.  smem: RowsSmem<KC>::kFloats floats of LDS,
+// the workgroup calls this.  smem: RowsSmem<KC, rows_lw(NWV, RE)>::kFloats floats of LDS,
 // 16-byte aligned.
 template <int NWV, int RE, int KC, bool SKIP>
 __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem) {
@@ -292,9 +309,9 @@ __device__ void route_rows_block(const RouteArgs &a, int tb, float *smem) {
     constexpr int XQ = 16 * KC / 4;                // float4s of x per chunk
     constexpr int XL = (XQ + NT - 1) / NT;
     constexpr int WV = KC / 16;                    // router VGPRs per expert per chunk
-    using S = RowsSmem<KC>;
+    using S = RowsSmem<KC, rows_lw(NWV, RE)>;
     float (*xs)[16][LD] = reinterpret_cast<float (*)[16][LD]>(smem);
-    float (*lg)[kMaxExperts + 1] = reinterpret_cast<float (*)[kMaxExperts + 1]>(smem + S::kLg);
+    float (*lg)[S::kLw] = reinterpret_cast<float (*)[S::kLw]>(smem + S::kLg);
     float (*p_sel)[kMaxTopK] = reinterpret_cast<float (*)[kMaxTopK]>(smem + S::kPSel);
     int (*id_sel)[kMaxTopK] = reinterpret_cast<int (*)[kMaxTopK]>(smem + S::kIdSel);
     float *inv_sel = smem + S::kInv;

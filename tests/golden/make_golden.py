@@ -13,6 +13,8 @@ small .npz fixtures next to this script:
   golden_route.npz     probs/ids of token samples at every config's router
                        shape (config 5 with its Zipf bias)
   golden_moe.npz       layer outputs of token samples at configs 2-5
+  golden_route_wide.npz probs/ids of routers wider than 128 experts (256
+                       experts top-8; 250 experts top-16, an E % 8 tail)
   golden_rms.npz       rms_norm (src/matrix.c:666-711) rows at the configs'
                        widths and at widths with 8-column and scalar tails
   golden_attn.npz      the decode step's attention sublayer, x after
@@ -28,7 +30,8 @@ ones and W_router by the bias row: the FMA chain's last term is then 1*b[e],
 i.e. logits + b rounded once — the mat_mul_add form the library implements.
 
 Run (where the reference sources are present): python tests/golden/make_golden.py
-(`... make_golden.py rms` / `... attn` write golden_rms.npz / golden_attn.npz only)
+(`... make_golden.py rms` / `... attn` / `... wide` write golden_rms.npz /
+golden_attn.npz / golden_route_wide.npz only)
 """
 import ctypes as C
 import hashlib
@@ -300,12 +303,39 @@ def main_attn():
     np.savez_compressed(os.path.join(HERE, "golden_attn.npz"), **gs)
 
 
+# Routing samples of layers wider than 128 experts (one with an E % 8 tail).
+WIDE_ROUTES = [
+    # name, T, d, E, k, std_router
+    ("e256k8", 64, 128, 256, 8, 0.1),
+    ("e250k16", 40, 64, 250, 16, 0.3),
+]
+
+
+def main_wide():
+    if not orc.ref_available():
+        sys.exit("oracle/_ref/libref_moe.so missing: run `make -C oracle ref` first")
+    orc.orc().orc_set_ftz_daz(1)
+    rt = {}
+    for name, T, d, E, k, std in WIDE_ROUTES:
+        x = orc.synth((T, d), 7, 0, 1.0)
+        wr = orc.synth((d, E), 7, 1, std)
+        z = np.zeros((E, d, 32), np.float32)
+        zd = np.zeros((E, 32, d), np.float32)
+        _, probs, ids = ref_moe(x, HostMoE(wr, z, z, zd, k))
+        rt[f"{name}_probs"], rt[f"{name}_ids"] = probs, ids
+        rt[f"{name}_sha_x"], rt[f"{name}_sha_wr"] = sha(x), sha(wr)
+    np.savez_compressed(os.path.join(HERE, "golden_route_wide.npz"), **rt)
+
+
 if __name__ == "__main__":
     if sys.argv[1:] == ["rms"]:
         main_rms()
     elif sys.argv[1:] == ["attn"]:
         main_attn()
+    elif sys.argv[1:] == ["wide"]:
+        main_wide()
     else:
         main()
         main_rms()
         main_attn()
+        main_wide()

@@ -154,8 +154,8 @@ def run_device_backward(d, F, E, k, T, seed, aux_coef, accumulate_twice=False):
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape", [(128, 512, 4, 2, 256), (256, 1024, 8, 2, 384),
                                    (128, 256, 16, 4, 100), (64, 96, 4, 2, 150),
-                                   (192, 1024, 8, 2, 600)],
-                         ids=["c1", "c2-rows", "e16-k4", "untiled", "d192"])
+                                   (192, 1024, 8, 2, 600), (64, 128, 256, 8, 400)],
+                         ids=["c1", "c2-rows", "e16-k4", "untiled", "d192", "e256-k8"])
 @pytest.mark.parametrize("aux_coef", [0.0, 0.5])
 def test_backward_device_vs_oracle(shape, aux_coef):
     """The tile-engine path (d, F multiples of 64; split partials by slot at

@@ -130,6 +130,10 @@ ROUTE_CASES = [
     ("e128k2_g6", 3000, 64, 128, 2, 0.2),
     ("t20000_g32", 20000, 64, 16, 2, 0.1),
     ("e128k16_g32", 8192, 64, 128, 16, 0.3),   # 131072 assignments, four groups per wave
+    # wider than 128 experts: 8-wave router blocks, four expert bases per lane
+    ("e256k8_g24", 3000, 128, 256, 8, 0.1),
+    ("e160k4", 700, 192, 160, 4, 0.2),
+    ("e250k16_t40", 40, 64, 250, 16, 0.3),     # the router's fused dispatch
 ]
 
 ROUTER_PATHS = [0, 1, 2]   # automatic, token x expert tiles, 16-token row blocks
@@ -153,6 +157,24 @@ def test_route_bitexact(name, T, d, E, k, std_router, path, router_path):
     assert np.array_equal(bits(wr), bits(orc.synth((d, E), 11, 1, std_router)))
     assert_route_equal(route_on_device(layer, x), x, wr, k, E)
     layer.close()
+
+
+WIDE_GOLDEN = [("e256k8", 64, 128, 256, 8, 0.1), ("e250k16", 40, 64, 250, 16, 0.3)]
+
+
+@pytest.mark.parametrize("name,T,d,E,k,std", WIDE_GOLDEN, ids=[c[0] for c in WIDE_GOLDEN])
+def test_route_wide_matches_compiled_reference(name, T, d, E, k, std):
+    """Probabilities and ids of routers wider than 128 experts against the
+    compiled reference's golden bits (same seeded inputs)."""
+    say(f"route wide golden {name}: T={T} d={d} E={E} k={k}")
+    g = np.load(os.path.join(GOLDEN, "golden_route_wide.npz"))
+    layer = mh.Layer(d, 64, E, k)
+    layer.fill_synthetic(7, std, 0.02)
+    x = orc.synth((T, d), 7, 0, 1.0)
+    probs, ids = route_on_device(layer, x)[:2]
+    layer.close()
+    assert np.array_equal(bits(probs), bits(g[f"{name}_probs"]))
+    assert np.array_equal(ids, g[f"{name}_ids"])
 
 
 @pytest.mark.parametrize("path", ROUTER_PATHS, ids=["auto", "tiles", "rows"])
@@ -561,6 +583,8 @@ EDGE_CASES = [
     ("t129", 129, 192, 160, 6, 2),
     ("k_eq_e", 70, 64, 64, 4, 4),
     ("e3", 200, 128, 128, 3, 2),
+    ("e256_k8", 300, 64, 64, 256, 8),
+    ("e130", 90, 128, 96, 130, 2),
 ]
 
 
@@ -599,7 +623,7 @@ def test_error_paths():
     x = orc.synth((4, 128), 0, 0, 1.0)
     with pytest.raises(mh.MoeHipError):
         mh.moe_forward(x, bad)
-    many = host_layer(64, 32, 130, 2, 0, 0.02, 0.02)    # n_experts above the supported 128
+    many = host_layer(64, 32, 260, 2, 0, 0.02, 0.02)    # n_experts above the supported 256
     with pytest.raises(mh.MoeHipError):
         mh.moe_forward(orc.synth((4, 64), 0, 0, 1.0), many)
 

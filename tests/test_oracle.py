@@ -254,6 +254,19 @@ def test_routing_samples_match_compiled_reference(name):
     assert np.array_equal(ids, g[f"{name}_ids"])
 
 
+@pytest.mark.parametrize("name,T,d,E,k,std", mg.WIDE_ROUTES, ids=[c[0] for c in mg.WIDE_ROUTES])
+def test_wide_routing_matches_compiled_reference(name, T, d, E, k, std):
+    """Routers wider than 128 experts (the 8-lane softmax blocks, the E % 8
+    tail and top-16) against the compiled reference's bits."""
+    g = load("golden_route_wide.npz")
+    x = orc.synth((T, d), 7, 0, 1.0)
+    wr = orc.synth((d, E), 7, 1, std)
+    assert mg.sha(x) == str(g[f"{name}_sha_x"]) and mg.sha(wr) == str(g[f"{name}_sha_wr"])
+    probs, ids, _ = orc.route(x, wr, k)
+    assert np.array_equal(bits(probs), bits(g[f"{name}_probs"]))
+    assert np.array_equal(ids, g[f"{name}_ids"])
+
+
 @pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5"])
 def test_layer_samples_match_compiled_reference(name):
     g = load("golden_moe.npz")
