@@ -78,7 +78,7 @@ __device__ void dispatch_body(const DispatchArgs &a, int (*hist)[kMaxExperts], i
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int E = a.E, n = a.n;
-    for (int i = tid; i < NW * kMaxExperts; i += NT) (&hist[0][0])[i] = 0;
+    for (int x = lane; x < E; x += 64) hist[w][x] = 0;   // (the experts in use)
     __syncthreads();
 
     const int chunk = ((n + NW * 64 - 1) / (NW * 64)) * 64;
@@ -229,8 +229,10 @@ __global__ __launch_bounds__(1024) void dispatch_groups_kernel(DispatchArgs a, i
     const int G = gridDim.x, g = blockIdx.x, E = a.E, n = a.n;
     int nbits = 0;
     while ((1 << nbits) < E) ++nbits;
-    for (int i = tid; i < kDispMaxGroups * kMaxExperts; i += 1024) (&hg[0][0])[i] = 0;
-    for (int i = tid; i < kDispWaves * kMaxExperts; i += 1024) (&hw[0][0])[i] = 0;
+    // (Only the rows and columns in use are cleared: G ranges, E experts.)
+    for (int gg = w; gg < G; gg += kDispWaves)
+        for (int x = lane; x < E; x += 64) hg[gg][x] = 0;
+    for (int x = lane; x < E; x += 64) hw[w][x] = 0;
     __syncthreads();
 
     // Pass 1: wave w counts chunks gg * 16 + w, gg < G (LDS atomics per
