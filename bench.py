@@ -28,10 +28,12 @@ Also measured in the same run (each a median of K marked steps unless said):
   * decode_step: the whole block stack of that decode step (GQA attention
     over a 1024-position KV cache, then the MoE FFN sublayer, per block) with
     the residual stream on the device;
-  * cpu_baseline: the CPU oracle (a restatement of the reference's
-    moe_forward, bit-identical routing) on a bounded token sample of the same
-    prefill workload, on this host's cores: one warm-up pass, then the median
-    of 5 passes.
+  * cpu_baseline: the reference's own moe_forward, compiled from its
+    sources (oracle/_ref), on a bounded token sample of the same prefill
+    layer, on one host thread as that build runs it (its 1-row expert
+    products are not parallelised): one warm-up pass, then the median of 5
+    passes; cpu_port_all_threads: the oracle port on every host thread,
+    parallel over tokens, for context.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
 """
@@ -398,12 +400,68 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, pass_s=2.5, threads=None):
-    """Oracle moe_forward on the first tokens of the prefill workload with
-    `threads` host threads (all cores by default): the sample is sized so one
-    pass takes about pass_s seconds, then one warm-up pass and the median of
-    5 timed passes.  Tokens/s extrapolates linearly (tokens are independent in
-    the reference loop, src/transformer.c:312)."""
+# How oracle/Makefile builds the reference's own MoE path (oracle/_ref).
+REF_BUILD = ("gcc -O3 -march=native -ffast-math -funroll-loops -flto -fopenmp, the reference's "
+             "release flags minus -DUSE_OPENBLAS (its AVX2+FMA mat_mul; oracle/Makefile)")
+
+
+def _sized_passes(run, n0, n_max, pass_s):
+    """Calibrate a sample size n so one pass of run(n) takes about pass_s
+    seconds, run one warm-up pass at that size, then time 5 passes; returns
+    (n, median seconds)."""
+    n = n0
+    for _ in range(2):   # calibration (small samples run slower per token)
+        secs = run(n)
+        n = int(min(n_max, max(n, n * pass_s / max(secs, 1e-6))))
+    run(n)
+    return n, float(np.median([run(n) for _ in range(5)]))
+
+
+def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, pass_s=2.5):
+    """The CPU baseline of the prefill layer: the reference's own moe_forward
+    (src/transformer.c:287-366, compiled from its sources into oracle/_ref)
+    on the first tokens of the same layer's rows and weights, on one host
+    thread, which is how that build runs the layer: its expert products are
+    1-row mat_muls, and mat_mul only parallelises blocks of 128+ rows
+    (src/matrix.c:385).  The reference has no router bias, so it routes
+    without one; its per-token work (k experts, three 1-row products each)
+    is the same either way.  Tokens/s extrapolates linearly: tokens are
+    independent in its loop (src/transformer.c:312).  Falls back to the
+    oracle port (one thread) where oracle/_ref was not built."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import orc
+    layer = st["layer"]
+    wr = layer.get_router()
+    xh = st["x"].to_host()
+    ex = st.setdefault("host_experts", {})
+    kind = "reference" if orc.ref_available() else "port"
+
+    def run(n):
+        xs = np.ascontiguousarray(xh[:n])
+        _, ids, _ = orc.route(xs, wr, k)
+        for e in sorted(set(ids.ravel().tolist()) - set(ex)):
+            ex[e] = layer.get_expert(e)
+        t0 = time.perf_counter()
+        if kind == "reference":
+            orc.ref_moe_forward_experts(xs, wr, ex, d, F, E, k, threads=1)
+        else:
+            orc.moe_forward_experts(xs, wr, ex, d, F, E, k, None, nthreads=1)
+        return time.perf_counter() - t0
+
+    n, med = _sized_passes(run, 4, T, pass_s)
+    what = (f"the reference's moe_forward built from its sources ({REF_BUILD})"
+            if kind == "reference" else "the oracle port (oracle/Makefile)")
+    return dict(value=n / med, unit="tokens/s", cores=1, kind=kind,
+                sample=f"first {n} of {T} tokens of the same layer (router bias off: the "
+                       f"reference has none), warm-up then median of 5 passes ({med:.2f} s "
+                       f"each), 1 thread, as that build runs each token's expert products; "
+                       f"{cpu_model()}; {what}")
+
+
+def cpu_port_threads(mh, st, T=16384, d=2048, F=8192, E=64, k=4, pass_s=2.5, threads=None):
+    """Context for the baseline above: the oracle port of the same layer
+    (bias included) on every host thread, parallelised over tokens, which
+    the reference's build does not do."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     layer, ids = st["layer"], st["ids"]
@@ -420,23 +478,19 @@ def cpu_baseline(mh, st, T=16384, d=2048, F=8192, E=64, k=4, pass_s=2.5, threads
         orc.moe_forward_experts(xs, wr, ex, d, F, E, k, st["bias"], nthreads=threads)
         return time.perf_counter() - t0
 
-    n = max(4 * threads, 8)
-    for _ in range(2):   # calibration (small samples run slower per token)
-        secs = run(n)
-        n = int(min(T, max(n, n * pass_s / max(secs, 1e-6))))
-    run(n)               # warm-up at the sample size
-    times = [run(n) for _ in range(5)]
-    med = float(np.median(times))
+    n, med = _sized_passes(run, max(4 * threads, 8), T, pass_s)
     return dict(value=n / med, unit="tokens/s", cores=threads, kind="port",
-                sample=f"first {n} of {T} tokens of the same prefill layer, warm-up then "
-                       f"median of 5 passes ({med:.2f} s each), {threads} threads, "
-                       f"{cpu_model()}; oracle built with {ORACLE_BUILD}")
+                sample=f"first {n} of {T} tokens of the same prefill layer, warm-up then median "
+                       f"of 5 passes ({med:.2f} s each), {threads} threads each taking whole "
+                       f"tokens (the reference runs a token's experts on one thread, "
+                       f"src/matrix.c:385); {cpu_model()}; oracle built with {ORACLE_BUILD}")
 
 
 def cpu_decode_baseline(mh, T=64, d=512, F=2048, E=16, k=2, n_layers=8):
-    """Oracle moe_forward on the 64 decode rows of one layer (all experts
-    host-resident), all host threads, warm-up then the median of 5; decode
-    tokens/s = 64 / (8 layers x that time)."""
+    """The reference's moe_forward (oracle/_ref; the oracle port where it
+    was not built) on the 64 decode rows of one layer, one thread as that
+    build runs it, warm-up then the median of 5; decode tokens/s = 64 / (8
+    layers x that time)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
     L = mh.Layer(d, F, E, k)
@@ -445,18 +499,24 @@ def cpu_decode_baseline(mh, T=64, d=512, F=2048, E=16, k=2, n_layers=8):
     wr = L.get_router()
     L.close()
     x = np.random.default_rng(3).standard_normal((T, d)).astype(np.float32)
-    threads = os.cpu_count() or 1
-    orc.moe_forward_experts(x, wr, ex, d, F, E, k, None, nthreads=threads)
-    times = []
-    for _ in range(5):
+    kind = "reference" if orc.ref_available() else "port"
+
+    def run():
         t0 = time.perf_counter()
-        orc.moe_forward_experts(x, wr, ex, d, F, E, k, None, nthreads=threads)
-        times.append(time.perf_counter() - t0)
-    layer_s = float(np.median(times))
-    return dict(value=T / (n_layers * layer_s), unit="tokens/s", cores=threads, kind="port",
+        if kind == "reference":
+            orc.ref_moe_forward_experts(x, wr, ex, d, F, E, k, threads=1)
+        else:
+            orc.moe_forward_experts(x, wr, ex, d, F, E, k, None, nthreads=1)
+        return time.perf_counter() - t0
+
+    run()
+    layer_s = float(np.median([run() for _ in range(5)]))
+    what = (f"the reference's moe_forward built from its sources ({REF_BUILD})"
+            if kind == "reference" else "the oracle port (oracle/Makefile)")
+    return dict(value=T / (n_layers * layer_s), unit="tokens/s", cores=1, kind=kind,
                 sample=f"one MoE layer on the 64 decode rows, x{n_layers} layers, warm-up then "
-                       f"median of 5 ({layer_s * 1e3:.1f} ms per layer), {threads} threads, "
-                       f"{cpu_model()}; oracle built with {ORACLE_BUILD}")
+                       f"median of 5 ({layer_s * 1e3:.1f} ms per layer), 1 thread; "
+                       f"{cpu_model()}; {what}")
 
 
 def main():
@@ -531,12 +591,12 @@ def main():
             L.close()
         stp = decode_step(mh, args.steps, args.warmup)
         log("decode_step", json.dumps(stp))
-    cpu = cpu1 = cpu_dec = None
+    cpu = cpu_all = cpu_dec = None
     if not args.no_cpu:
         cpu = cpu_baseline(mh, st)
         log("cpu", json.dumps(cpu))
-        cpu1 = cpu_baseline(mh, st, pass_s=1.0, threads=1)
-        log("cpu 1 thread", json.dumps(cpu1))
+        cpu_all = cpu_port_threads(mh, st)
+        log("cpu port, all threads", json.dumps(cpu_all))
         cpu_dec = cpu_decode_baseline(mh)
         log("cpu decode", json.dumps(cpu_dec))
 
@@ -574,7 +634,7 @@ def main():
                                      pre["phase_ms"])),
         "expert_load_max_over_mean": pre["counts_max_over_mean"],
         "cpu_baseline": cpu,
-        "cpu_baseline_1thread": cpu1,
+        "cpu_port_all_threads": cpu_all,
     }
     line["prefill_host_io"] = {
         "workload": "the headline layer with x from and out / probs / ids to pageable host "

@@ -337,6 +337,13 @@ int moe_hip_set_expert_path(int mode);
  * every choice gives the same bits. */
 int moe_hip_set_router_path(int mode);
 
+/* Which kernels the library's last layer forward ran (no
+ * counterpart in the reference; for tests and tuning): 1 = router launch and
+ * grouped GEMMs, 2 = router launch and the fused decode kernel, 3 = router
+ * launch and the two-launch decode, 4 = the fused decode kernel with the
+ * routing inside; 0 before any forward. */
+int moe_hip_last_forward_path(void);
+
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,
  * src/matrix.c:82-116) or glibc-expf restatement (which = 1) of x[i], the two
  * scalar exponentials the routing softmax uses. */

@@ -47,6 +47,7 @@ hipEvent_t g_marks[kMarks] = {};
 bool g_have_times = false;
 int g_path = 0;   // 0 auto, 1 grouped GEMMs, 2 decode GEMVs (fused), 3 decode GEMVs (two launches)
 int g_rpath = 0;  // 0 auto, 1 token x expert tiles, 2 one token per lane
+int g_last_path = 0;   // moe_hip_last_forward_path
 // A captured graph keeps the workspace addresses it recorded, so the
 // workspace must not be freed and reallocated while one may still run:
 // graphs made by moe_hip_graph_end and not yet destroyed, a capture begun by
@@ -86,10 +87,14 @@ int ensure_init() {
     return moe_hip_init(-1);
 }
 
-// The stream a call runs on (NULL: the library stream).  Notes a capture
-// the caller began on it (see g_ext_capture).
+// The stream a call runs on (NULL: the library stream), for calls that
+// record no workspace address (the allocation-free forward, fills, norms).
+hipStream_t stream_of(void *s) { return s ? static_cast<hipStream_t>(s) : g_stream; }
+
+// The same for calls whose launches take workspace addresses: notes a
+// capture the caller began on the stream (see g_ext_capture).
 hipStream_t pick_stream(void *s) {
-    hipStream_t st = s ? static_cast<hipStream_t>(s) : g_stream;
+    hipStream_t st = stream_of(s);
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (!g_api_capture && hipStreamIsCapturing(st, &cs) == hipSuccess &&
         cs == hipStreamCaptureStatusActive)
@@ -795,7 +800,7 @@ int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed, uint64_t stream
                             float std, void *stream) {
     TRY(ensure_init());
     if (!dst && n) return set_err(MOE_HIP_ERR_ARG, "null destination");
-    HIP_TRY(moe::launch_fill_normal(dst, n, seed, stream_id, mean, std, pick_stream(stream)));
+    HIP_TRY(moe::launch_fill_normal(dst, n, seed, stream_id, mean, std, stream_of(stream)));
     return MOE_HIP_OK;
 }
 
@@ -803,7 +808,7 @@ int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream
     TRY(ensure_init());
     if (which != 0 && which != 1) return set_err(MOE_HIP_ERR_ARG, "which must be 0 or 1");
     if (n && (!x || !y)) return set_err(MOE_HIP_ERR_ARG, "null pointer");
-    HIP_TRY(moe::launch_eval_exp(which, x, y, n, pick_stream(stream)));
+    HIP_TRY(moe::launch_eval_exp(which, x, y, n, stream_of(stream)));
     return MOE_HIP_OK;
 }
 
@@ -1024,6 +1029,7 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
         TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
                        b.tile_expert, b.counters, s, !p.use_decode, nm));
     }
+    g_last_path = routed ? 4 : !p.use_decode ? 1 : p.fused ? 2 : 3;
     if (routed) {
         // (the expert products ran with the routing)
     } else if (p.use_decode) {
@@ -1102,7 +1108,9 @@ int moe_hip_forward_dev_noalloc(MoeHipLayer *L, const float *x, int T, float *ou
     if (!L || T < 0 || (T > 0 && (!x || !out))) return set_err(MOE_HIP_ERR_ARG, "bad forward arguments");
     if (!g_init) return set_err(MOE_HIP_ERR_ARG, "the library is not initialised (moe_hip_init)");
     if (T == 0) return MOE_HIP_OK;
-    hipStream_t s = pick_stream(stream);
+    // (its launches take only scratch addresses: a capture of this call
+    // leaves the workspace free to grow)
+    hipStream_t s = stream_of(stream);
     char *base = nullptr;
     TRY(scratch_of(s, &base));
     FwdPlan p;
@@ -1122,6 +1130,8 @@ int moe_hip_set_router_path(int mode) {
     g_rpath = mode;
     return MOE_HIP_OK;
 }
+
+int moe_hip_last_forward_path(void) { return g_last_path; }
 
 int moe_hip_set_expert_path(int mode) {
     if (mode < 0 || mode > 3) return set_err(MOE_HIP_ERR_ARG, "expert path mode %d", mode);
@@ -1242,7 +1252,7 @@ int moe_hip_rms_norm_dev(const float *x, const float *w, float eps, int rows, in
         return set_err(MOE_HIP_ERR_ARG, "bad rms_norm arguments");
     if (rows == 0) return MOE_HIP_OK;
     TRY(ensure_init());
-    HIP_TRY(moe::launch_rms_norm(x, w, eps, rows, cols, y, pick_stream(stream)));
+    HIP_TRY(moe::launch_rms_norm(x, w, eps, rows, cols, y, stream_of(stream)));
     return MOE_HIP_OK;
 }
 

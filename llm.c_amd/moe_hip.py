@@ -78,6 +78,7 @@ SIGNATURES = {
     "moe_hip_set_timing": (C.c_int, [C.c_int]),
     "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
     "moe_hip_set_router_path": (C.c_int, [C.c_int]),
+    "moe_hip_last_forward_path": (C.c_int, []),
     "moe_hip_backward_dev": (C.c_int, [_P, _P, C.c_int, _P, C.c_float, _P, _P, _P, _P, _P, _P,
                                        C.c_int, _P]),
     "moe_hip_decode_block_dev": (C.c_int, [_P, _P, _P, _P, C.c_int, _P, _P, _P, C.c_float, _P,
@@ -421,6 +422,13 @@ def set_expert_path(mode):
 def set_router_path(mode):
     """0 automatic, 1 token x expert tiles, 2 16-token row blocks."""
     check(lib().moe_hip_set_router_path(int(mode)))
+
+
+def last_forward_path():
+    """Kernels of the last layer forward: 1 router + grouped GEMMs, 2 router +
+    fused decode kernel, 3 router + two-launch decode, 4 fused decode kernel
+    with the routing inside."""
+    return int(lib().moe_hip_last_forward_path())
 
 
 def set_timing(on):

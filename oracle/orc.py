@@ -199,6 +199,43 @@ def moe_forward_experts(x, wr, experts, d, F, E, k, bias=None, nthreads=1):
     return out, probs, ids
 
 
+def ref_moe_forward_experts(x, wr, experts, d, F, E, k, threads=1):
+    """The compiled reference's own moe_forward (oracle/_ref/libref_moe.so,
+    src/transformer.c:287-366 built with the release flags) on x [T x d],
+    with OpenMP limited to `threads`; FTZ/DAZ on, as its executables run.
+    `experts` maps expert id -> (wg, wu, wd) and must hold every expert the
+    rows choose (the reference has no router bias; `route` gives its ids).
+    Returns (out, probs, ids)."""
+    from abi_types import FFNWeights, Matrix, MoEWeights, ModelConfig, make_cache, matrix
+    T = x.shape[0]
+    _, need, _ = route(x, wr, k)
+    missing = set(need.ravel().tolist()) - set(experts)
+    if missing:
+        raise ValueError(f"experts {sorted(missing)} are chosen but not materialised")
+    arr = (FFNWeights * E)()
+    empty = Matrix(None, None, 0, 0)
+    for e in range(E):
+        arr[e] = (FFNWeights(matrix(experts[e][0]), matrix(experts[e][1]), matrix(experts[e][2]))
+                  if e in experts else FFNWeights(empty, empty, empty))
+    w = MoEWeights(C.cast(arr, C.POINTER(FFNWeights)), matrix(wr), E, k)
+    cfg = ModelConfig(vocab_size=0, max_seq_len=T, d_model=d, n_layers=1, n_heads=1,
+                      n_kv_heads=1, head_dim=d, window_size=0, ffn_hidden=F, n_experts=E,
+                      top_k_experts=k, rms_norm_eps=1e-5, rope_theta=10000.0)
+    fc, probs, ids = make_cache(T, E, k)
+    out = np.zeros((T, d), np.float32)
+    gomp = C.CDLL("libgomp.so.1")
+    prev = gomp.omp_get_max_threads()
+    gomp.omp_set_num_threads(threads)
+    orc().orc_set_ftz_daz(1)
+    try:
+        ref().moe_forward(C.byref(matrix(x)), C.byref(w), C.byref(cfg), C.byref(fc),
+                          C.byref(matrix(out)))
+    finally:
+        orc().orc_set_ftz_daz(0)
+        gomp.omp_set_num_threads(prev)
+    return out, probs, ids
+
+
 def moe_forward_f64(x, hw, ids, probs):
     T = x.shape[0]
     out = np.empty((T, hw.d), np.float64)

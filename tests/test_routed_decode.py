@@ -43,15 +43,23 @@ def host_layer(d, F, E, k, seed, std_router, std_expert):
 
 
 CASES = [
-    # name, T, d, F, E, k, bias, std_router
-    ("c4", 64, 512, 2048, 16, 2, False, 0.02),
-    ("t1", 1, 512, 256, 16, 2, False, 0.1),
-    ("t7_e8_k1", 7, 256, 256, 8, 1, False, 0.1),          # one expert per token, RE = 1
-    ("t33_e12_k3_bias", 33, 512, 384, 12, 3, True, 0.1),  # E % 8 tail, ragged last block
-    ("t64_e3_k3", 64, 256, 256, 3, 3, False, 0.5),        # k == E: every expert per token
-    ("t48_e16_k4_bias", 48, 512, 256, 16, 4, True, 0.1),
-    ("t17_e16_k16", 17, 256, 128, 16, 16, False, 0.1),    # all 16 experts, 272 slots
-    ("t64_e16_k2_hot", 64, 512, 256, 16, 2, True, 0.1),   # biased: one expert takes > 32 rows
+    # name, T, d, F, E, k, bias, std_router, routed (the routing runs inside
+    # the fused kernel; otherwise the rows, results and slot lists exceed
+    # its 160 KB of LDS and the router launch runs first)
+    ("c4", 64, 512, 2048, 16, 2, False, 0.02, True),
+    ("t1", 1, 512, 256, 16, 2, False, 0.1, True),
+    ("t7_e8_k1", 7, 256, 256, 8, 1, False, 0.1, True),          # one expert per token, RE = 1
+    ("t33_e12_k3_bias", 33, 512, 384, 12, 3, True, 0.1, True),  # E % 8 tail, ragged last block
+    ("t64_e3_k3", 64, 256, 256, 3, 3, False, 0.5, True),        # k == E: every expert per token
+    ("t48_e16_k4_bias", 48, 512, 256, 16, 4, True, 0.1, True),
+    ("t17_e16_k16", 17, 256, 128, 16, 16, False, 0.1, True),    # all 16 experts, 272 slots
+    ("t64_e16_k2_hot", 64, 512, 256, 16, 2, True, 0.1, True),   # biased: one expert takes > 32 rows
+    # more slots than the workgroup's 512 threads: the slot lists take
+    # several ballot rounds (576 and 1024 slots)
+    ("t64_e16_k9", 64, 256, 256, 16, 9, False, 0.1, True),
+    ("t64_e16_k16", 64, 256, 128, 16, 16, False, 0.1, True),
+    ("t64_d512_e16_k9", 64, 512, 256, 16, 9, False, 0.1, True),    # 159 KB of LDS
+    ("t64_d512_e16_k16", 64, 512, 128, 16, 16, False, 0.1, False),  # 166 KB: router launch
 ]
 
 
@@ -74,8 +82,10 @@ def bias_of(name, E):
     return b
 
 
-@pytest.mark.parametrize("name,T,d,F,E,k,bias,std_router", CASES, ids=[c[0] for c in CASES])
-def test_routed_matches_router_launch_and_oracle(name, T, d, F, E, k, bias, std_router, paths):
+@pytest.mark.parametrize("name,T,d,F,E,k,bias,std_router,routed", CASES,
+                         ids=[c[0] for c in CASES])
+def test_routed_matches_router_launch_and_oracle(name, T, d, F, E, k, bias, std_router, routed,
+                                                 paths):
     say(f"routed decode {name}: T={T} d={d} F={F} E={E} k={k}")
     mh.set_expert_path(2)      # the fused decode kernel
     layer = mh.Layer(d, F, E, k)
@@ -95,6 +105,9 @@ def test_routed_matches_router_launch_and_oracle(name, T, d, F, E, k, bias, std_
         dids = mh.DeviceArray((T, k), np.int32)
         layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr, accumulate=1)
         mh.synchronize()
+        # path 0 must be the routed kernel (4) where it fits, path 2 the
+        # router launch before the fused kernel (2)
+        assert mh.last_forward_path() == (4 if rp == 0 and routed else 2), mh.last_forward_path()
         res[rp] = (dout.to_host(), dprobs.to_host(), dids.to_host())
     for a, c in zip(res[0], res[2]):
         assert np.array_equal(bits(a), bits(c)), "routing inside the kernel changed the bits"
@@ -130,6 +143,7 @@ def test_routed_ffn_sublayer(T, d, F, E, k, paths):
         dids = mh.DeviceArray((T, k), np.int32)
         layer.ffn_sublayer_dev(dx.ptr, dw.ptr, 1e-5, T, dxn.ptr, dprobs.ptr, dids.ptr)
         mh.synchronize()
+        assert mh.last_forward_path() == (4 if rp == 0 else 2), mh.last_forward_path()
         res[rp] = (dx.to_host(), dxn.to_host(), dprobs.to_host(), dids.to_host())
     for a, c in zip(res[0], res[2]):
         assert np.array_equal(bits(a), bits(c)), "routing inside the kernel changed the bits"

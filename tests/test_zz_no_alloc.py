@@ -140,3 +140,57 @@ def test_noalloc_refuses_oversized_call():
         mh.synchronize()
     finally:
         layer.close()
+
+
+CHILD = r"""
+import ctypes as C, os, sys
+import numpy as np
+sys.path[:0] = sys.argv[1:3]
+import moe_hip as mh
+hip = C.CDLL(os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "libamdhip64.so"))
+mh.check(mh.lib().moe_hip_init(0))
+T, d, F, E, k = 64, 512, 2048, 16, 2
+small = mh.Layer(d, F, E, k)
+small.fill_synthetic(14, 0.02, 0.02)
+x = mh.DeviceArray((T, d))
+mh.fill_normal_dev(x.ptr, T * d, 14, 0, 0.0, 1.0)
+out, ref = mh.DeviceArray((T, d)), mh.DeviceArray((T, d))
+small.forward_dev_noalloc(x.ptr, T, ref.ptr)
+mh.synchronize()
+s, g, ge = C.c_void_p(), C.c_void_p(), C.c_void_p()
+assert hip.hipStreamCreate(C.byref(s)) == 0
+assert hip.hipStreamBeginCapture(s, 1) == 0          # thread-local mode
+small.forward_dev_noalloc(x.ptr, T, out.ptr, stream=s)
+assert hip.hipStreamEndCapture(s, C.byref(g)) == 0
+assert hip.hipGraphInstantiate(C.byref(ge), g, None, None, 0) == 0
+assert hip.hipGraphLaunch(ge, s) == 0
+assert hip.hipStreamSynchronize(s) == 0
+assert np.array_equal(out.to_host().view(np.uint32), ref.to_host().view(np.uint32))
+assert hip.hipGraphExecDestroy(ge) == 0 and hip.hipGraphDestroy(g) == 0
+assert hip.hipStreamDestroy(s) == 0
+# The capture recorded no workspace address, so the workspace may grow:
+# a wider layer's synthetic fill stages more than the first one did, and a
+# forward of it through the workspace entry point sizes new buffers.
+big = mh.Layer(d, 2 * F, E, k)
+big.fill_synthetic(15, 0.02, 0.02)
+big.forward_dev(x.ptr, T, out.ptr)
+mh.synchronize()
+print("child ok", flush=True)
+"""
+
+
+def test_noalloc_captured_on_caller_stream_leaves_workspace_growable():
+    """A capture the caller begins on its own stream, with only the
+    allocation-free entry point recorded into it, must not pin the
+    workspace: afterwards calls that grow it still succeed (in a fresh
+    process, so that the first sizing is known to be the small layer's)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    say("noalloc captured on a caller stream, then a workspace-growing call (child process)")
+    r = subprocess.run([sys.executable, "-c", CHILD, os.path.join(root, "llm.c_amd"),
+                        os.path.join(root, "oracle")], capture_output=True, text=True,
+                       timeout=180)
+    say(r.stdout.strip(), r.stderr.strip()[-2000:])
+    assert r.returncode == 0 and "child ok" in r.stdout
