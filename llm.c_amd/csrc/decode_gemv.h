@@ -129,9 +129,14 @@ __device__ inline WSrc wsrc(const float *block, size_t nfloats, unsigned lo) {
                 lo};
 }
 
-// The 16-byte piece at byte offset off (wave-uniform) of a weight row.
+// The 16-byte piece at byte offset off (wave-uniform) of a weight row, as a
+// non-temporal (streaming) load: every weight byte is read once per step, and
+// a plain read of 192 MiB over 256 workgroups runs at 5.9-6.0 TB/s this way
+// against 5.5 TB/s with the default policy (the decode layer: 46.4-46.9 ->
+// 44.1-44.8 us).
+constexpr int kCachePolicyNt = 2;
 __device__ inline floatx4 ldw(const WSrc &s, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(s.r, s.lo, off, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(s.r, s.lo, off, kCachePolicyNt);
 }
 
 // Byte size of a unit (a 16-wide K step of 16 rows).
