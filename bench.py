@@ -116,23 +116,17 @@ def prefill(mh, steps, warmup, T=16384, d=2048, F=8192, E=64, k=4, seed=5):
 
 
 def prefill_host_io(mh, st, steps=5):
-    """The headline layer with its activations in pageable host memory: x
-    copied in, the layer, out / probs / ids copied back, synchronous (the
-    moe_forward drop-in's data movement, on the same router-biased layer)."""
-    layer, x, out, probs, ids = st["layer"], st["x"], st["out"], st["probs"], st["ids_dev"]
+    """The headline layer with its activations in pageable host memory
+    (moe_hip_forward_host: x up, out / probs / ids back through the pinned
+    staging, as the moe_forward drop-in moves them; same router-biased
+    layer, weights resident), wall time of the synchronous call."""
+    layer, x, probs, ids = st["layer"], st["x"], st["probs"], st["ids_dev"]
     T, d = x.shape
     xh = x.to_host()
     oh = np.empty_like(xh)
     ph = np.empty(probs.shape, np.float32)
     ih = np.empty(ids.shape, np.int32)
-
-    def call():
-        x.upload(xh)
-        layer.forward_dev(x.ptr, T, out.ptr, probs.ptr, ids.ptr)
-        mh.check(mh.lib().moe_hip_memcpy(oh.ctypes.data_as(mh._P), out.ptr, oh.nbytes, 2))
-        mh.check(mh.lib().moe_hip_memcpy(ph.ctypes.data_as(mh._P), probs.ptr, ph.nbytes, 2))
-        mh.check(mh.lib().moe_hip_memcpy(ih.ctypes.data_as(mh._P), ids.ptr, ih.nbytes, 2))
-
+    call = lambda: layer.forward_host(xh, oh, ph, ih)
     call()
     per = []
     for _ in range(steps):
@@ -142,7 +136,8 @@ def prefill_host_io(mh, st, steps=5):
     s = stats(per)
     pcie = float(xh.nbytes + oh.nbytes + ph.nbytes + ih.nbytes)
     return dict(T=T, ms=s["median"], step_ms=s, tokens_per_s=T / (s["median"] * 1e-3),
-                pcie_bytes=pcie)
+                pcie_bytes=pcie, up_bytes=float(xh.nbytes), down_bytes=float(oh.nbytes),
+                overlapped_bytes=float(ph.nbytes + ih.nbytes))
 
 
 def layer_bench(mh, steps, warmup, T, d, F, E, k, std_router, seed):
@@ -539,13 +534,23 @@ def main():
 
     if args.only == "copy":
         # Calibration for the HBM traffic counters: one 1 GiB device-to-device
-        # copy (1 GiB read + 1 GiB written).
+        # copy (1 GiB read + 1 GiB written), then 1 GiB read through each load
+        # path of the kernels (LDS DMA, vector loads, non-temporal vector
+        # loads; moe_hip_read_probe), each from a buffer not read before.
         n = 1 << 28
         a, b = mh.DeviceArray((n,)), mh.DeviceArray((n,))
         mh.fill_normal_dev(a.ptr, n, 1, 0, 0.0, 1.0)
         mh.synchronize()
         mh.check(mh.lib().moe_hip_memcpy(b.ptr, a.ptr, 4 * n, 3))
-        log("copy", json.dumps({"bytes": 4 * n}))
+        out = mh.DeviceArray((1024,))
+        for mode in range(3):
+            src = mh.DeviceArray((n,))
+            mh.fill_normal_dev(src.ptr, n, 2 + mode, 0, 0.0, 1.0)
+            mh.synchronize()
+            mh.check(mh.lib().moe_hip_read_probe(src.ptr, 4 * n, mode, out.ptr, None))
+            mh.synchronize()
+            src.free()
+        log("copy", json.dumps({"bytes": 4 * n, "probes": ["lds_dma", "vector", "vector_nt"]}))
         return
     small_shape = dict(T=4096, d=256, F=1024, E=8, k=2, std_router=0.1, seed=2)
     c3_shape = dict(T=4096, d=512, F=2048, E=8, k=2, std_router=0.02, seed=3)
@@ -569,6 +574,8 @@ def main():
     log("prefill", json.dumps(pre))
     if args.only == "prefill":
         return
+    h2d, d2h = mh.link_rate()
+    log("link", json.dumps({"h2d_gbs": h2d, "d2h_gbs": d2h}))
     hio = prefill_host_io(mh, st)
     log("prefill_host_io", json.dumps(hio))
     small = layer_bench(mh, args.steps, args.warmup, **small_shape)
@@ -636,11 +643,16 @@ def main():
         "cpu_baseline": cpu,
         "cpu_port_all_threads": cpu_all,
     }
+    line["host_link_gbs"] = {"h2d": h2d, "d2h": d2h,
+                             "how": "one 256 MiB pinned copy each way (moe_hip_link_rate)"}
     line["prefill_host_io"] = {
         "workload": "the headline layer with x from and out / probs / ids to pageable host "
-                    "memory (PCIe included, synchronous call)",
+                    "memory through the pinned staging (moe_hip_forward_host, synchronous)",
         "tokens_per_s": hio["tokens_per_s"], "ms_per_step": hio["ms"],
-        "pcie_bytes_per_call": hio["pcie_bytes"]}
+        "pcie_bytes_per_call": hio["pcie_bytes"],
+        # device time plus x up and out down at the link rate (probs and ids
+        # travel under the expert products)
+        "bound_ms": ms + hio["up_bytes"] / (h2d * 1e6) + hio["down_bytes"] / (d2h * 1e6)}
     line["prefill_batch8x512"] = {
         "workload": "moe prefill layer T=4096 (8 x 512) d=256 d_ff=1024 E=8 top-2",
         "tokens_per_s": small["tokens_per_s"], "ms_per_step": small["ms"],
@@ -678,8 +690,10 @@ def main():
         }
         line["decode_host_dropin"] = {
             "workload": "the same 8 layers through moe_decode_batch, host x_norm and x "
-                        "(PCIe included, synchronous calls)",
-            "tokens_per_s": dech["tokens_per_s"], "ms_per_step": dech["ms_per_step"]}
+                        "(pinned staging, synchronous calls)",
+            "tokens_per_s": dech["tokens_per_s"], "ms_per_step": dech["ms_per_step"],
+            "bound_ms": dec["ms_per_step"] + dech["layers"] * dech["pcie_bytes_per_layer"]
+                        * (2 / (h2d * 1e6) + 1 / (d2h * 1e6)) / 3}
     if stp:
         line["decode_step"] = {
             "workload": "64 seqs x 1 token at context 1024, 8 blocks of GQA 8/2 attention "

@@ -205,6 +205,16 @@ int moe_hip_forward_dev(MoeHipLayer *layer, const float *x, int T, float *out,
 int moe_hip_forward_dev_noalloc(MoeHipLayer *layer, const float *x, int T, float *out,
                                 float *probs, int *ids, int accumulate, void *stream);
 
+/* The layer forward on T host rows: x [T x d_model] and out [T x d_model]
+ * in host memory (pageable), probs [T x E] and ids [T x top_k] too when not
+ * null, weights resident in the layer.  The rows go up and the results come
+ * back through pinned staging buffers, the copies overlapping each other and,
+ * for probs and ids, the expert products; synchronous at return.  This is
+ * moe_forward's data movement for callers that keep their weights resident
+ * (no counterpart in the reference). */
+int moe_hip_forward_host(MoeHipLayer *layer, const float *x, int T, float *out, float *probs,
+                         int *ids);
+
 /* rms_norm (src/matrix.c:666-711) on device rows: y [rows x cols] =
  * (x * inv_rms) * w with the reference's summation order and fused
  * multiply-adds, and a correctly rounded 1/sqrt (see moe_block_ffn). */
@@ -348,6 +358,19 @@ int moe_hip_last_forward_path(void);
  * src/matrix.c:82-116) or glibc-expf restatement (which = 1) of x[i], the two
  * scalar exponentials the routing softmax uses. */
 int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream);
+
+/* Calibration hook for hardware memory counters (no counterpart in the
+ * reference): reads `bytes` of device memory at src (a nonzero multiple of
+ * 32 MiB) through one load path of the kernels, mode 0 = global-to-LDS DMA
+ * (the grouped GEMMs' operand loads), 1 = vector loads, 2 = non-temporal
+ * vector loads (the decode weight stream), and writes 1024 per-workgroup
+ * sums to out. */
+int moe_hip_read_probe(const void *src, size_t bytes, int mode, float *out, void *stream);
+
+/* Host link rate (no counterpart in the reference): one host-to-device and
+ * one device-to-host copy of `bytes` between pinned host memory and the
+ * device, in GB/s (the rate the host drop-ins' staged copies run at). */
+int moe_hip_link_rate(size_t bytes, float *h2d_gbs, float *d2h_gbs);
 
 /* Kernel timing of the last moe_hip_forward_dev call on the library's
  * events: milliseconds for [route, dispatch, gate_up, down, combine]. */

@@ -993,6 +993,57 @@ hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stre
     return hipGetLastError();
 }
 
+// A read of known size through one load path (counter calibration): MODE 0
+// the grouped GEMMs' LDS DMA (global_load_lds_dwordx4), 1 buffer loads into
+// registers with the default cache policy, 2 the same loads non-temporal
+// (the decode weight stream).  Workgroup b (4 waves) reads bytes [b span,
+// (b + 1) span) in 4 KB steps, eight 1 KB wave instructions in flight; the
+// sum of what it read (MODE 0: of its LDS) goes to out[b].
+constexpr int kProbeGroups = 1024;
+template <int MODE>
+__global__ __launch_bounds__(256) void read_probe_kernel(const float *src, size_t span,
+                                                         float *out) {
+    __shared__ __align__(16) float lds[4][8][256];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const char *base = reinterpret_cast<const char *>(src) + (size_t)blockIdx.x * span;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (size_t off = 0; off < span; off += 4096 * 8) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const char *g = base + off + 4096 * i + 1024 * wave;
+            if (MODE == 0) {
+                gemm_dma16(reinterpret_cast<const float *>(g) + 4 * lane,
+                           (unsigned)(size_t)(const __attribute__((address_space(3))) float *)
+                               &lds[wave][i][0]);
+            } else {
+                const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<char *>(g), (short)0, 1024, 0x00020000);
+                acc += __builtin_amdgcn_raw_buffer_load_b128(r, 16 * lane, 0, MODE == 2 ? 2 : 0);
+            }
+        }
+        if (MODE == 0) GEMM_WAIT_VMCNT(0);
+    }
+    if (MODE == 0) {
+        __syncthreads();
+        acc[0] = lds[wave][lane & 7][threadIdx.x & 255];
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = acc[0] + acc[1] + acc[2] + acc[3];
+}
+
+hipError_t launch_read_probe(const float *src, size_t bytes, int mode, float *out,
+                             hipStream_t s) {
+    const size_t step = (size_t)kProbeGroups * 4096 * 8;
+    if (bytes == 0 || bytes % step != 0 || mode < 0 || mode > 2) return hipErrorInvalidValue;
+    const size_t span = bytes / kProbeGroups;
+    if (mode == 0)
+        hipLaunchKernelGGL(read_probe_kernel<0>, dim3(kProbeGroups), dim3(256), 0, s, src, span, out);
+    else if (mode == 1)
+        hipLaunchKernelGGL(read_probe_kernel<1>, dim3(kProbeGroups), dim3(256), 0, s, src, span, out);
+    else
+        hipLaunchKernelGGL(read_probe_kernel<2>, dim3(kProbeGroups), dim3(256), 0, s, src, span, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_zero_ints(int *p, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)std::min(1024, (n + 255) / 256)), dim3(256),

@@ -10,6 +10,10 @@
 #include <cstring>
 #include <map>
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
+#include <mutex>
+#include <thread>
 #include <vector>
 
 #include "moe_internal.h"
@@ -149,6 +153,107 @@ struct Workspace {
 };
 Workspace g_ws;
 
+// Pinned host staging of the host drop-ins (x in; out, probs and ids back).
+// The caller's pageable buffers are copied by the CPU into pinned memory and
+// moved by the DMA engine from there, so no copy takes the runtime's
+// synchronous path for pageable memory; probs and ids go back on a copy
+// stream as soon as the routing has run, under the expert products.
+constexpr size_t kStageChunk = (size_t)16 << 20;   // half of the pinned area
+struct HostStage {
+    char *area = nullptr;         // 2 x kStageChunk bytes, pinned
+    hipEvent_t ev[2] = {};        // the last DMA that used each half (chunked transfers)
+    hipStream_t copy = nullptr;   // (default priority)
+    hipEvent_t routed = nullptr;  // recorded after a drop-in's routing
+    bool ready = false;
+    void release() {
+        if (area) (void)hipHostFree(area);
+        area = nullptr;
+        for (auto &e : ev) {
+            if (e) (void)hipEventDestroy(e);
+            e = nullptr;
+        }
+        if (copy) (void)hipStreamDestroy(copy);
+        if (routed) (void)hipEventDestroy(routed);
+        copy = nullptr;
+        routed = nullptr;
+        ready = false;
+    }
+};
+HostStage g_hs;
+// When set, run_forward records it on its stream right after the routing.
+hipEvent_t g_route_mark = nullptr;
+
+// Host copies between pageable and pinned memory split over a few threads
+// (one thread copies ~10-20 GB/s, below the link rate).  The workers live
+// for the process; a copy is cut into kCopyThreads equal parts, the calling
+// thread taking part 0.
+class CopyPool {
+  public:
+    static constexpr int kCopyThreads = 8;
+    void copy(void *dst, const void *src, size_t n) {
+        if (n < ((size_t)1 << 20)) {
+            memcpy(dst, src, n);
+            return;
+        }
+        start();
+        {
+            std::lock_guard<std::mutex> lk(m_);
+            dst_ = static_cast<char *>(dst);
+            src_ = static_cast<const char *>(src);
+            n_ = n;
+            left_ = kCopyThreads - 1;
+            ++gen_;
+        }
+        cv_.notify_all();
+        part(0);
+        std::unique_lock<std::mutex> lk(m_);
+        done_.wait(lk, [&] { return left_ == 0; });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> lk(m_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto &t : workers_) t.join();
+    }
+
+  private:
+    void start() {
+        if (!workers_.empty()) return;
+        for (int i = 1; i < kCopyThreads; ++i)
+            workers_.emplace_back([this, i] {
+                unsigned long seen = 0;
+                for (;;) {
+                    {
+                        std::unique_lock<std::mutex> lk(m_);
+                        cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
+                        if (stop_) return;
+                        seen = gen_;
+                    }
+                    part(i);
+                    std::lock_guard<std::mutex> lk(m_);
+                    if (--left_ == 0) done_.notify_one();
+                }
+            });
+    }
+    void part(int i) {
+        const size_t per = (n_ + kCopyThreads - 1) / kCopyThreads;
+        const size_t lo = std::min(n_, per * i), hi = std::min(n_, lo + per);
+        if (hi > lo) memcpy(dst_ + lo, src_ + lo, hi - lo);
+    }
+    std::vector<std::thread> workers_;
+    std::mutex m_;
+    std::condition_variable cv_, done_;
+    char *dst_ = nullptr;
+    const char *src_ = nullptr;
+    size_t n_ = 0;
+    int left_ = 0;
+    unsigned long gen_ = 0;
+    bool stop_ = false;
+};
+CopyPool g_copy_pool;
+
 // Device ints that are zero between launches (each launch's last workgroup
 // resets what it counted), so they are cleared only when allocated: [0] the
 // fused route+dispatch launch's completion counter.
@@ -181,6 +286,126 @@ int scratch_of(hipStream_t s, char **out) {
     *out = g_scratch[dev];
     return MOE_HIP_OK;
 }
+
+int stage_init() {
+    if (g_hs.ready) return MOE_HIP_OK;
+    if (hipHostMalloc(reinterpret_cast<void **>(&g_hs.area), 2 * kStageChunk,
+                      hipHostMallocDefault) != hipSuccess) {
+        g_hs.area = nullptr;
+        return set_err(MOE_HIP_ERR_NOMEM, "pinned staging of %zu bytes", 2 * kStageChunk);
+    }
+    for (auto &e : g_hs.ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    HIP_TRY(hipStreamCreateWithFlags(&g_hs.copy, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreateWithFlags(&g_hs.routed, hipEventDisableTiming));
+    g_hs.ready = true;
+    return MOE_HIP_OK;
+}
+
+// The staging of one drop-in call (calls are synchronous, so the whole
+// pinned area is free when one starts).  An array that fits the area's free
+// part takes a region of its own: one CPU copy and one DMA, and for a
+// download a copy out in finish(), after one wait per stream.  Larger arrays
+// go through the two halves of the area in turn, the CPU copying one while
+// the DMA engine moves the other.
+class Staging {
+  public:
+    // host (pageable) -> dev, queued on the library stream.
+    int up(void *dev, const void *host, size_t n) {
+        TRY(stage_init());
+        if (n == 0) return MOE_HIP_OK;
+        if (fits(n)) {
+            if (chunked_up_) {   // (a chunked upload's DMAs may still read the area)
+                HIP_TRY(hipStreamSynchronize(g_stream));
+                chunked_up_ = false;
+            }
+            char *pin = g_hs.area + off_;
+            off_ += align(n);
+            g_copy_pool.copy(pin, host, n);
+            HIP_TRY(hipMemcpyAsync(dev, pin, n, hipMemcpyHostToDevice, g_stream));
+            return MOE_HIP_OK;
+        }
+        TRY(drain());
+        chunked_up_ = true;
+        for (size_t o = 0, i = 0; o < n; o += kStageChunk, ++i) {
+            const size_t m = std::min(kStageChunk, n - o);
+            char *pin = g_hs.area + (i & 1) * kStageChunk;
+            HIP_TRY(hipEventSynchronize(g_hs.ev[i & 1]));   // (the half's last DMA is done)
+            g_copy_pool.copy(pin, static_cast<const char *>(host) + o, m);
+            HIP_TRY(hipMemcpyAsync(static_cast<char *>(dev) + o, pin, m, hipMemcpyHostToDevice,
+                                   g_stream));
+            HIP_TRY(hipEventRecord(g_hs.ev[i & 1], g_stream));
+        }
+        return MOE_HIP_OK;
+    }
+    // dev -> host (pageable) after the work queued on s; host holds the bytes
+    // once finish() has returned.  A download on another stream than the
+    // library's must be ordered after the uploads (the drop-ins' copy stream
+    // waits for the routing, which follows them on the library stream).
+    int down(void *host, const void *dev, size_t n, hipStream_t s) {
+        TRY(stage_init());
+        if (n == 0) return MOE_HIP_OK;
+        if (fits(n)) {
+            char *pin = g_hs.area + off_;
+            off_ += align(n);
+            HIP_TRY(hipMemcpyAsync(pin, dev, n, hipMemcpyDeviceToHost, s));
+            pend_.push_back({host, pin, n, s});
+            return MOE_HIP_OK;
+        }
+        TRY(drain());
+        const size_t nch = (n + kStageChunk - 1) / kStageChunk;
+        auto issue = [&](size_t i) -> int {
+            const size_t o = i * kStageChunk, m = std::min(kStageChunk, n - o);
+            HIP_TRY(hipEventSynchronize(g_hs.ev[i & 1]));
+            HIP_TRY(hipMemcpyAsync(g_hs.area + (i & 1) * kStageChunk,
+                                   static_cast<const char *>(dev) + o, m, hipMemcpyDeviceToHost, s));
+            HIP_TRY(hipEventRecord(g_hs.ev[i & 1], s));
+            return MOE_HIP_OK;
+        };
+        TRY(issue(0));
+        for (size_t i = 0; i < nch; ++i) {
+            if (i + 1 < nch) TRY(issue(i + 1));
+            const size_t o = i * kStageChunk, m = std::min(kStageChunk, n - o);
+            HIP_TRY(hipEventSynchronize(g_hs.ev[i & 1]));
+            g_copy_pool.copy(static_cast<char *>(host) + o, g_hs.area + (i & 1) * kStageChunk, m);
+        }
+        off_ = 0;   // (every DMA into the area is done)
+        return MOE_HIP_OK;
+    }
+    int finish() {
+        TRY(flush());
+        HIP_TRY(hipStreamSynchronize(g_stream));
+        return MOE_HIP_OK;
+    }
+
+  private:
+    struct Pending {
+        void *host;
+        const char *pin;
+        size_t n;
+        hipStream_t s;
+    };
+    static size_t align(size_t n) { return (n + 255) & ~(size_t)255; }
+    bool fits(size_t n) const { return off_ + n <= 2 * kStageChunk; }
+    // The queued small downloads waited for and copied out.
+    int flush() {
+        for (const Pending &p : pend_) HIP_TRY(hipStreamSynchronize(p.s));
+        for (const Pending &p : pend_) g_copy_pool.copy(p.host, p.pin, p.n);
+        pend_.clear();
+        return MOE_HIP_OK;
+    }
+    // Before a chunked transfer: every region handed out is released (the
+    // small downloads copied out, the queued DMAs done); after a chunked
+    // upload the whole area is handed out afresh.
+    int drain() {
+        TRY(flush());
+        HIP_TRY(hipStreamSynchronize(g_stream));
+        off_ = 0;
+        return MOE_HIP_OK;
+    }
+    size_t off_ = 0;
+    bool chunked_up_ = false;
+    std::vector<Pending> pend_;
+};
 
 // Norm: with x_raw set, the rows to route (x, written here) are first
 // rms_norm(x_raw; rms_w, eps), by the router where it can.
@@ -346,6 +571,33 @@ int dropin_forward(MoeHipLayer *L, int d, const float *x, int T, float *out, flo
     return MOE_HIP_OK;
 }
 
+// A forward of T host rows x [T x d] (the caller's width d, the layer's own
+// or narrower) through a resident layer: x goes up through the pinned
+// staging, probs and ids (either may be null) come back under the expert
+// products, out [T x d] at the end; synchronous at return.
+int host_forward(MoeHipLayer *L, int d, const float *x, int T, float *out, float *probs,
+                 int *ids) {
+    const int E = L->E, k = L->k;
+    const size_t xd = (size_t)T * d;
+    TRY(g_ws.x.reserve(sizeof(float) * xd));
+    TRY(g_ws.out.reserve(sizeof(float) * xd));
+    TRY(g_ws.probs.reserve(sizeof(float) * (size_t)T * E));
+    TRY(g_ws.ids.reserve(sizeof(int) * (size_t)T * k));
+    float *dx = g_ws.x.as<float>(), *dout = g_ws.out.as<float>(), *dprobs = g_ws.probs.as<float>();
+    int *dids = g_ws.ids.as<int>();
+    Staging st;
+    TRY(st.up(dx, x, sizeof(float) * xd));
+    g_route_mark = g_hs.routed;
+    const int rc = dropin_forward(L, d, dx, T, dout, dprobs, dids, 0);
+    g_route_mark = nullptr;
+    TRY(rc);
+    HIP_TRY(hipStreamWaitEvent(g_hs.copy, g_hs.routed, 0));
+    if (probs) TRY(st.down(probs, dprobs, sizeof(float) * (size_t)T * E, g_hs.copy));
+    if (ids) TRY(st.down(ids, dids, sizeof(int) * (size_t)T * k, g_hs.copy));
+    TRY(st.down(out, dout, sizeof(float) * xd, g_stream));
+    return st.finish();
+}
+
 void die_on(int rc, const char *what) {
     if (rc == MOE_HIP_OK) return;
     fprintf(stderr, "[libmoe_hip] %s: %s\n", what, g_msg);
@@ -385,6 +637,7 @@ void moe_hip_shutdown(void) {
     for (auto &kv : g_resident) moe_hip_layer_destroy(kv.second.layer);
     g_resident.clear();
     g_ws.release_all();
+    g_hs.release();
     g_ext_capture = false;
     for (auto &ev : g_ev) (void)hipEventDestroy(ev);
     for (auto &ev : g_tev) (void)hipEventDestroy(ev);
@@ -804,6 +1057,45 @@ int moe_hip_fill_normal_dev(float *dst, size_t n, uint64_t seed, uint64_t stream
     return MOE_HIP_OK;
 }
 
+int moe_hip_link_rate(size_t bytes, float *h2d_gbs, float *d2h_gbs) {
+    if (!h2d_gbs || !d2h_gbs || bytes == 0) return set_err(MOE_HIP_ERR_ARG, "bad link-rate arguments");
+    TRY(ensure_init());
+    void *dev = nullptr, *host = nullptr;
+    if (hipMalloc(&dev, bytes) != hipSuccess) return set_err(MOE_HIP_ERR_NOMEM, "link rate: device");
+    if (hipHostMalloc(&host, bytes, hipHostMallocDefault) != hipSuccess) {
+        (void)hipFree(dev);
+        return set_err(MOE_HIP_ERR_NOMEM, "link rate: pinned host");
+    }
+    memset(host, 0, bytes);
+    float ms[2] = {0.0f, 0.0f};
+    hipError_t e = hipSuccess;
+    for (int rep = 0; rep < 3 && e == hipSuccess; ++rep)   // (the last pass counts)
+        for (int dir = 0; dir < 2 && e == hipSuccess; ++dir) {
+            e = hipEventRecord(g_tev[0], g_stream);
+            if (e == hipSuccess)
+                e = dir ? hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, g_stream)
+                        : hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, g_stream);
+            if (e == hipSuccess) e = hipEventRecord(g_tev[1], g_stream);
+            if (e == hipSuccess) e = hipEventSynchronize(g_tev[1]);
+            if (e == hipSuccess) e = hipEventElapsedTime(&ms[dir], g_tev[0], g_tev[1]);
+        }
+    (void)hipHostFree(host);
+    (void)hipFree(dev);
+    if (e != hipSuccess) return set_err(MOE_HIP_ERR_HIP, "link rate: %s", hipGetErrorString(e));
+    *h2d_gbs = (float)(bytes / (ms[0] * 1e-3) / 1e9);
+    *d2h_gbs = (float)(bytes / (ms[1] * 1e-3) / 1e9);
+    return MOE_HIP_OK;
+}
+
+int moe_hip_read_probe(const void *src, size_t bytes, int mode, float *out, void *stream) {
+    TRY(ensure_init());
+    if (!src || !out || mode < 0 || mode > 2 || bytes == 0 || bytes % ((size_t)32 << 20) != 0)
+        return set_err(MOE_HIP_ERR_ARG, "read probe: mode 0-2, bytes a nonzero multiple of 32 MiB");
+    HIP_TRY(moe::launch_read_probe(static_cast<const float *>(src), bytes, mode, out,
+                                   stream_of(stream)));
+    return MOE_HIP_OK;
+}
+
 int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream) {
     TRY(ensure_init());
     if (which != 0 && which != 1) return set_err(MOE_HIP_ERR_ARG, "which must be 0 or 1");
@@ -1021,6 +1313,7 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
         if (g_timing)
             for (int i = 0; i < 3; ++i) HIP_TRY(hipEventRecord(g_ev[i], s));
         HIP_TRY(moe::launch_decode_routed(gu, ra, s));
+        if (g_route_mark) HIP_TRY(hipEventRecord(g_route_mark, s));
         if (g_timing) {
             HIP_TRY(hipEventRecord(g_ev[3], s));
             HIP_TRY(hipEventRecord(g_ev[4], s));
@@ -1028,6 +1321,7 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
     } else {
         TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
                        b.tile_expert, b.counters, s, !p.use_decode, nm));
+        if (g_route_mark) HIP_TRY(hipEventRecord(g_route_mark, s));
     }
     g_last_path = routed ? 4 : !p.use_decode ? 1 : p.fused ? 2 : 3;
     if (routed) {
@@ -1197,22 +1491,15 @@ int moe_hip_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg
     TRY(ensure_init());
     MoeHipLayer *L = nullptr;
     TRY(resident_layer(w, d, F, &L));
-    const size_t xd = (size_t)T * d;
-    TRY(g_ws.x.reserve(sizeof(float) * xd));
-    TRY(g_ws.out.reserve(sizeof(float) * xd));
-    TRY(g_ws.probs.reserve(sizeof(float) * (size_t)T * E));
-    TRY(g_ws.ids.reserve(sizeof(int) * (size_t)T * k));
-    float *dx = g_ws.x.as<float>(), *dout = g_ws.out.as<float>(), *dprobs = g_ws.probs.as<float>();
-    int *dids = g_ws.ids.as<int>();
-    HIP_TRY(hipMemcpyAsync(dx, x->data, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
-    TRY(dropin_forward(L, d, dx, T, dout, dprobs, dids, 0));
-    HIP_TRY(hipMemcpyAsync(out->data, dout, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipMemcpyAsync(cache->router_probs, dprobs, sizeof(float) * (size_t)T * E,
-                           hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
-                           hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipStreamSynchronize(g_stream));
-    return MOE_HIP_OK;
+    return host_forward(L, d, x->data, T, out->data, cache->router_probs, cache->expert_ids);
+}
+
+int moe_hip_forward_host(MoeHipLayer *L, const float *x, int T, float *out, float *probs,
+                         int *ids) {
+    if (!L || T < 0 || (T > 0 && (!x || !out))) return set_err(MOE_HIP_ERR_ARG, "bad forward arguments");
+    if (T == 0) return MOE_HIP_OK;
+    TRY(ensure_init());
+    return host_forward(L, L->d, x, T, out, probs, ids);
 }
 
 void moe_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg, ForwardCache *cache,
@@ -1234,11 +1521,12 @@ int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x
     TRY(g_ws.x.reserve(sizeof(float) * xd));
     TRY(g_ws.out.reserve(sizeof(float) * xd));
     float *dxn = g_ws.x.as<float>(), *dx = g_ws.out.as<float>();
-    HIP_TRY(hipMemcpyAsync(dxn, x_norm, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
-    HIP_TRY(hipMemcpyAsync(dx, x, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
+    Staging st;
+    TRY(st.up(dxn, x_norm, sizeof(float) * xd));
+    TRY(st.up(dx, x, sizeof(float) * xd));
     TRY(dropin_forward(L, d, dxn, n_rows, dx, nullptr, nullptr, 1));
-    HIP_TRY(hipMemcpyAsync(x, dx, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipStreamSynchronize(g_stream));
+    TRY(st.down(x, dx, sizeof(float) * xd, g_stream));
+    TRY(st.finish());
     return MOE_HIP_OK;
 }
 
@@ -1372,17 +1660,22 @@ int moe_hip_block_ffn(Matrix *x, const float *rms_ffn, const MoEWeights *w,
     float *dx = g_ws.x.as<float>(), *dxn = g_ws.xn.as<float>(), *dout = g_ws.out.as<float>();
     float *dw = g_ws.rmsw.as<float>(), *dprobs = g_ws.probs.as<float>();
     int *dids = g_ws.ids.as<int>();
-    HIP_TRY(hipMemcpyAsync(dx, x->data, sizeof(float) * xd, hipMemcpyHostToDevice, g_stream));
-    HIP_TRY(hipMemcpyAsync(dw, rms_ffn, sizeof(float) * d, hipMemcpyHostToDevice, g_stream));
+    Staging st;
+    TRY(st.up(dw, rms_ffn, sizeof(float) * d));
+    TRY(st.up(dx, x->data, sizeof(float) * xd));
     HIP_TRY(moe::launch_rms_norm(dx, dw, cfg->rms_norm_eps, T, d, dxn, g_stream));
-    TRY(dropin_forward(L, d, dxn, T, dout, dprobs, dids, 0));
-    HIP_TRY(hipMemcpyAsync(xn.data, dxn, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipMemcpyAsync(fo.data, dout, sizeof(float) * xd, hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipMemcpyAsync(cache->router_probs, dprobs, sizeof(float) * (size_t)T * E,
-                           hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipMemcpyAsync(cache->expert_ids, dids, sizeof(int) * (size_t)T * k,
-                           hipMemcpyDeviceToHost, g_stream));
-    HIP_TRY(hipStreamSynchronize(g_stream));
+    g_route_mark = g_hs.routed;
+    const int rc = dropin_forward(L, d, dxn, T, dout, dprobs, dids, 0);
+    g_route_mark = nullptr;
+    TRY(rc);
+    // x_norm, probs and ids come back under the expert products, ffn_out at
+    // the end
+    HIP_TRY(hipStreamWaitEvent(g_hs.copy, g_hs.routed, 0));
+    TRY(st.down(xn.data, dxn, sizeof(float) * xd, g_hs.copy));
+    TRY(st.down(cache->router_probs, dprobs, sizeof(float) * (size_t)T * E, g_hs.copy));
+    TRY(st.down(cache->expert_ids, dids, sizeof(int) * (size_t)T * k, g_hs.copy));
+    TRY(st.down(fo.data, dout, sizeof(float) * xd, g_stream));
+    TRY(st.finish());
     // Residual 2 (src/transformer.c:767, mat_add_inplace).
     for (size_t i = 0; i < xd; ++i) x->data[i] = x->data[i] + fo.data[i];
     return MOE_HIP_OK;

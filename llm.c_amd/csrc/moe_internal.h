@@ -255,6 +255,11 @@ hipError_t launch_transpose(const float *src, float *dst, int rows, int cols, hi
 // Elementwise exp_poly (which = 0) or glibc-expf (which = 1) on the device,
 // exactly as the routing kernels evaluate them.
 hipError_t launch_eval_exp(int which, const float *x, float *y, size_t n, hipStream_t s);
+// Reads bytes of src through one load path (0 LDS DMA, 1 buffer loads,
+// 2 non-temporal buffer loads) and writes 1024 per-workgroup sums to out;
+// bytes must be a multiple of 32 MiB.
+hipError_t launch_read_probe(const float *src, size_t bytes, int mode, float *out,
+                             hipStream_t s);
 // p[0 .. n) = 0 by a kernel (safe to record in a graph, unlike a memset node).
 hipError_t launch_zero_ints(int *p, int n, hipStream_t s);
 hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed,

@@ -57,6 +57,7 @@ SIGNATURES = {
     "moe_hip_layer_get_router": (C.c_int, [_P, _F]),
     "moe_hip_forward_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
     "moe_hip_forward_dev_noalloc": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, C.c_int, _P]),
+    "moe_hip_forward_host": (C.c_int, [_P, _F, C.c_int, _F, _F, _I]),
     "moe_hip_route_dev": (C.c_int, [_P, _P, C.c_int, _P, _P, _P, _P, _P, _P, _P]),
     "moe_hip_rms_norm_dev": (C.c_int, [_P, _P, C.c_float, C.c_int, C.c_int, _P, _P]),
     "moe_hip_attn_create": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
@@ -74,6 +75,8 @@ SIGNATURES = {
     "moe_hip_fill_normal_dev": (C.c_int, [_P, C.c_size_t, C.c_uint64, C.c_uint64, C.c_float,
                                           C.c_float, _P]),
     "moe_hip_eval_exp": (C.c_int, [C.c_int, _P, _P, C.c_size_t, _P]),
+    "moe_hip_read_probe": (C.c_int, [_P, C.c_size_t, C.c_int, _P, _P]),
+    "moe_hip_link_rate": (C.c_int, [C.c_size_t, _F, _F]),
     "moe_hip_last_timings": (C.c_int, [_F]),
     "moe_hip_set_timing": (C.c_int, [C.c_int]),
     "moe_hip_set_expert_path": (C.c_int, [C.c_int]),
@@ -231,6 +234,14 @@ class Layer:
         allocation; moe_hip_forward_dev_noalloc)."""
         check(lib().moe_hip_forward_dev_noalloc(self.h, x_ptr, T, out_ptr, probs_ptr, ids_ptr,
                                                 accumulate, stream))
+
+    def forward_host(self, x, out, probs=None, ids=None):
+        """moe_hip_forward_host: x, out [T x d] (and probs [T x E], ids
+        [T x k] when given) numpy arrays in host memory."""
+        assert x.dtype == np.float32 and out.dtype == np.float32 and x.flags["C_CONTIGUOUS"]
+        check(lib().moe_hip_forward_host(self.h, fptr(x), x.shape[0], fptr(out),
+                                         fptr(probs) if probs is not None else None,
+                                         iptr(ids) if ids is not None else None))
 
     def ffn_sublayer_dev(self, x_ptr, rms_w_ptr, eps, T, x_norm_ptr=None, probs_ptr=None,
                          ids_ptr=None, stream=None):
@@ -429,6 +440,13 @@ def last_forward_path():
     fused decode kernel, 3 router + two-launch decode, 4 fused decode kernel
     with the routing inside."""
     return int(lib().moe_hip_last_forward_path())
+
+
+def link_rate(nbytes=256 << 20):
+    """(host-to-device, device-to-host) GB/s of pinned copies of nbytes."""
+    a, b = C.c_float(), C.c_float()
+    check(lib().moe_hip_link_rate(nbytes, C.byref(a), C.byref(b)))
+    return a.value, b.value
 
 
 def set_timing(on):

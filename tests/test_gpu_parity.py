@@ -264,6 +264,42 @@ def test_forward_dev_configs(name):
     assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
     assert np.array_equal(dids.to_host(), i_ref)
     assert_close(dout.to_host(), o_ref, name)
+    # the same rows from host memory through the pinned staging: the same bits
+    oh = np.empty((T, d), np.float32)
+    ph = np.empty((T, E), np.float32)
+    ih = np.empty((T, k), np.int32)
+    layer.forward_host(x, oh, ph, ih)
+    assert np.array_equal(bits(oh), bits(dout.to_host()))
+    assert np.array_equal(bits(ph), bits(dprobs.to_host()))
+    assert np.array_equal(ih, dids.to_host())
+    layer.close()
+
+
+def test_forward_host_chunks():
+    """moe_hip_forward_host on 41 MB of rows (three 16 MB staging chunks up
+    and down, the last one partial): the same bits as forward_dev on the
+    same rows, with and without the probs / ids outputs."""
+    T, d, F, E, k = 40000, 256, 256, 8, 2
+    say(f"forward_host chunks: T={T} d={d}")
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(7, 0.1, 0.02)
+    x = orc.synth((T, d), 7, 0, 1.0)
+    dx = mh.DeviceArray.from_host(x)
+    dout = mh.DeviceArray((T, d))
+    dprobs = mh.DeviceArray((T, E))
+    dids = mh.DeviceArray((T, k), np.int32)
+    layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+    mh.synchronize()
+    oh = np.full((T, d), np.nan, np.float32)
+    ph = np.empty((T, E), np.float32)
+    ih = np.empty((T, k), np.int32)
+    layer.forward_host(x, oh, ph, ih)
+    assert np.array_equal(bits(oh), bits(dout.to_host()))
+    assert np.array_equal(bits(ph), bits(dprobs.to_host()))
+    assert np.array_equal(ih, dids.to_host())
+    oh2 = np.full((T, d), np.nan, np.float32)
+    layer.forward_host(x, oh2)
+    assert np.array_equal(bits(oh2), bits(oh))
     layer.close()
 
 
