@@ -106,8 +106,9 @@ enum {
  * call moe_hip_invalidate() after changing weight values in place.  Any
  * d_model and ffn_hidden: widths the kernels do not tile are padded with
  * zeros inside the resident layer (same routing bits, same outputs within
- * the layer tolerance); n_experts <= 256 and top_k <= 16.  The same holds for
- * moe_decode_step, moe_decode_batch and moe_block_ffn.
+ * the layer tolerance); n_experts <= 4096 and top_k <= 256 (layers past 256
+ * experts or top-16 route through general kernels, with the same bits).  The
+ * same holds for moe_decode_step, moe_decode_batch and moe_block_ffn.
  * On error it prints the reason and aborts, as the reference does on OOM
  * (src/matrix.c:148-158). */
 void moe_forward(const Matrix *x, const MoEWeights *w, const ModelConfig *cfg,
@@ -233,7 +234,8 @@ int moe_hip_rms_norm_dev(const float *x, const float *w, float eps, int rows, in
  * dw_gate, dw_up [n_experts][d x ffn_hidden], dw_down [n_experts][ffn_hidden
  * x d]; accumulate != 0 adds to them.  aux_loss (device float, may be NULL)
  * receives aux.  A router bias, if set, enters the forward but gets no
- * gradient here.  Deterministic; fp32 with fixed summation orders. */
+ * gradient here.  Deterministic; fp32 with fixed summation orders.  Layers
+ * of n_experts <= 256 and top_k <= 16 (MOE_HIP_ERR_UNSUPPORTED past them). */
 int moe_hip_backward_dev(MoeHipLayer *layer, const float *x, int T, const float *dout,
                          float aux_coef, float *dx, float *dw_router, float *dw_gate,
                          float *dw_up, float *dw_down, float *aux_loss, int accumulate,

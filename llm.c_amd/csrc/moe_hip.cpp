@@ -143,11 +143,11 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, pieces,
-        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork, xpad, gu_part;
+        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork, xpad, gu_part, wprobs, wide;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
                          &tile_expert, &perm, &h, &ys, &pieces, &stage, &counters, &xn, &rmsw,
-                         &aq, &ao, &apart, &acnt, &bw, &bwork, &xpad, &gu_part};
+                         &aq, &ao, &apart, &acnt, &bw, &bwork, &xpad, &gu_part, &wprobs, &wide};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -443,9 +443,10 @@ int check_shapes(int d, int F, int E, int k, bool widths = true) {
         return set_err(MOE_HIP_ERR_ARG, "bad MoE shape d=%d F=%d E=%d k=%d", d, F, E, k);
     if (k > E)
         return set_err(MOE_HIP_ERR_ARG, "top_k %d exceeds n_experts %d", k, E);
-    if (E > moe::kMaxExperts || k > moe::kMaxTopK)
+    // Past the fast routing kernels' tables the general routing kernels take over.
+    if ((E > moe::kMaxExperts || k > moe::kMaxTopK) && !moe::route_wide_ok(E, k))
         return set_err(MOE_HIP_ERR_UNSUPPORTED, "n_experts %d / top_k %d above the supported %d / %d",
-                       E, k, moe::kMaxExperts, moe::kMaxTopK);
+                       E, k, moe::kWideMaxExperts, moe::kWideMaxTopK);
     if (widths && (d % 64 != 0 || F % 32 != 0))
         return set_err(MOE_HIP_ERR_UNSUPPORTED,
                        "d_model %% 64 and ffn_hidden %% 32 must be 0 (got d=%d F=%d)", d, F);
@@ -1104,12 +1105,28 @@ int moe_hip_eval_exp(int which, const float *x, float *y, size_t n, void *stream
     return MOE_HIP_OK;
 }
 
+// Layers routed by the general kernels (more experts or a larger top-k than
+// the fast routing kernels' tables) need a logits buffer when the caller
+// passes no probs, and scratch for their dispatch.
+static bool is_wide(int E, int k) { return E > moe::kMaxExperts || k > moe::kMaxTopK; }
+struct WideBufs {
+    float *probs = nullptr;   // [T x E]
+    int *ints = nullptr;      // [moe::wide_dispatch_ints(T k, E)]
+};
+
 // Routing (and, with dispatch, the stable counting sort by expert) of T
 // rows.  tile_expert: ceil(T k / kGemmBM) + E ints; counter: one device int,
 // zero between launches (the fused dispatch's last workgroup resets it).
 static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *ids, float *gw,
                       int *counts, int *offsets, int *tile_off, int *perm, int *tile_expert,
-                      int *counter, hipStream_t s, bool dispatch = true, Norm nm = Norm{}) {
+                      int *counter, hipStream_t s, bool dispatch = true, Norm nm = Norm{},
+                      const WideBufs &wb = WideBufs{}) {
+    if (is_wide(L->E, L->k)) {
+        // (the general kernels put the logits in probs first)
+        if (!probs) probs = wb.probs;
+        if (!probs || (dispatch && !wb.ints))
+            return set_err(MOE_HIP_ERR_ARG, "wide routing without its buffers");
+    }
     moe::RouteArgs ra{x, L->wr, L->bias, T, L->d, L->E, L->k, probs, ids, gw};
     ra.no_dispatch = dispatch ? 0 : 1;
     if (nm.x_raw) {
@@ -1122,6 +1139,7 @@ static int route_impl(MoeHipLayer *L, const float *x, int T, float *probs, int *
     }
     moe::DispatchArgs da{ids, T * L->k, L->E, moe::kGemmBM, counts, offsets, tile_off, perm,
                          counter, tile_expert};
+    da.wide = wb.ints;
     if (g_timing) HIP_TRY(hipEventRecord(g_ev[0], s));
     HIP_TRY(moe::launch_route_dispatch(ra, da, s));
     if (g_timing) {
@@ -1147,11 +1165,18 @@ int moe_hip_route_dev(MoeHipLayer *L, const float *x, int T, float *probs, int *
     TRY(g_ws.perm.reserve(sizeof(int) * n));
     TRY(g_ws.tile_expert.reserve(sizeof(int) * max_mtiles_of(n, L->E)));
     TRY(ensure_counters());
+    WideBufs wb;
+    if (is_wide(L->E, L->k)) {
+        TRY(g_ws.wprobs.reserve(sizeof(float) * (size_t)T * L->E));
+        TRY(g_ws.wide.reserve(sizeof(int) * moe::wide_dispatch_ints(n, L->E)));
+        wb.probs = g_ws.wprobs.as<float>();
+        wb.ints = g_ws.wide.as<int>();
+    }
     return route_impl(L, x, T, probs, ids ? ids : g_ws.ids.as<int>(), gw ? gw : g_ws.gw.as<float>(),
                       counts ? counts : g_ws.counts.as<int>(),
                       offsets ? offsets : g_ws.offsets.as<int>(), g_ws.tile_off.as<int>(),
                       perm ? perm : g_ws.perm.as<int>(), g_ws.tile_expert.as<int>(),
-                      g_ws.counters.as<int>(), s);
+                      g_ws.counters.as<int>(), s, true, Norm{}, wb);
 }
 
 namespace {
@@ -1169,6 +1194,7 @@ struct FwdPlan {
     size_t pieces_ints = 0; // stream-K piece counts [n][d / 256]
     int gu_tail = 0;        // gate/up split tail: workgroups per round (moe::gateup_tail_groups)
     size_t gu_part_floats = 0;  // its pieces
+    size_t wide_probs_floats = 0, wide_ints = 0;   // general routing kernels' buffers (WideBufs)
 };
 
 // The device buffers of one forward.
@@ -1181,6 +1207,7 @@ struct FwdBufs {
     int *pieces = nullptr;     // [n][d / 256] (stream-K down projection)
     float *gu_part = nullptr;  // gate/up split-tail pieces
     int *counters = nullptr;   // kMaxCounters ints, zero between launches
+    WideBufs wide;             // (layers routed by the general kernels)
 };
 
 int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
@@ -1190,6 +1217,10 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
         return set_err(MOE_HIP_ERR_UNSUPPORTED, "T*k*max(F,d) exceeds 32-bit indexing");
     p->n = n;
     p->max_mtiles = (int)max_mtiles_of(n, E);
+    if (is_wide(E, k)) {
+        p->wide_probs_floats = (size_t)T * E;
+        p->wide_ints = moe::wide_dispatch_ints(n, E);
+    }
     // Expert products: skinny decode GEMVs (which find their own slots from
     // the expert ids, so routing skips the dispatch) or grouped GEMMs.
     // (the decode kernels address one expert's gate/up block, 2*F*d floats,
@@ -1240,6 +1271,8 @@ int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
     TRY(g_ws.ys.reserve(sizeof(float) * p.ys_floats));
     if (p.pieces_ints) TRY(g_ws.pieces.reserve(sizeof(int) * p.pieces_ints));
     if (p.gu_part_floats) TRY(g_ws.gu_part.reserve(sizeof(float) * p.gu_part_floats));
+    if (p.wide_probs_floats) TRY(g_ws.wprobs.reserve(sizeof(float) * p.wide_probs_floats));
+    if (p.wide_ints) TRY(g_ws.wide.reserve(sizeof(int) * p.wide_ints));
     TRY(ensure_counters());
     b->ids = g_ws.ids.as<int>(); b->gw = g_ws.gw.as<float>();
     b->counts = g_ws.counts.as<int>(); b->offsets = g_ws.offsets.as<int>();
@@ -1248,6 +1281,8 @@ int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
     b->pieces = p.pieces_ints ? g_ws.pieces.as<int>() : nullptr;
     b->gu_part = p.gu_part_floats ? g_ws.gu_part.as<float>() : nullptr;
     b->counters = g_ws.counters.as<int>();
+    b->wide.probs = p.wide_probs_floats ? g_ws.wprobs.as<float>() : nullptr;
+    b->wide.ints = p.wide_ints ? g_ws.wide.as<int>() : nullptr;
     return MOE_HIP_OK;
 }
 
@@ -1275,6 +1310,8 @@ void carve_bufs(const MoeHipLayer *L, const FwdPlan &p, char *base, size_t cap, 
     c.ys = static_cast<float *>(take(sizeof(float) * p.ys_floats));
     c.pieces = p.pieces_ints ? static_cast<int *>(take(sizeof(int) * p.pieces_ints)) : nullptr;
     c.gu_part = p.gu_part_floats ? static_cast<float *>(take(sizeof(float) * p.gu_part_floats)) : nullptr;
+    c.wide.probs = p.wide_probs_floats ? static_cast<float *>(take(sizeof(float) * p.wide_probs_floats)) : nullptr;
+    c.wide.ints = p.wide_ints ? static_cast<int *>(take(sizeof(int) * p.wide_ints)) : nullptr;
     *need = off;
     if (off <= cap) *b = c;
 }
@@ -1320,7 +1357,7 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
         }
     } else {
         TRY(route_impl(L, x, T, probs, ids_d, b.gw, b.counts, b.offsets, b.tile_off, b.perm,
-                       b.tile_expert, b.counters, s, !p.use_decode, nm));
+                       b.tile_expert, b.counters, s, !p.use_decode, nm, b.wide));
         if (g_route_mark) HIP_TRY(hipEventRecord(g_route_mark, s));
     }
     g_last_path = routed ? 4 : !p.use_decode ? 1 : p.fused ? 2 : 3;
@@ -1555,6 +1592,9 @@ int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dou
     const size_t n = (size_t)T * k;
     if (n * (size_t)(F > d ? F : d) > (size_t)0x7fffffff)
         return set_err(MOE_HIP_ERR_UNSUPPORTED, "T*k*max(F,d) exceeds 32-bit indexing");
+    if (is_wide(E, k))
+        return set_err(MOE_HIP_ERR_UNSUPPORTED, "backward: n_experts %d / top_k %d above %d / %d",
+                       E, k, moe::kMaxExperts, moe::kMaxTopK);
     hipStream_t s = pick_stream(stream);
     // The forward's routing and dispatch (bit-exact with moe_forward).
     TRY(g_ws.probs.reserve(sizeof(float) * (size_t)T * E));

@@ -49,6 +49,7 @@ struct DispatchArgs {
     int *perm;           // [n]
     int *counter;        // zeroed device int for the fused path (reset after use)
     int *tile_expert;    // [n / bm + E] expert of each m-tile (optional)
+    int *wide = nullptr; // [wide_dispatch_ints(n, E)] (layers routed by route_wide.hip)
 };
 
 // Up to this many (token, slot) assignments, and router workgroups, the
@@ -129,6 +130,15 @@ constexpr size_t kFusedPartialBytes = (size_t)32 << 20;
 
 
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
+// Layers past the fast routing kernels' tables (n_experts > kMaxExperts or
+// top_k > kMaxTopK) route through general kernels (route_wide.hip), up to
+// these limits; launch_route_dispatch hands them over.  They need
+// RouteArgs.probs (the logits go there first) and, with the dispatch,
+// DispatchArgs.wide.
+constexpr int kWideMaxExperts = 4096, kWideMaxTopK = 256;
+bool route_wide_ok(int E, int k);
+size_t wide_dispatch_ints(size_t n, int E);
+hipError_t launch_route_wide(const RouteArgs &a, const DispatchArgs &da, hipStream_t s);
 hipError_t launch_gemm_gateup(const GemmArgs &a, hipStream_t s);
 // The split tail's pieces of a gate/up launch with tail_groups > 0 added in
 // order, swiglu applied, written to H (same stream, after the gate/up).

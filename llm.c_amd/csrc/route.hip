@@ -801,6 +801,7 @@ hipError_t launch_rows_router(const RouteArgs &a, const DispatchArgs &da, hipStr
 // (about one 64-entry group per wave, over up to 32 workgroups).
 hipError_t launch_route_dispatch(const RouteArgs &a, const DispatchArgs &da, hipStream_t s) {
     if (a.T <= 0) return hipSuccess;
+    if (a.E > kMaxExperts || a.k > kMaxTopK) return launch_route_wide(a, da, s);
     if (a.rms_w && !(a.wrT && a.d % 16 == 0)) {
         // Only the row-block router normalises its rows itself.
         hipError_t e = launch_rms_norm(a.x_raw, a.rms_w, a.rms_eps, a.T, a.d, a.xn_out, s);

@@ -14,7 +14,9 @@ small .npz fixtures next to this script:
                        shape (config 5 with its Zipf bias)
   golden_moe.npz       layer outputs of token samples at configs 2-5
   golden_route_wide.npz probs/ids of routers wider than 128 experts (256
-                       experts top-8; 250 experts top-16, an E % 8 tail)
+                       experts top-8; 250 experts top-16, an E % 8 tail) and
+                       past 256 experts or top-16 (264 top-4, 300 top-20,
+                       1024 top-32, 40 top-24)
   golden_rms.npz       rms_norm (src/matrix.c:666-711) rows at the configs'
                        widths and at widths with 8-column and scalar tails
   golden_attn.npz      the decode step's attention sublayer, x after
@@ -308,6 +310,11 @@ WIDE_ROUTES = [
     # name, T, d, E, k, std_router
     ("e256k8", 64, 128, 256, 8, 0.1),
     ("e250k16", 40, 64, 250, 16, 0.3),
+    # past the fast routing kernels' tables (the general kernels)
+    ("e264k4", 64, 64, 264, 4, 0.2),
+    ("e300k20", 48, 64, 300, 20, 0.3),
+    ("e1024k32", 32, 128, 1024, 32, 0.1),
+    ("e40k24", 40, 64, 40, 24, 0.5),
 ]
 
 

@@ -88,7 +88,8 @@ def test_argument_validation_without_gpu():
     assert lib.moe_hip_layer_create(128, 512, 4, 5, C.byref(h)) == 1      # k > E
     assert lib.moe_hip_layer_create(96, 512, 4, 2, C.byref(h)) == 2       # d % 64
     assert lib.moe_hip_layer_create(128, 48, 4, 2, C.byref(h)) == 2       # F % 32
-    assert lib.moe_hip_layer_create(128, 512, 300, 2, C.byref(h)) == 2    # E > 256
+    assert lib.moe_hip_layer_create(128, 512, 5000, 2, C.byref(h)) == 2   # E > 4096
+    assert lib.moe_hip_layer_create(128, 512, 300, 257, C.byref(h)) == 2  # top_k > 256
     assert b"must be 0" in lib.moe_hip_last_error_message() or lib.moe_hip_last_error() == 2
     assert lib.moe_hip_forward(None, None, None, None, None) == 1
     assert lib.moe_hip_set_expert_path(7) == 1

@@ -159,7 +159,10 @@ def test_route_bitexact(name, T, d, E, k, std_router, path, router_path):
     layer.close()
 
 
-WIDE_GOLDEN = [("e256k8", 64, 128, 256, 8, 0.1), ("e250k16", 40, 64, 250, 16, 0.3)]
+WIDE_GOLDEN = [("e256k8", 64, 128, 256, 8, 0.1), ("e250k16", 40, 64, 250, 16, 0.3),
+               # past 256 experts or top-16: the general routing kernels
+               ("e264k4", 64, 64, 264, 4, 0.2), ("e300k20", 48, 64, 300, 20, 0.3),
+               ("e1024k32", 32, 128, 1024, 32, 0.1), ("e40k24", 40, 64, 40, 24, 0.5)]
 
 
 @pytest.mark.parametrize("name,T,d,E,k,std", WIDE_GOLDEN, ids=[c[0] for c in WIDE_GOLDEN])
@@ -171,10 +174,13 @@ def test_route_wide_matches_compiled_reference(name, T, d, E, k, std):
     layer = mh.Layer(d, 64, E, k)
     layer.fill_synthetic(7, std, 0.02)
     x = orc.synth((T, d), 7, 0, 1.0)
-    probs, ids = route_on_device(layer, x)[:2]
+    dev = route_on_device(layer, x)
     layer.close()
+    probs, ids = dev[:2]
     assert np.array_equal(bits(probs), bits(g[f"{name}_probs"]))
     assert np.array_equal(ids, g[f"{name}_ids"])
+    # gate weights and the dispatch (counts, offsets, stable permutation)
+    assert_route_equal(dev, x, orc.synth((d, E), 7, 1, std), k, E)
 
 
 @pytest.mark.parametrize("path", ROUTER_PATHS, ids=["auto", "tiles", "rows"])
@@ -659,9 +665,69 @@ def test_error_paths():
     x = orc.synth((4, 128), 0, 0, 1.0)
     with pytest.raises(mh.MoeHipError):
         mh.moe_forward(x, bad)
-    many = host_layer(64, 32, 260, 2, 0, 0.02, 0.02)    # n_experts above the supported 256
+    many = host_layer(64, 32, 300, 257, 0, 0.02, 0.02)  # top_k above the supported 256
     with pytest.raises(mh.MoeHipError):
         mh.moe_forward(orc.synth((4, 64), 0, 0, 1.0), many)
+
+
+# Layers past the fast routing kernels' tables (more than 256 experts or
+# top-k above 16) route through the general kernels and then run the same
+# expert products: the decode kernels for small batches, the grouped GEMMs
+# for large ones.
+WIDE_LAYERS = [
+    # name, T, d, F, E, k, expert path (2 fused decode, 1 grouped GEMMs)
+    ("e300k20_decode", 24, 64, 128, 300, 20, 2),
+    ("e300k20_gemm", 400, 64, 128, 300, 20, 1),
+    ("e40k24_gemm", 256, 128, 64, 40, 24, 1),
+    ("e520k2_decode", 96, 64, 64, 520, 2, 2),
+    ("e520k2_gemm", 3000, 64, 64, 520, 2, 1),
+]
+
+
+@pytest.mark.parametrize("name,T,d,F,E,k,path", WIDE_LAYERS, ids=[c[0] for c in WIDE_LAYERS])
+def test_wide_layers(name, T, d, F, E, k, path):
+    """The layer (device rows and the host drop-in) and the in-place FFN
+    sublayer at wide routing shapes: routing and dispatch bit-exact with
+    the oracle, outputs within the bars."""
+    say(f"wide layer {name}: T={T} d={d} F={F} E={E} k={k}")
+    hw = host_layer(d, F, E, k, 23, 0.3, 0.05)
+    x = orc.synth((T, d), 23, 0, 1.0)
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw, nthreads=16)
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(23, 0.3, 0.05)
+    try:
+        dx = mh.DeviceArray.from_host(x)
+        dout = mh.DeviceArray((T, d))
+        dprobs = mh.DeviceArray((T, E))
+        dids = mh.DeviceArray((T, k), np.int32)
+        layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+        mh.synchronize()
+        assert mh.last_forward_path() == path
+        assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+        assert np.array_equal(dids.to_host(), i_ref)
+        assert_close(dout.to_host(), o_ref, f"{name} forward_dev")
+        # without probs / ids outputs (the logits then go to library scratch)
+        dout2 = mh.DeviceArray((T, d))
+        layer.forward_dev(dx.ptr, T, dout2.ptr, None, None)
+        mh.synchronize()
+        assert np.array_equal(bits(dout2.to_host()), bits(dout.to_host()))
+        dev = route_on_device(layer, x)
+        assert_route_equal(dev, x, hw.wr, k, E)
+        # x += MoE(rms_norm(x)) in place (the rows are normalised by a
+        # separate launch first)
+        w = orc.synth((d,), 23, 9, 0.1, mean=1.0)
+        dw = mh.DeviceArray.from_host(w)
+        layer.ffn_sublayer_dev(dx.ptr, dw.ptr, 1e-5, T)
+        mh.synchronize()
+        xn_ref = orc.rms_norm(x, w, 1e-5)
+        o2, _, i2 = orc.moe_forward(xn_ref, hw, nthreads=16)
+        assert_close(dx.to_host(), x + o2, f"{name} ffn sublayer")
+    finally:
+        layer.close()
+    out, probs, ids = mh.moe_forward(x, hw)
+    assert np.array_equal(bits(probs), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    assert_close(out, o_ref, f"{name} moe_forward")
 
 
 # Widths the kernels do not tile, which the host drop-ins take by padding
