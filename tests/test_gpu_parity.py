@@ -232,6 +232,47 @@ def test_route_ties_and_bias():
     layer.close()
 
 
+def test_route_wide_skip_ties_bias():
+    """The general routing kernels (300 experts, top-20) on the edge cases
+    of the fast ones: zero, negative-zero and denormal x facing inf and NaN
+    router weights (the per-step zero-skip), exact ties (lowest experts
+    first) and a router bias that starves experts."""
+    T, d, E, k = 100, 128, 300, 20
+    x = orc.synth((T, d), 7, 0, 1.0)
+    x[:, 5] = 0.0
+    x[:, 9] = -0.0
+    x[:, 40] = np.float32(1e-40)            # denormal: zero under DAZ
+    x[::3, 77] = 0.0
+    wr = orc.synth((d, E), 7, 1, 0.1)
+    wr[5, :] = np.inf
+    wr[9, ::2] = -np.inf
+    wr[40, 3] = np.nan
+    wr[77, 1] = 0.0
+    z = lambda *s: np.zeros(s, np.float32)
+    hw = HostMoE(wr, z(E, d, 64), z(E, d, 64), z(E, 64, d), k)
+    layer = mh.Layer(d, 64, E, k)
+    layer.load(hw)
+    dev = route_on_device(layer, x)
+    assert np.isfinite(dev[0]).all()
+    assert_route_equal(dev, x, wr, k, E)
+    layer.close()
+    col = orc.synth((d, 1), 5, 1, 0.1)
+    wr = np.ascontiguousarray(np.repeat(col, E, axis=1))     # all logits equal per row
+    hw = HostMoE(wr, z(E, d, 64), z(E, d, 64), z(E, 64, d), k)
+    layer = mh.Layer(d, 64, E, k)
+    layer.load(hw)
+    dev = route_on_device(layer, x)
+    assert (dev[1] == np.arange(k)).all(), "ties must pick experts 0..k-1"
+    assert_route_equal(dev, x, wr, k, E)
+    bias = np.zeros(E, np.float32)
+    bias[[3, 9, 260]] = 50.0
+    layer.set_bias(bias)
+    dev = route_on_device(layer, x)
+    assert_route_equal(dev, x, wr, k, E, bias)
+    assert dev[3][3] == T and dev[3][9] == T and dev[3][260] == T and dev[3].sum() == T * k
+    layer.close()
+
+
 # --------------------------------------------------------------------- full layer
 def test_dropin_moe_forward_c1():
     """Config 1 through the host-pointer drop-in moe_forward."""

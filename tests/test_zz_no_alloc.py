@@ -93,6 +93,23 @@ def test_noalloc_matches_forward_dev(cfg, t1, t2):
         layer.close()
 
 
+def test_noalloc_wide_routing():
+    """A layer past the fast routing kernels' tables (300 experts, top-20):
+    the general routing kernels' logits and dispatch scratch come from the
+    fixed array too; the grouped GEMMs at T = 400, then the decode kernels
+    at T = 24, each bit-identical to forward_dev."""
+    d, F, E, k = 64, 128, 300, 20
+    say(f"noalloc wide: T=400 then T=24, d={d} F={F} E={E} k={k}")
+    layer, x = make_layer(400, d, F, E, k, 0.3, 0.05, 13)
+    try:
+        for T in (400, 24):
+            ref = run(layer, layer.forward_dev, x, T)
+            got = run(layer, layer.forward_dev_noalloc, x, T)
+            assert_same(got, ref, f"wide T={T}")
+    finally:
+        layer.close()
+
+
 def test_noalloc_in_graph_replays():
     """Recorded in a HIP graph (no allocation happens during capture) and
     replayed several times with eager work and synchronisations between the
