@@ -38,6 +38,7 @@ Also measured in the same run (each a median of K marked steps unless said):
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
 """
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -300,10 +301,16 @@ def decode_host_dropin(mh, st, steps=10, T=64):
         hws.append(abi_types.HostMoE(L.get_router(), wg, wu, wd, L.k))
     xn = st["xn"].to_host()
     x = st["x"].to_host()
+    # As a C caller makes the calls: the structs built once, x updated in
+    # place by each layer (x += MoE(x_norm)).
+    cfgs = [hw.config(T) for hw in hws]
+    fn = mh.lib().moe_decode_batch
+    pxn, px = mh.fptr(xn), mh.fptr(x)
+    calls = [(C.byref(hw.weights), C.byref(cfg)) for hw, cfg in zip(hws, cfgs)]
 
     def step():
-        for hw in hws:
-            mh.decode_batch(xn, x, hw)
+        for w, cfg in calls:
+            mh.check(fn(w, cfg, pxn, T, px))
 
     step()
     per = []

@@ -1044,6 +1044,24 @@ hipError_t launch_read_probe(const float *src, size_t bytes, int mode, float *ou
     return hipGetLastError();
 }
 
+// dst = src, n16 16-byte units; either side may be pinned host memory,
+// which the kernel then reads or writes across the bus itself.
+__global__ __launch_bounds__(256) void copy16_kernel(const uint4 *src, uint4 *dst, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy16(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    if (bytes % 16 || reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+        return hipErrorInvalidValue;
+    const size_t n16 = bytes / 16;
+    const unsigned blocks = (unsigned)std::min<size_t>((n16 + 255) / 256, 1024);
+    hipLaunchKernelGGL(copy16_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const uint4 *>(src),
+                       static_cast<uint4 *>(dst), n16);
+    return hipGetLastError();
+}
+
 hipError_t launch_zero_ints(int *p, int n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)std::min(1024, (n + 255) / 256)), dim3(256),

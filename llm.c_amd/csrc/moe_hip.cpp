@@ -159,15 +159,22 @@ Workspace g_ws;
 // synchronous path for pageable memory; probs and ids go back on a copy
 // stream as soon as the routing has run, under the expert products.
 constexpr size_t kStageChunk = (size_t)16 << 20;   // half of the pinned area
+// Transfers of at most kZeroCopyMax bytes skip the copy engine: a copy
+// kernel on the call's stream reads or writes their region of a fine-grained
+// (coherent) pinned area of kZeroCopyArea bytes across the bus itself, which
+// spares the small decode transfers the copy engine's round trip.
+constexpr size_t kZeroCopyMax = (size_t)256 << 10, kZeroCopyArea = (size_t)2 << 20;
 struct HostStage {
     char *area = nullptr;         // 2 x kStageChunk bytes, pinned
+    char *zc = nullptr;           // kZeroCopyArea bytes, pinned, fine-grained
     hipEvent_t ev[2] = {};        // the last DMA that used each half (chunked transfers)
     hipStream_t copy = nullptr;   // (default priority)
     hipEvent_t routed = nullptr;  // recorded after a drop-in's routing
     bool ready = false;
     void release() {
         if (area) (void)hipHostFree(area);
-        area = nullptr;
+        if (zc) (void)hipHostFree(zc);
+        area = zc = nullptr;
         for (auto &e : ev) {
             if (e) (void)hipEventDestroy(e);
             e = nullptr;
@@ -294,6 +301,11 @@ int stage_init() {
         g_hs.area = nullptr;
         return set_err(MOE_HIP_ERR_NOMEM, "pinned staging of %zu bytes", 2 * kStageChunk);
     }
+    if (hipHostMalloc(reinterpret_cast<void **>(&g_hs.zc), kZeroCopyArea, hipHostMallocCoherent) !=
+        hipSuccess) {
+        g_hs.zc = nullptr;
+        return set_err(MOE_HIP_ERR_NOMEM, "pinned staging of %zu bytes", kZeroCopyArea);
+    }
     for (auto &e : g_hs.ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     HIP_TRY(hipStreamCreateWithFlags(&g_hs.copy, hipStreamNonBlocking));
     HIP_TRY(hipEventCreateWithFlags(&g_hs.routed, hipEventDisableTiming));
@@ -313,6 +325,13 @@ class Staging {
     int up(void *dev, const void *host, size_t n) {
         TRY(stage_init());
         if (n == 0) return MOE_HIP_OK;
+        if (zero_copy(dev, n)) {
+            char *pin = g_hs.zc + zoff_;
+            zoff_ += align(n);
+            memcpy(pin, host, n);
+            HIP_TRY(moe::launch_copy16(dev, pin, n, g_stream));
+            return MOE_HIP_OK;
+        }
         if (fits(n)) {
             if (chunked_up_) {   // (a chunked upload's DMAs may still read the area)
                 HIP_TRY(hipStreamSynchronize(g_stream));
@@ -344,6 +363,13 @@ class Staging {
     int down(void *host, const void *dev, size_t n, hipStream_t s) {
         TRY(stage_init());
         if (n == 0) return MOE_HIP_OK;
+        if (zero_copy(dev, n)) {
+            char *pin = g_hs.zc + zoff_;
+            zoff_ += align(n);
+            HIP_TRY(moe::launch_copy16(pin, dev, n, s));
+            pend_.push_back({host, pin, n, s});
+            return MOE_HIP_OK;
+        }
         if (fits(n)) {
             char *pin = g_hs.area + off_;
             off_ += align(n);
@@ -371,6 +397,19 @@ class Staging {
         off_ = 0;   // (every DMA into the area is done)
         return MOE_HIP_OK;
     }
+    // A small host array the device updates in place (kernels read and
+    // write it across the bus): its region of the fine-grained area, holding
+    // the host's values now and copied back by finish().  Null when the
+    // array does not qualify; the caller then stages it both ways.
+    float *inout(void *host, size_t n) {
+        if (stage_init() != MOE_HIP_OK) return nullptr;
+        if (n == 0 || n > kZeroCopyMax || n % 16 || zoff_ + n > kZeroCopyArea) return nullptr;
+        char *pin = g_hs.zc + zoff_;
+        zoff_ += align(n);
+        memcpy(pin, host, n);
+        pend_.push_back({host, pin, n, g_stream});
+        return reinterpret_cast<float *>(pin);
+    }
     int finish() {
         TRY(flush());
         HIP_TRY(hipStreamSynchronize(g_stream));
@@ -386,6 +425,10 @@ class Staging {
     };
     static size_t align(size_t n) { return (n + 255) & ~(size_t)255; }
     bool fits(size_t n) const { return off_ + n <= 2 * kStageChunk; }
+    bool zero_copy(const void *dev, size_t n) const {
+        return n <= kZeroCopyMax && n % 16 == 0 && reinterpret_cast<uintptr_t>(dev) % 16 == 0 &&
+               zoff_ + n <= kZeroCopyArea;
+    }
     // The queued small downloads waited for and copied out.
     int flush() {
         for (const Pending &p : pend_) HIP_TRY(hipStreamSynchronize(p.s));
@@ -402,7 +445,7 @@ class Staging {
         off_ = 0;
         return MOE_HIP_OK;
     }
-    size_t off_ = 0;
+    size_t off_ = 0, zoff_ = 0;
     bool chunked_up_ = false;
     std::vector<Pending> pend_;
 };
@@ -1560,9 +1603,15 @@ int moe_decode_batch(const MoEWeights *w, const ModelConfig *cfg, const float *x
     float *dxn = g_ws.x.as<float>(), *dx = g_ws.out.as<float>();
     Staging st;
     TRY(st.up(dxn, x_norm, sizeof(float) * xd));
-    TRY(st.up(dx, x, sizeof(float) * xd));
-    TRY(dropin_forward(L, d, dxn, n_rows, dx, nullptr, nullptr, 1));
-    TRY(st.down(x, dx, sizeof(float) * xd, g_stream));
+    // x += MoE(x_norm): a small x is updated where it is staged, across the
+    // bus, by the combine itself.
+    if (float *px = st.inout(x, sizeof(float) * xd)) {
+        TRY(dropin_forward(L, d, dxn, n_rows, px, nullptr, nullptr, 1));
+    } else {
+        TRY(st.up(dx, x, sizeof(float) * xd));
+        TRY(dropin_forward(L, d, dxn, n_rows, dx, nullptr, nullptr, 1));
+        TRY(st.down(x, dx, sizeof(float) * xd, g_stream));
+    }
     TRY(st.finish());
     return MOE_HIP_OK;
 }

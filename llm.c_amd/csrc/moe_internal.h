@@ -272,6 +272,9 @@ hipError_t launch_read_probe(const float *src, size_t bytes, int mode, float *ou
                              hipStream_t s);
 // p[0 .. n) = 0 by a kernel (safe to record in a graph, unlike a memset node).
 hipError_t launch_zero_ints(int *p, int n, hipStream_t s);
+// dst = src by a kernel (bytes and both addresses multiples of 16); either
+// side may be pinned host memory.
+hipError_t launch_copy16(void *dst, const void *src, size_t bytes, hipStream_t s);
 hipError_t launch_fill_normal(float *dst, size_t n, uint64_t seed,
                               uint64_t stream_id, float mean, float std,
                               hipStream_t s);
