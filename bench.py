@@ -697,7 +697,8 @@ def main():
         }
         line["decode_host_dropin"] = {
             "workload": "the same 8 layers through moe_decode_batch, host x_norm and x "
-                        "(pinned staging, synchronous calls)",
+                        "(synchronous calls from a C-style loop, x updated in place; transfers "
+                        "by copy kernels across the bus)",
             "tokens_per_s": dech["tokens_per_s"], "ms_per_step": dech["ms_per_step"],
             "bound_ms": dec["ms_per_step"] + dech["layers"] * dech["pcie_bytes_per_layer"]
                         * (2 / (h2d * 1e6) + 1 / (d2h * 1e6)) / 3}

@@ -1253,7 +1253,9 @@ struct FwdBufs {
     WideBufs wide;             // (layers routed by the general kernels)
 };
 
-int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
+// probs_given: the caller takes the router probabilities (the general
+// routing kernels then need no logits buffer of their own).
+int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p, bool probs_given) {
     const int d = L->d, F = L->F, E = L->E, k = L->k;
     const size_t n = (size_t)T * k;
     if (n > (size_t)0x7fffffff / (size_t)(F > d ? F : d))
@@ -1261,7 +1263,7 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p) {
     p->n = n;
     p->max_mtiles = (int)max_mtiles_of(n, E);
     if (is_wide(E, k)) {
-        p->wide_probs_floats = (size_t)T * E;
+        p->wide_probs_floats = probs_given ? 0 : (size_t)T * E;
         p->wide_ints = moe::wide_dispatch_ints(n, E);
     }
     // Expert products: skinny decode GEMVs (which find their own slots from
@@ -1468,7 +1470,7 @@ static int forward_impl(MoeHipLayer *L, const float *x, int T, float *out, float
     if (T == 0) return MOE_HIP_OK;
     hipStream_t s = pick_stream(stream);
     FwdPlan p;
-    TRY(plan_forward(L, T, &p));
+    TRY(plan_forward(L, T, &p, probs != nullptr));
     FwdBufs b;
     TRY(workspace_bufs(L, p, &b));
     return run_forward(L, x, T, out, probs, ids, accumulate, s, nm, p, b);
@@ -1488,7 +1490,7 @@ int moe_hip_forward_dev_noalloc(MoeHipLayer *L, const float *x, int T, float *ou
     char *base = nullptr;
     TRY(scratch_of(s, &base));
     FwdPlan p;
-    TRY(plan_forward(L, T, &p));
+    TRY(plan_forward(L, T, &p, probs != nullptr));
     FwdBufs b;
     size_t need = 0;
     carve_bufs(L, p, base, kScratchBytes, &b, &need);
