@@ -210,16 +210,18 @@ __global__ __launch_bounds__(1024) void proj16_kernel(AttnArgs a) {
 // Merged output of one head at dimension dim from its chunk partials at
 // float index ph + c * (hd + 2) = (m_c, l_c, o_c[hd]), c < nc:
 // o = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c with M = max_c m_c,
-// taken eight chunks at a time (online: the running sums are rescaled when
-// the maximum grows).  Loads past nc read chunk 0 and are masked, so every
-// batch's loads are in flight together.
+// taken sixteen chunks at a time (online: the running sums are rescaled when
+// the maximum grows), so contexts up to 2048 positions merge in one round
+// trip (eight at a time: 0.25-0.3 us more per block at context 1024).  Loads
+// past nc read chunk 0 and are masked, so every batch's loads are in flight
+// together.
 template <class RD>
 __device__ inline float merge_head(const RD &rd, size_t ph, int nc, int hd, int dim) {
     float M = -INFINITY, L = 0.0f, O = 0.0f;
-    for (int c0 = 0; c0 < nc; c0 += 8) {
-        float m[8], l[8], o[8];
+    for (int c0 = 0; c0 < nc; c0 += 16) {
+        float m[16], l[16], o[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 16; ++u) {
             const size_t pc = ph + (size_t)(c0 + u < nc ? c0 + u : 0) * (hd + 2);
             m[u] = rd(pc);
             l[u] = rd(pc + 1);
@@ -227,13 +229,13 @@ __device__ inline float merge_head(const RD &rd, size_t ph, int nc, int hd, int 
         }
         float Mn = M;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 16; ++u)
             if (c0 + u < nc) Mn = fmaxf(Mn, m[u]);
         const float f0 = expf(M - Mn);
         L *= f0;
         O *= f0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < 16; ++u)
             if (c0 + u < nc) {
                 const float f = expf(m[u] - Mn);
                 L = fmaf(f, l[u], L);
