@@ -43,6 +43,32 @@ __device__ inline void rope_pair(float &v0, float &v1, float c, float s) {
     v1 = a * s + b * c;
 }
 
+// Wave-wide max and sum through DPP instead of LDS permutes: four row_shr
+// steps (lanes without a source take the identity) leave each 16-lane row's
+// total in its lane 15; lanes 15, 31, 47 and 63 are then combined as
+// (r0 op r1) op (r2 op r3), the same value in every lane.
+template <int N> __device__ inline float shr_fill(float v, float fill) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v),
+                                                      0x110 + N, 0xF, 0xF, false));
+}
+__device__ inline float lane_of(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ inline float wave_max(float v) {
+    v = fmaxf(v, shr_fill<1>(v, -INFINITY));
+    v = fmaxf(v, shr_fill<2>(v, -INFINITY));
+    v = fmaxf(v, shr_fill<4>(v, -INFINITY));
+    v = fmaxf(v, shr_fill<8>(v, -INFINITY));
+    return fmaxf(fmaxf(lane_of(v, 15), lane_of(v, 31)), fmaxf(lane_of(v, 47), lane_of(v, 63)));
+}
+__device__ inline float wave_sum(float v) {
+    v = v + shr_fill<1>(v, 0.0f);
+    v = v + shr_fill<2>(v, 0.0f);
+    v = v + shr_fill<4>(v, 0.0f);
+    v = v + shr_fill<8>(v, 0.0f);
+    return (lane_of(v, 15) + lane_of(v, 31)) + (lane_of(v, 47) + lane_of(v, 63));
+}
+
 __device__ inline float4 add4(float4 a, float4 b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
 }
@@ -176,8 +202,7 @@ __global__ __launch_bounds__(1024) void proj16_kernel(AttnArgs a) {
     }
     if (QKV) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            for (int off = 32; off >= 1; off >>= 1) ss[i] += __shfl_xor(ss[i], off);
+        for (int i = 0; i < 2; ++i) ss[i] = wave_sum(ss[i]);
         if (lane == 0) {
             sm.ssw[0][wave] = ss[0];   // row wave / 2
             sm.ssw[1][wave] = ss[1];   // row 8 + wave / 2
@@ -371,14 +396,14 @@ __device__ void chunk(const AttnArgs &a, int bid, ChunkSmem<HD, G> &sm) {
     for (int h = wave; h < G; h += 4) {
         float m = -INFINITY;
         for (int t = lane; t < n; t += 64) m = fmaxf(m, sm.sc[h][t]);
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        m = wave_max(m);
         float l = 0.0f;
         for (int t = lane; t < kChunkPos; t += 64) {
             const float e = t < n ? expf(sm.sc[h][t] - m) : 0.0f;
             sm.sc[h][t] = e;
             l += e;
         }
-        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
+        l = wave_sum(l);
         if (lane == 0) {
             cstore(part + h * head_stride, m);
             cstore(part + h * head_stride + 1, l);
@@ -495,7 +520,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
     for (int h = 0; h < gqa; ++h) {
         float m = -INFINITY;
         for (int t = tid; t < n; t += 256) m = fmaxf(m, sc[h][t]);
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        m = wave_max(m);
         if (lane == 0) red[h][wave] = m;
     }
     __syncthreads();
@@ -507,7 +532,7 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(AttnArgs a) {
             sc[h][t] = e;
             l += e;
         }
-        for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
+        l = wave_sum(l);
         __syncthreads();   // every wave has read red[h] before it is reused
         if (lane == 0) red[h][wave] = l;
         if (tid == 0) part[h * head_stride] = m;
