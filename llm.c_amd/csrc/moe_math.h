@@ -99,6 +99,19 @@ __device__ inline float glibc_expf(float x) {
 // calls this (a dead row passes any valid row and store = false).  ys: an
 // optional second copy of the row (e.g. in LDS), written even when !store,
 // flushed to zero if FTZ.
+// Within each 16-lane row: lane l reads lane l + N (DPP row_shl; the top N
+// lanes keep their own value, which the folds below never read), and lane
+// 0's value to every lane of the row (row_newbcast).  The same moves as
+// width-16 shuffles, without an LDS permute round trip.
+template <int N> __device__ inline float row_down(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                      0x100 + N, 0xF, 0xF, false));
+}
+__device__ inline float row_lane0(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v),
+                                                      0x150, 0xF, 0xF, false));
+}
+
 template <class LD>
 __device__ inline void rms_row16(const LD &ld, const float *w, int nb, float eps, float rcp_cols,
                                  float *y, bool store, float *ys = nullptr, bool ftz = false) {
@@ -124,11 +137,11 @@ __device__ inline void rms_row16(const LD &ld, const float *w, int nb, float eps
                 if (b0 + u < nb) acc = fmaf(u8[u], u8[u], acc);
         }
     }
-    acc = acc + __shfl_down(acc, 8, 16);
-    acc = acc + __shfl_down(acc, 4, 16);
-    acc = acc + __shfl_down(acc, 1, 16);
-    acc = acc + __shfl_down(acc, 2, 16);
-    const float inv = __shfl(1.0f / sqrtf(fmaf(acc, rcp_cols, eps)), 0, 16);
+    acc = acc + row_down<8>(acc);
+    acc = acc + row_down<4>(acc);
+    acc = acc + row_down<1>(acc);
+    acc = acc + row_down<2>(acc);
+    const float inv = row_lane0(1.0f / sqrtf(fmaf(acc, rcp_cols, eps)));
     if (!store && !ys) return;
     auto put = [&](int i, float o) {
         if (store) y[i] = o;

@@ -641,11 +641,11 @@ __global__ __launch_bounds__(NB > 0 ? 64 : 256) void rms_norm_kernel(
         float acc = 0.0f;
 #pragma unroll
         for (int b = 0; b < NB; ++b) acc = fmaf(v[b], v[b], acc);
-        acc = acc + __shfl_down(acc, 8, 16);
-        acc = acc + __shfl_down(acc, 4, 16);
-        acc = acc + __shfl_down(acc, 1, 16);
-        acc = acc + __shfl_down(acc, 2, 16);
-        const float inv = __shfl(1.0f / sqrtf(fmaf(acc, rcp_cols, eps)), 0, 16);
+        acc = acc + row_down<8>(acc);
+        acc = acc + row_down<4>(acc);
+        acc = acc + row_down<1>(acc);
+        acc = acc + row_down<2>(acc);
+        const float inv = row_lane0(1.0f / sqrtf(fmaf(acc, rcp_cols, eps)));
         if (!live) return;
         float *yr = y + (size_t)row * cols;
 #pragma unroll
