@@ -185,25 +185,22 @@ __global__ __launch_bounds__(512, 1) void decode_routed_kernel(DecodeArgs a, Rou
         fused_down_pass<NW, true>(a, g, fb, acc2, rows, list, r0, hs, wa, wb);
     }
 
-    // The routing results (and the normalised rows) from the first
-    // workgroup, last, so that no stores of varying count sit among the
-    // weight loads whose completion the loops count.
-    if (blockIdx.x == 0) {
-        for (int i = tid; i < n; i += 64 * NW) {
+    // The routing results (and the normalised rows, when wanted), token t
+    // by workgroup t (every workgroup holds them all), last, so that no
+    // stores of varying count sit among the weight loads whose completion
+    // the loops count, and no one workgroup's end waits on all of them.
+    for (int ct = blockIdx.x; ct < T; ct += gridDim.x) {
+        if (tid < k) {
+            const int i = ct * k + tid;
             if (ra.ids) ra.ids[i] = isel[i];
-            if (ra.gw) ra.gw[i] = ftz_f(psel[i] * invs[i / k]);
+            if (ra.gw) ra.gw[i] = ftz_f(psel[i] * invs[ct]);
         }
         if (ra.probs)
-            for (int i = tid; i < T * E; i += 64 * NW) {
-                const int ct = i / E, ex = i - ct * E;
-                ra.probs[i] = lg[ct * (E + 1) + ex];
-            }
-        if (ra.rms_w)
-            for (int i = tid; i < T * (KC / 4); i += 64 * NW) {
-                const int rr = i / (KC / 4), c4 = i - rr * (KC / 4);
-                *reinterpret_cast<float4 *>(ra.xn_out + (size_t)rr * KC + 4 * c4) =
-                    *reinterpret_cast<const float4 *>(xs + rr * LD + 4 * c4);
-            }
+            for (int ex = tid; ex < E; ex += 64 * NW) ra.probs[ct * E + ex] = lg[ct * (E + 1) + ex];
+        if (ra.rms_w && ra.xn_out)
+            for (int c4 = tid; c4 < KC / 4; c4 += 64 * NW)
+                *reinterpret_cast<float4 *>(ra.xn_out + (size_t)ct * KC + 4 * c4) =
+                    *reinterpret_cast<const float4 *>(xs + ct * LD + 4 * c4);
     }
 }
 
@@ -239,7 +236,7 @@ bool decode_routed_ok(int T, int d, int F, int E, int k) {
 
 hipError_t launch_decode_routed(const DecodeArgs &a, const RouteArgs &ra, hipStream_t s) {
     if (!decode_routed_ok(ra.T, a.d, a.F, a.E, ra.k) || ra.d != a.d || ra.E != a.E ||
-        a.nslots != ra.T * ra.k || !ra.wrT || !a.w2 || (ra.rms_w && (!ra.x_raw || !ra.xn_out)))
+        a.nslots != ra.T * ra.k || !ra.wrT || !a.w2 || (ra.rms_w && !ra.x_raw))
         return hipErrorInvalidValue;
     const size_t lds = decode_routed_lds(ra.T, a.d, a.E, ra.k);
     if (a.d == 512) return a.E <= 8 ? launch_routed<512, 1>(a, ra, lds, s) : launch_routed<512, 2>(a, ra, lds, s);

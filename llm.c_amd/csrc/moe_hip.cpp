@@ -455,6 +455,9 @@ class Staging {
 struct Norm {
     const float *x_raw = nullptr, *rms_w = nullptr;
     float eps = 0.0f;
+    // The normalised rows are the caller's output (else only the kernels that
+    // read them back need them written).
+    bool keep_rows = true;
 };
 
 // Residency cache for the drop-in entry points.
@@ -1386,8 +1389,10 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
         ra.wrT = L->wrT;
         ra.no_dispatch = 1;
         if (nm.x_raw) {
+            // (the routed kernel keeps the normalised rows in LDS: they go to
+            // x only when the caller takes them)
             ra.x_raw = nm.x_raw; ra.rms_w = nm.rms_w; ra.rms_eps = nm.eps;
-            ra.rms_rcp = 1.0f / (float)d; ra.xn_out = const_cast<float *>(x);
+            ra.rms_rcp = 1.0f / (float)d; ra.xn_out = nm.keep_rows ? const_cast<float *>(x) : nullptr;
         }
         moe::DecodeArgs gu{};
         gu.x = x; gu.ids = ids_d; gu.topk = k; gu.w = L->wgu; gu.w2 = L->wdT; gu.out = b.ys;
@@ -1723,6 +1728,7 @@ int moe_hip_ffn_sublayer_dev(MoeHipLayer *L, float *x, const float *rms_w, float
     }
     Norm nm;
     nm.x_raw = x; nm.rms_w = rms_w; nm.eps = eps;
+    nm.keep_rows = x_norm != nullptr;
     return forward_impl(L, xn, T, x, probs, ids, 1, stream, nm);
 }
 
