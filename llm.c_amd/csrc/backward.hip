@@ -728,7 +728,7 @@ __global__ __launch_bounds__(256) void slot_kernel(SlotRows Y, const float *dout
 
 // Eight lanes per token: dlogits [T x E] from dgw through the gate
 // renormalisation, the aux term and the softmax.  Every lane of a token
-// loads its ids, dgw and gw (kMaxTopK of each, clamped, masked) and the
+// loads its ids and dgw (kMaxTopK of each, clamped, masked) and the
 // probabilities of its experts e = g, g + 8, ... (g = lane % 8) at once, then
 // the selected probabilities; S, c and dp(e) are summed in slot order and
 // the dot over the experts in expert order (through shuffles), as one thread
@@ -737,7 +737,7 @@ __global__ __launch_bounds__(256) void slot_kernel(SlotRows Y, const float *dout
 constexpr int kRbG = 8;
 template <int JN>
 __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, const int *ids,
-                                                         const float *gw, const float *dgw,
+                                                         const float *dgw,
                                                          const int *counts, int T, int E, int k,
                                                          float aux_coef, float *dlogits) {
     const int gid = blockIdx.x * 256 + threadIdx.x;
@@ -745,31 +745,39 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(const float *probs, con
     const int tc = min(t, T - 1);
     const float *p = probs + (size_t)tc * E;
     int id[kMaxTopK];
-    float dg[kMaxTopK], w[kMaxTopK], ps[kMaxTopK];
+    float dg[kMaxTopK], ps[kMaxTopK];
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s) {
         const size_t q = (size_t)tc * k + min(s, k - 1);
         id[s] = ids[q];
         dg[s] = dgw[q];
-        w[s] = gw[q];
     }
+    // The aux term's counts enter as differences from a fixed count (the
+    // softmax gradient p (dp - sum p dp) does not change when every dp moves
+    // by one constant): near-uniform loads then give small exact values, so
+    // the subtraction below does not cancel the large common part in fp32.
+    const int cref = (int)(((long long)T * k) / E);
     float pv[JN], cn[JN];
 #pragma unroll
     for (int j = 0; j < JN; ++j)
         if (kRbG * j < E) {
             const int e = min(g + kRbG * j, E - 1);
             pv[j] = p[e];
-            cn[j] = (float)counts[e];
+            cn[j] = (float)(counts[e] - cref);
         }
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s) ps[s] = p[id[s]];
+    // c = sum over slots of dgw * (p / S), the renormalised weights taken
+    // as p / S here: at top-1 that is exactly 1, so the slot term (dgw - c)
+    // / S vanishes exactly as its derivative does (the stored gate weight,
+    // p * (1 / S), can sit an ulp below 1).
     float S = 0.f, c = 0.f;
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
-        if (s < k) {
-            S += ps[s];
-            c = fmaf(dg[s], w[s], c);
-        }
+        if (s < k) S += ps[s];
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s)
+        if (s < k) c = fmaf(dg[s], ps[s] / S, c);
     const float aux_scale = aux_coef * (float)E / ((float)T * (float)T * (float)k);
     float dpv[JN];
 #pragma unroll
@@ -845,6 +853,10 @@ unsigned blocks_for(size_t n) { return (unsigned)std::min<size_t>((n + 255) / 25
 }  // namespace
 
 bool backward_engine_ok(int d, int F) { return d % 64 == 0 && F % 64 == 0; }
+
+size_t backward_dh_floats(size_t n, int d, int F, int E) {
+    return std::max(n * (size_t)F, (size_t)d * E + E);
+}
 
 size_t backward_tail_floats(int d, int F, int max_mtiles) {
     if (!backward_engine_ok(d, F)) return 0;
@@ -948,10 +960,10 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
         const dim3 grid((unsigned)(((size_t)T * kRbG + 255) / 256));
         if (E <= 128)
             hipLaunchKernelGGL(router_bwd_kernel<128 / kRbG>, grid, dim3(256), 0, s, b.probs, b.ids,
-                               b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
+                               b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
         else
             hipLaunchKernelGGL(router_bwd_kernel<kMaxExperts / kRbG>, grid, dim3(256), 0, s, b.probs,
-                               b.ids, b.gw, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
+                               b.ids, b.dgw, b.counts, T, E, k, b.aux_coef, b.dlogits);
     }
     hipLaunchKernelGGL(dx_kernel, dim3((unsigned)(((size_t)T * (d / 4) + 255) / 256)), dim3(256),
                        0, s, dXr, b.inv,
@@ -1007,10 +1019,12 @@ hipError_t launch_moe_backward(const BackwardArgs &b, hipStream_t s) {
     }
     // The router's over all tokens (and the aux loss's column sums), in row
     // chunks whose partials (in dH, free by now) are then added in chunk
-    // order: enough chunks for about one workgroup per CU.
+    // order: enough chunks for about one workgroup per CU, as many as dH
+    // holds (it holds one chunk's at least: backward_dh_floats).
     const int ncb = (d + 63) / 64;
+    const size_t cap = backward_dh_floats(n, d, F, E);
     int R = std::max(16, (int)((T + std::max(1, 256 / ncb) - 1) / std::max(1, 256 / ncb)));
-    while ((size_t)((T + R - 1) / R) * ((size_t)d * E + E) > n * F) R *= 2;
+    while (R < T && (size_t)((T + R - 1) / R) * ((size_t)d * E + E) > cap) R *= 2;
     const int nz = (T + R - 1) / R;
     float *P = b.dH, *CS = b.aux ? b.dH + (size_t)nz * d * E : nullptr;
     hipLaunchKernelGGL(router_grad_kernel, dim3((unsigned)ncb, (unsigned)nz), dim3(256), 0, s,

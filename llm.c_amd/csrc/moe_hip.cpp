@@ -1674,18 +1674,19 @@ int moe_hip_backward_dev(MoeHipLayer *L, const float *x, int T, const float *dou
     TRY(g_ws.bw.reserve(sizeof(float) * 3 * E * dF));
     float *w0 = g_ws.bw.as<float>(), *w1 = w0 + E * dF, *w2 = w1 + E * dF;
     if (!engine) HIP_TRY(moe::launch_unpack_experts(L->wgu, L->wdT, w0, w1, w2, E, d, F, s));
-    // Workspace: G, U, H, dH [n x F]; Y [splits][n x d], dY [n x d]; dgw,
-    // inv [n]; dlogits [T x E].
-    const size_t nF = n * F, nd = n * d;
+    // Workspace: G, U, H [n x F], dH [n x F, at least d E + E: the router
+    // gradient's chunk partials reuse it]; Y [splits][n x d], dY [n x d];
+    // dgw, inv [n]; dlogits [T x E].
+    const size_t nF = n * F, nd = n * d, ndh = moe::backward_dh_floats(n, d, F, E);
     const size_t ysplits = (size_t)moe::backward_slot_splits(d, F, max_mtiles, n);
     const size_t npieces = engine && d % 256 == 0 ? n * (size_t)(d / 256) : 0;
     const size_t ntail = moe::backward_tail_floats(d, F, max_mtiles);
     // (the split-tail pieces last, 256-byte aligned)
-    const size_t tail_off = (4 * nF + (ysplits + 1) * nd + 2 * n + (size_t)T * E + npieces + 63) &
-                            ~(size_t)63;
+    const size_t tail_off = (3 * nF + ndh + (ysplits + 1) * nd + 2 * n + (size_t)T * E + npieces +
+                             63) & ~(size_t)63;
     TRY(g_ws.bwork.reserve(sizeof(float) * (tail_off + ntail)));
     float *G = g_ws.bwork.as<float>(), *U = G + nF, *H = U + nF, *dH = H + nF;
-    float *Y = dH + nF, *dY = Y + ysplits * nd, *dgw = dY + nd;
+    float *Y = dH + ndh, *dY = Y + ysplits * nd, *dgw = dY + nd;
     int *inv = reinterpret_cast<int *>(dgw + n);
     float *dlogits = reinterpret_cast<float *>(inv + n);
     int *pieces = npieces ? reinterpret_cast<int *>(dlogits + (size_t)T * E) : nullptr;

@@ -222,8 +222,8 @@ hipError_t launch_pack_cols16(const float *src, float *dst, int K, int N, int co
 // Backward pass of the layer (backward.hip) with the routing of a forward
 // already run (probs, ids, gw, counts, offsets, tile schedule, perm).
 // Weights in the reference layout: wr [d x E], wg, wu [E][d x F], wd [E][F x d].
-// Workspace: G, U, H, dH [n x F], Y, dY [n x d] (n = T k), dgw [n], inv [n],
-// dlogits [T x E].  Outputs (accumulate: added to): dx [T x d], dwr,
+// Workspace: G, U, H [n x F], dH [backward_dh_floats], Y, dY [n x d]
+// (n = T k), dgw [n], inv [n], dlogits [T x E].  Outputs (accumulate: added to): dx [T x d], dwr,
 // dwg, dwu, dwd (layouts of the weights); aux (optional) = the loss value.
 struct BackwardArgs {
     const float *x, *dout;
@@ -256,6 +256,9 @@ bool backward_engine_ok(int d, int F);
 int backward_slot_splits(int d, int F, int max_mtiles, size_t n);
 // Floats of BackwardArgs::tail_part the engine path uses (0: none).
 size_t backward_tail_floats(int d, int F, int max_mtiles);
+// Floats of BackwardArgs::dH: n x F, and at least one row chunk of the
+// router gradient's partials (d E + E), which reuse it at the end.
+size_t backward_dh_floats(size_t n, int d, int F, int E);
 
 // rms_norm (src/matrix.c:666-711) of rows x cols, weight w [cols].
 hipError_t launch_rms_norm(const float *x, const float *w, float eps, int rows, int cols,

@@ -154,12 +154,17 @@ def run_device_backward(d, F, E, k, T, seed, aux_coef, accumulate_twice=False):
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape", [(128, 512, 4, 2, 256), (256, 1024, 8, 2, 384),
                                    (128, 256, 16, 4, 100), (64, 96, 4, 2, 150),
-                                   (192, 1024, 8, 2, 600), (64, 128, 256, 8, 400)],
-                         ids=["c1", "c2-rows", "e16-k4", "untiled", "d192", "e256-k8"])
+                                   (192, 1024, 8, 2, 600), (64, 128, 256, 8, 400),
+                                   (128, 96, 3, 1, 64), (64, 64, 4, 1, 700)],
+                         ids=["c1", "c2-rows", "e16-k4", "untiled", "d192", "e256-k8",
+                              "top1-e3", "top1-e4"])
 @pytest.mark.parametrize("aux_coef", [0.0, 0.5])
 def test_backward_device_vs_oracle(shape, aux_coef):
     """The tile-engine path (d, F multiples of 64; split partials by slot at
-    c2-rows) and the untiled row products (F = 96).  The weight-gradient
+    c2-rows) and the untiled row products (F = 96).  At top-1 the router's
+    gradient is the aux term alone, small against its parts when the loads
+    are near-uniform (a cancellation the kernel avoids by counting loads
+    from a fixed count).  The weight-gradient
     tiles: 64 x 64 at the small shapes, 64 x 128 for dW_g/dW_u at d192 (d
     not a multiple of 128), 128 x 128 and 128 x 64 at the batch-8x512 shape
     (test_backward_device_split_tail)."""
@@ -168,6 +173,26 @@ def test_backward_device_vs_oracle(shape, aux_coef):
     res, x, dout, wr, wg, wu, wd = run_device_backward(d, F, E, k, T, 31, aux_coef)
     hw_ids = orc.route(x, wr, k)[1]   # the fp32 forward's routing (bit-exact on the device)
     g = mb.moe_backward64(x, wr, wg, wu, wd, hw_ids, dout, aux_coef)
+    for name in ("dx", "dwr", "dwg", "dwu", "dwd"):
+        rel = orc.rel_l2(res[name], g[name])
+        print(f"[gpu-test]   {name}: rel-L2 {rel:.3e}", flush=True)
+        assert rel <= 1e-5, name
+    assert abs(res["aux"] - g["aux"]) <= 1e-5 * max(1.0, abs(g["aux"]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(192, 96, 3, 1, 1), (128, 128, 16, 1, 1), (64, 64, 256, 2, 3),
+                                   (256, 64, 64, 4, 5)],
+                         ids=["untiled-t1", "engine-t1", "e256-t3", "e64-t5"])
+def test_backward_tiny_layers(shape):
+    """A few tokens against a wide router: the router gradient's row-chunk
+    partials (d E + E floats for one chunk) exceed the T k F floats of dH,
+    which they reuse; the workspace holds one chunk at least."""
+    d, F, E, k, T = shape
+    print(f"[gpu-test] backward tiny d={d} F={F} E={E} k={k} T={T}", flush=True)
+    res, x, dout, wr, wg, wu, wd = run_device_backward(d, F, E, k, T, 51, 0.5)
+    hw_ids = orc.route(x, wr, k)[1]
+    g = mb.moe_backward64(x, wr, wg, wu, wd, hw_ids, dout, 0.5)
     for name in ("dx", "dwr", "dwg", "dwu", "dwd"):
         rel = orc.rel_l2(res[name], g[name])
         print(f"[gpu-test]   {name}: rel-L2 {rel:.3e}", flush=True)
