@@ -227,3 +227,38 @@ def test_backward_deterministic_and_accumulates():
     for name in ("dx", "dwr", "dwg", "dwu", "dwd"):
         assert np.array_equal(a[name], b[name]), name
         assert np.array_equal(c[name], a[name] + a[name]), name
+
+
+def draw_backward(i):
+    rng = np.random.default_rng(9000 + i)
+    d = int(rng.choice([64, 128, 192, 256]))
+    F = int(rng.choice([64, 96, 128, 256, 320, 512]))
+    E = int(rng.choice([1, 2, 3, 4, 8, 16, 64, 256]))
+    k = int(rng.integers(1, min(E, 16) + 1))
+    T = int(rng.choice([1, 5, 64, 129, 300, 700]))
+    aux = float(rng.choice([0.0, 0.5]))
+    return d, F, E, k, T, aux
+
+
+BWD_RANDOM = [draw_backward(i) for i in range(32)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(len(BWD_RANDOM)),
+                         ids=[f"d{c[0]}_F{c[1]}_E{c[2]}_k{c[3]}_T{c[4]}_a{c[5]}" for c in BWD_RANDOM])
+def test_backward_random_shapes(i):
+    """Seeded random layers (1 to 700 tokens, 1 to 256 experts, top-1 to
+    top-16, tiled and untiled widths, with and without the aux loss): every
+    gradient within rel-L2 1e-5 of the fp64 oracle."""
+    d, F, E, k, T, aux = BWD_RANDOM[i]
+    print(f"[gpu-test] backward random {i}: d={d} F={F} E={E} k={k} T={T} aux={aux}", flush=True)
+    res, x, dout, wr, wg, wu, wd = run_device_backward(d, F, E, k, T, 100 + i, aux)
+    hw_ids = orc.route(x, wr, k)[1]
+    g = mb.moe_backward64(x, wr, wg, wu, wd, hw_ids, dout, aux)
+    for name in ("dx", "dwr", "dwg", "dwu", "dwd"):
+        if not np.abs(g[name]).max() > 0:   # (top-1 without the loss: no router gradient)
+            assert np.abs(res[name]).max() <= 1e-6, name
+            continue
+        rel = orc.rel_l2(res[name], g[name])
+        assert rel <= 1e-5, (name, rel)
+    assert abs(res["aux"] - g["aux"]) <= 1e-5 * max(1.0, abs(g["aux"]))
