@@ -257,3 +257,38 @@ def test_attn_decode_device_vs_reference(case):
     for b, p in enumerate(pos):
         assert orc.rel_l2(kg[b, p], g[f"k_{case}"][b]) < 1e-5
         assert orc.rel_l2(vg[b, p], g[f"v_{case}"][b]) < 1e-5
+
+
+def draw_attn(i):
+    rng = np.random.default_rng(7000 + i)
+    hd = int(rng.choice([8, 16, 32, 64]))
+    nkv = int(rng.choice([1, 2, 4]))
+    nh = nkv * int(rng.choice([1, 2, 4, 8]))
+    d = int(rng.choice([64, 128, 256, 512]))
+    B = int(rng.choice([1, 3, 17, 64]))
+    max_seq = int(rng.choice([1, 2, 100, 129, 700, 1100]))
+    return d, nh, nkv, hd, B, max_seq, rng.integers(0, max_seq, B)
+
+
+ATTN_RANDOM = [draw_attn(i) for i in range(24)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("i", range(len(ATTN_RANDOM)),
+                         ids=[f"d{c[0]}_h{c[1]}_kv{c[2]}_hd{c[3]}_B{c[4]}_S{c[5]}" for c in ATTN_RANDOM])
+def test_attn_decode_random_shapes(i):
+    """Seeded random head shapes (hd 8-64, one to eight query heads per kv
+    head, 1-64 sequences at random positions, caches of 1-1100 positions):
+    x within the layer tolerance of the oracle, the new cache rows too,
+    every other cache row unchanged bit for bit."""
+    d, nh, nkv, hd, B, max_seq, pos = ATTN_RANDOM[i]
+    x, w, kc, vc, pos, c, s = make_case(B, max_seq, pos, 200 + i, d, nh, nkv, hd)
+    print(f"[gpu-test] attention random {i}: d={d} nh={nh} nkv={nkv} hd={hd} B={B} S={max_seq}",
+          flush=True)
+    xg, kg, vg = run_device(x, w, kc, vc, pos, c, s, nh, nkv, hd)
+    xo, ko, vo = run_oracle(x, w, kc, vc, pos, c, s, nh, nkv, hd)
+    assert orc.rel_l2(xg, xo) <= 1e-5 and float(np.abs(xg - xo).max()) <= 1e-4
+    for b, p in enumerate(pos):
+        keep = np.arange(max_seq) != p
+        assert np.array_equal(kg[b, keep], kc[b, keep]) and np.array_equal(vg[b, keep], vc[b, keep])
+        assert orc.rel_l2(kg[b, p], ko[b, p]) < 1e-5 and orc.rel_l2(vg[b, p], vo[b, p]) < 1e-5
