@@ -439,8 +439,9 @@ __global__ __launch_bounds__(128 * WN) void grouped_gemm_kernel(GemmArgs a) {
     const int per_split = a.max_mtiles * ntiles;
     const int ks = blockIdx.x / per_split;       // reduction split (down projection)
     const int nt = (blockIdx.x % per_split) % ntiles;
-    const int mtg = (blockIdx.x % per_split) / ntiles;
+    int mtg = (blockIdx.x % per_split) / ntiles;
     if (mtg >= a.tile_off[a.E]) return;
+    if (a.order) mtg = a.order[mtg];
     const int nk = nks / a.ksplit;   // K steps of this split
     gemm_tile<MODE, WN>(a, smem, mtg, nt, ks * nk * KT, nk, ks, 0);
 }
@@ -745,6 +746,56 @@ __global__ __launch_bounds__(512) void tail_fixup_kernel(GemmArgs a) {
     }
 }
 
+// The short-first m-tile order: thread t takes experts [t EPT, (t + 1)
+// EPT); the count of short last m-tiles before each expert comes from a
+// workgroup scan (wave shuffles, then the wave totals).
+constexpr int kOrderThreads = 1024;
+__global__ __launch_bounds__(kOrderThreads) void short_first_order_kernel(const int *offsets,
+                                                                          const int *tile_off,
+                                                                          int E, int *order) {
+    __shared__ int wtot[kOrderThreads / 64];
+    __shared__ int nshort;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int ept = (E + kOrderThreads - 1) / kOrderThreads;
+    const int e0 = min(E, tid * ept), e1 = min(E, e0 + ept);
+    auto is_short = [&](int e) {
+        const int m = tile_off[e + 1] - tile_off[e];
+        return m > 0 && offsets[e + 1] - offsets[e] - BM * (m - 1) <= 96;
+    };
+    int c = 0;
+    for (int e = e0; e < e1; ++e) c += is_short(e);
+    int v = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    if (lane == 63) wtot[w] = v;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int i = 0; i < kOrderThreads / 64; ++i) {
+            const int t = wtot[i];
+            wtot[i] = run;
+            run += t;
+        }
+        nshort = run;
+    }
+    __syncthreads();
+    int sb = wtot[w] + v - c;   // short m-tiles of the experts before e0
+    const int ns = nshort;
+    for (int e = e0; e < e1; ++e) {
+        const int t0 = tile_off[e], m = tile_off[e + 1] - t0;
+        const bool sh = is_short(e);
+        for (int j = 0; j < m; ++j) {
+            const int mt = t0 + j;
+            if (sh && j == m - 1) order[sb] = mt;
+            else order[ns + mt - sb] = mt;
+        }
+        sb += sh;
+    }
+}
+
 }  // namespace
 
 // Compute units of the current device (cached; 256 on MI355X).
@@ -856,6 +907,14 @@ hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s) {
         attr_set = true;
     }
     hipLaunchKernelGGL((grouped_gemm_kernel<1, 4>), dim3((unsigned)a.sk_groups), dim3(512), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_short_first_order(const int *offsets, const int *tile_off, int E, int *order,
+                                    hipStream_t s) {
+    if (E <= 0 || E > 4 * kOrderThreads || !order) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(short_first_order_kernel, dim3(1), dim3(kOrderThreads), 0, s, offsets,
+                       tile_off, E, order);
     return hipGetLastError();
 }
 

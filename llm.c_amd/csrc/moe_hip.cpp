@@ -143,11 +143,13 @@ struct DevBuf {
 // Workspace shared by every call (calls are serialised by the caller).
 struct Workspace {
     DevBuf x, out, probs, ids, gw, counts, offsets, tile_off, tile_expert, perm, h, ys, pieces,
-        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork, xpad, gu_part, wprobs, wide;
+        stage, counters, xn, rmsw, aq, ao, apart, acnt, bw, bwork, xpad, gu_part, wprobs, wide,
+        order;
     void release_all() {
         DevBuf *all[] = {&x, &out, &probs, &ids, &gw, &counts, &offsets, &tile_off,
                          &tile_expert, &perm, &h, &ys, &pieces, &stage, &counters, &xn, &rmsw,
-                         &aq, &ao, &apart, &acnt, &bw, &bwork, &xpad, &gu_part, &wprobs, &wide};
+                         &aq, &ao, &apart, &acnt, &bw, &bwork, &xpad, &gu_part, &wprobs, &wide,
+                         &order};
         for (DevBuf *b : all) b->release();
     }
 };
@@ -1240,6 +1242,7 @@ struct FwdPlan {
     size_t pieces_ints = 0; // stream-K piece counts [n][d / 256]
     int gu_tail = 0;        // gate/up split tail: workgroups per round (moe::gateup_tail_groups)
     size_t gu_part_floats = 0;  // its pieces
+    size_t order_ints = 0;  // the down projection's short-first m-tile order (whole tiles, >= 4 rounds)
     size_t wide_probs_floats = 0, wide_ints = 0;   // general routing kernels' buffers (WideBufs)
 };
 
@@ -1252,6 +1255,7 @@ struct FwdBufs {
     float *h = nullptr, *ys = nullptr;
     int *pieces = nullptr;     // [n][d / 256] (stream-K down projection)
     float *gu_part = nullptr;  // gate/up split-tail pieces
+    int *order = nullptr;      // [max_mtiles] m-tile order of the down projection
     int *counters = nullptr;   // kMaxCounters ints, zero between launches
     WideBufs wide;             // (layers routed by the general kernels)
 };
@@ -1300,6 +1304,9 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p, bool probs_given) {
         p->pieces_ints = dp.streamk ? n * (size_t)(d / 256) : 0;
         p->gu_tail = moe::gateup_tail_groups(2 * F, d, p->max_mtiles);
         p->gu_part_floats = (size_t)p->gu_tail * moe::kGemmBM * 256;
+        if (!dp.streamk && dp.slots == 1 && dp.bn == 256 &&
+            (long)p->max_mtiles * (d / 256) >= 4L * moe::device_cus())
+            p->order_ints = (size_t)p->max_mtiles;
         p->h_floats = n * F;
         p->ys_floats = (size_t)p->ksplit * n * d;
     }
@@ -1319,6 +1326,7 @@ int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
     TRY(g_ws.ys.reserve(sizeof(float) * p.ys_floats));
     if (p.pieces_ints) TRY(g_ws.pieces.reserve(sizeof(int) * p.pieces_ints));
     if (p.gu_part_floats) TRY(g_ws.gu_part.reserve(sizeof(float) * p.gu_part_floats));
+    if (p.order_ints) TRY(g_ws.order.reserve(sizeof(int) * p.order_ints));
     if (p.wide_probs_floats) TRY(g_ws.wprobs.reserve(sizeof(float) * p.wide_probs_floats));
     if (p.wide_ints) TRY(g_ws.wide.reserve(sizeof(int) * p.wide_ints));
     TRY(ensure_counters());
@@ -1328,6 +1336,7 @@ int workspace_bufs(const MoeHipLayer *L, const FwdPlan &p, FwdBufs *b) {
     b->perm = g_ws.perm.as<int>(); b->h = g_ws.h.as<float>(); b->ys = g_ws.ys.as<float>();
     b->pieces = p.pieces_ints ? g_ws.pieces.as<int>() : nullptr;
     b->gu_part = p.gu_part_floats ? g_ws.gu_part.as<float>() : nullptr;
+    b->order = p.order_ints ? g_ws.order.as<int>() : nullptr;
     b->counters = g_ws.counters.as<int>();
     b->wide.probs = p.wide_probs_floats ? g_ws.wprobs.as<float>() : nullptr;
     b->wide.ints = p.wide_ints ? g_ws.wide.as<int>() : nullptr;
@@ -1358,6 +1367,7 @@ void carve_bufs(const MoeHipLayer *L, const FwdPlan &p, char *base, size_t cap, 
     c.ys = static_cast<float *>(take(sizeof(float) * p.ys_floats));
     c.pieces = p.pieces_ints ? static_cast<int *>(take(sizeof(int) * p.pieces_ints)) : nullptr;
     c.gu_part = p.gu_part_floats ? static_cast<float *>(take(sizeof(float) * p.gu_part_floats)) : nullptr;
+    c.order = p.order_ints ? static_cast<int *>(take(sizeof(int) * p.order_ints)) : nullptr;
     c.wide.probs = p.wide_probs_floats ? static_cast<float *>(take(sizeof(float) * p.wide_probs_floats)) : nullptr;
     c.wide.ints = p.wide_ints ? static_cast<int *>(take(sizeof(int) * p.wide_ints)) : nullptr;
     *need = off;
@@ -1453,6 +1463,13 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
         dn.streamk = p.streamk;
         dn.sk_groups = p.sk_groups;
         dn.pieces = b.pieces;
+        if (b.order) {
+            // The experts' short last m-tiles first: a CU that finishes one of
+            // them mid-round otherwise idles until the in-order dispatch
+            // reaches a workgroup it can take.
+            HIP_TRY(moe::launch_short_first_order(b.offsets, b.tile_off, E, b.order, s));
+            dn.order = b.order;
+        }
         HIP_TRY(moe::launch_gemm_down(dn, s));
         if (g_timing) HIP_TRY(hipEventRecord(g_ev[4], s));
     }

@@ -93,6 +93,9 @@ struct GemmArgs {
     // order and writes H.
     int tail_groups = 0;
     float *tail_part = nullptr;
+    // Whole-tile grid in a given m-tile order (order[i] = the i-th m-tile
+    // to run; launch_short_first_order), or null for m-tile order.
+    const int *order = nullptr;
 };
 
 struct CombineArgs {
@@ -147,6 +150,10 @@ hipError_t launch_gateup_fixup(const GemmArgs &a, hipStream_t s);
 // the pieces' sums go through that mode's epilogue.
 hipError_t launch_tail_fixup(const GemmArgs &a, int mode, hipStream_t s);
 hipError_t launch_gemm_down(const GemmArgs &a, hipStream_t s);
+// order [tile_off[E]] = the experts' short last m-tiles (97 rows or fewer)
+// in expert order, then every other m-tile in m-tile order (one workgroup).
+hipError_t launch_short_first_order(const int *offsets, const int *tile_off, int E, int *order,
+                                    hipStream_t s);
 // The backward's tile epilogues (gemm.hip), no reduction split:
 //   mode 2  gate/up rows gathered like the forward: c = [G | U] per 32-feature
 //           group in the packed column order (ldc = 2F), c2 = H (ldc2 = F);

@@ -399,6 +399,40 @@ def test_gateup_split_tail_layouts_covered():
     assert {0, 2, 3, 4} <= seen
 
 
+def test_down_short_first():
+    """A down projection of at least 4 rounds of 256-column tiles (d 2048,
+    64 experts, a skewed router bias) runs the experts' short last m-tiles
+    first: every token against the oracle, and the routes do give short
+    m-tiles (97 rows or fewer) to reorder."""
+    T, d, F, E, k = 2048, 2048, 64, 64, 4
+    say(f"down short-first: T={T} d={d} F={F} E={E} k={k}")
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(23, 0.02, 0.05)
+    bias = (np.linspace(1.5, -1.5, E) ** 3 * 0.5).astype(np.float32)
+    layer.set_bias(bias)
+    hw = host_layer(d, F, E, k, 23, 0.02, 0.05)
+    x = orc.synth((T, d), 23, 0, 1.0)
+    dx = mh.DeviceArray.from_host(x)
+    dout = mh.DeviceArray((T, d))
+    dprobs = mh.DeviceArray((T, E))
+    dids = mh.DeviceArray((T, k), np.int32)
+    layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+    mh.synchronize()
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw, bias, nthreads=16)
+    ids = dids.to_host()
+    assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+    assert np.array_equal(ids, i_ref)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    m = (counts + 127) // 128
+    short = int(((m > 0) & (counts - 128 * (m - 1) <= 96)).sum())
+    say(f"down short-first: m-tiles {int(m.sum())}, short {short}")
+    # (the library takes the order when its m-tile bound, ceil(T k / 128) + E,
+    # makes at least 4 rounds of 256 workgroups)
+    assert short > 0 and ((T * k + 127) // 128 + E) * (d // 256) >= 4 * 256
+    assert_close(dout.to_host(), o_ref, "down short-first")
+    layer.close()
+
+
 @pytest.mark.parametrize("accumulate", [0, 1])
 def test_forward_large_skewed(accumulate):
     """A large layer (T k = 32768 routed rows), every token against the
