@@ -19,14 +19,15 @@ namespace {
 // directly: no rows are staged and no router launch precedes the kernel.
 // Order of the loads: the rows (DMA) and router rows, a wait for them, the
 // item's first weight group (streaming under the routing), and the second
-// group once the chains are done.  The first workgroup also writes ids, gate
-// weights and probabilities (and, normalising, the normalised rows).
+// group once the chains are done.  At the end workgroup b also writes ids,
+// gate weights and probabilities of tokens b, b + grid, ... (and, when the
+// caller takes them, their normalised rows).
 //
 // LDS: rows [T][KC + 4]; the H block, whose start holds the rms weights
 // until the rows are normalised; the routing results (logits, then
 // probabilities, chosen experts and their probabilities, renormalisation
-// factors), kept to the end, where the first workgroup writes them out; the
-// slot and token lists.
+// factors), kept to the end, where they are written out; the slot and
+// token lists.
 constexpr int kRoutedMaxT = 64;
 constexpr int kRoutedHBlock = kRows * hld<8>();   // floats
 
