@@ -353,7 +353,8 @@ int moe_hip_set_router_path(int mode);
  * counterpart in the reference; for tests and tuning): 1 = router launch and
  * grouped GEMMs, 2 = router launch and the fused decode kernel, 3 = router
  * launch and the two-launch decode, 4 = the fused decode kernel with the
- * routing inside; 0 before any forward. */
+ * routing inside, 5 = router launch and the few-row decode kernel (steps of
+ * at most 4 assignments); 0 before any forward. */
 int moe_hip_last_forward_path(void);
 
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,

@@ -1235,6 +1235,7 @@ struct FwdPlan {
     size_t n = 0;           // T * k assignments
     int max_mtiles = 0;     // grouped GEMM m-tile bound
     bool use_decode = false, fused = false;
+    bool tiny = false;      // a step of at most moe::kTinySlots assignments (decode_tiny.hip)
     int ksplit = 1;         // partial products per slot the combine adds (at most, stream-K)
     int streamk = 0, sk_groups = 0;   // down projection in stream-K form (moe::down_plan)
     size_t h_floats = 0;    // H [n x F] (grouped GEMMs, unfused decode)
@@ -1287,7 +1288,14 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p, bool probs_given) {
     const int fused_splits = F / (16 * moe::decode_fused_waves(d, F));
     const size_t fused_floats = (size_t)fused_splits * n * d;
     p->fused = p->use_decode && g_path != 3 && sizeof(float) * fused_floats <= moe::kFusedPartialBytes;
-    if (p->fused) {
+    // One to a few tokens: their few experts' 16-feature groups spread over
+    // the CUs (the items of the fused kernels would leave most of them idle).
+    p->tiny = p->use_decode && g_path == 0 && moe::decode_tiny_ok((int)n, d, F, E);
+    if (p->tiny) {
+        p->fused = false;
+        p->ksplit = F / 16;
+        p->ys_floats = (size_t)p->ksplit * n * d;
+    } else if (p->fused) {
         p->ksplit = fused_splits;
         p->ys_floats = fused_floats;
     } else if (p->use_decode) {
@@ -1420,9 +1428,18 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
                        b.tile_expert, b.counters, s, !p.use_decode, nm, b.wide));
         if (g_route_mark) HIP_TRY(hipEventRecord(g_route_mark, s));
     }
-    g_last_path = routed ? 4 : !p.use_decode ? 1 : p.fused ? 2 : 3;
+    g_last_path = routed ? 4 : !p.use_decode ? 1 : p.tiny ? 5 : p.fused ? 2 : 3;
     if (routed) {
         // (the expert products ran with the routing)
+    } else if (p.tiny) {
+        moe::DecodeArgs tn{};
+        tn.x = x; tn.ids = ids_d; tn.topk = k; tn.w = L->wgu; tn.w2 = L->wdT; tn.out = b.ys;
+        tn.d = d; tn.F = F; tn.E = E; tn.ksplit = p.ksplit; tn.nslots = (int)n;
+        HIP_TRY(moe::launch_decode_tiny(tn, s));
+        if (g_timing) {
+            HIP_TRY(hipEventRecord(g_ev[3], s));
+            HIP_TRY(hipEventRecord(g_ev[4], s));
+        }
     } else if (p.use_decode) {
         // Fused gate/up + split-K down while its partials stay small, else
         // gate/up then down.

@@ -399,6 +399,47 @@ def test_gateup_split_tail_layouts_covered():
     assert {0, 2, 3, 4} <= seen
 
 
+TINY = [
+    # name, T, d, F, E, k (steps of at most 4 assignments)
+    ("t1_c4", 1, 512, 2048, 16, 2),
+    ("t1_k1", 1, 256, 256, 8, 1),
+    ("t2_c4", 2, 512, 2048, 16, 2),
+    ("t2_d1024", 2, 1024, 512, 8, 2),
+    ("t1_k4_e64", 1, 512, 128, 64, 4),
+    ("t3_k1_f192", 3, 256, 192, 4, 1),
+    ("t2_e2", 2, 256, 64, 2, 2),      # both experts take every token
+    ("t4_k1_e32", 4, 512, 1024, 32, 1),
+]
+
+
+@pytest.mark.parametrize("name,T,d,F,E,k", TINY, ids=[c[0] for c in TINY])
+def test_decode_tiny(name, T, d, F, E, k):
+    """Decode steps of at most four assignments: the few-row kernel (path 5, the
+    used experts' 16-feature groups over the CUs) within the bars of the
+    oracle, routing bit-exact, and as x += MoE through moe_decode_batch."""
+    say(f"tiny decode {name}: T={T} d={d} F={F} E={E} k={k}")
+    layer = mh.Layer(d, F, E, k)
+    layer.fill_synthetic(31, 0.1, 0.02)
+    hw = host_layer(d, F, E, k, 31, 0.1, 0.02)
+    x = orc.synth((T, d), 31, 0, 1.0)
+    try:
+        dx = mh.DeviceArray.from_host(x)
+        dout = mh.DeviceArray((T, d))
+        dprobs = mh.DeviceArray((T, E))
+        dids = mh.DeviceArray((T, k), np.int32)
+        layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+        mh.synchronize()
+        assert mh.last_forward_path() == 5
+        o_ref, p_ref, i_ref = orc.moe_forward(x, hw, nthreads=8)
+        assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+        assert np.array_equal(dids.to_host(), i_ref)
+        assert_close(dout.to_host(), o_ref, f"tiny {name}")
+        base = orc.synth((T, d), 31, 5, 1.0)
+        assert_close(mh.decode_batch(x, base, hw), base + o_ref, f"tiny {name} decode_batch")
+    finally:
+        layer.close()
+
+
 def test_down_short_first():
     """A down projection of at least 4 rounds of 256-column tiles (d 2048,
     64 experts, a skewed router bias) runs the experts' short last m-tiles
