@@ -354,7 +354,8 @@ int moe_hip_set_router_path(int mode);
  * grouped GEMMs, 2 = router launch and the fused decode kernel, 3 = router
  * launch and the two-launch decode, 4 = the fused decode kernel with the
  * routing inside, 5 = router launch and the few-row decode kernel (steps of
- * at most 4 assignments); 0 before any forward. */
+ * at most 4 assignments), 6 = the few-row decode kernel with the routing
+ * inside (at most 8 assignments); 0 before any forward. */
 int moe_hip_last_forward_path(void);
 
 /* Verification hook: y[i] = the device's exp_avx2 lane (which = 0,

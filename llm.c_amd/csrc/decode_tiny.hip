@@ -1,17 +1,18 @@
 // decode_tiny.hip — expert products of decode steps with a few routed rows
-// (a KV-cache step of one or two sequences at top-2: at most kTinySlots = 4
-// assignments), on gfx950.
+// (a KV-cache step of up to four sequences at top-2: at most kTinySlots = 8
+// assignments with the routing inside, kTinyLaunchSlots = 4 after a router
+// launch), on gfx950.
 //
-// With T * k <= 4 only a few experts hold rows, and the item kernels (one
+// With T * k <= 8 only a few experts hold rows, and the item kernels (one
 // workgroup per 128 features of every expert) would leave most CUs idle:
 // two experts' items take 32 of the 256 CUs, so one sequence's step read
 // its 25 MB of weights at ~0.8 TB/s.  Here the work is cut per used expert
 // into 16-feature groups, one workgroup each (the two used experts of a
 // one-token step give 2 x F/16 = 256 workgroups at F = 2048): a workgroup
 // reads the group's gate and up rows (2 x 16 x d floats) and its 16 columns
-// of W_down (d x 16), 96 KB at d = 512, all loads in flight at once.  (At
-// eight assignments, about seven experts, the fused kernel's items read the
-// weights faster than these groups do, so those steps stay with it.)
+// of W_down (d x 16), 96 KB at d = 512, all loads in flight at once.  (After
+// a router launch, eight assignments, about seven experts, ran faster on
+// the fused kernel's items; with the routing inside, on these groups.)
 //   gate/up  thread t: packed row t / 8 (gate rows 0-15, up rows 16-31 of
 //            the group), k chunk t % 8 (d / 8 long, k ascending), one dot
 //            per slot of the expert; the chunks' sums added by a fixed
@@ -23,36 +24,137 @@
 // the bits do not depend on the schedule).  Weights are read from the packed
 // unit layout (gemm.hip): element (row 16 nb + j, k = 16 qb + 4 h + s) of a
 // matrix with K columns sits at ((nb * K / 16) + qb) * 256 + h * 64 + j * 4 + s.
+//
+// ROUTE: every workgroup first routes the step's T <= 8 tokens itself (no
+// router launch, no ids read back): the rows (rms-normalised in place when
+// the FFN norm runs here) stay in LDS and feed the dots; lane (r, c) of wave
+// w runs token c's chain for expert 4 w + r, k ascending, with the router
+// row in VGPRs reaching the lanes by DPP, and eight lanes per token finish
+// (softmax, top-k, renormalisation) — the row-block router's chains and
+// finish (route_rows.h), so probabilities and experts are the same bits.
+// Workgroup t writes token t's ids, gate weights and probabilities.
 #include <algorithm>
 #include <climits>
+#include <utility>
 
 #include "moe_internal.h"
 #include "moe_math.h"
+#include "route_rows.h"
 
 namespace moe {
 namespace {
 
 constexpr int kTinyThreads = 256;
 
+// f(integral_constant<int, S>) for S in the sequence, in order.
+template <class Fn, int... S>
+__device__ inline void tiny_static_for(std::integer_sequence<int, S...>, Fn &&f) {
+    (f(std::integral_constant<int, S>{}), ...);
+}
+
+// The routing of the step's T <= kTinySlots tokens (E <= 16, d = KC): rows
+// to xs (normalised in place with ra.rms_w), then the chains, the finish of
+// eight token rows (rows past T repeat row T - 1; nothing reads them), and
+// token t's results written by workgroup t.  isel / psel: [8][k], invs [8].
+template <int KC>
+__device__ inline void tiny_route(const RouteArgs &ra, float (*xs)[KC + 4], float *lg, int *isel,
+                                  float *psel, float *invs) {
+    constexpr int WV4 = KC / 64, NS = KC / 16;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int T = ra.T, E = ra.E, k = ra.k;
+    const float *src = ra.rms_w ? ra.x_raw : ra.x;
+    for (int i = tid; i < T * (KC / 4); i += kTinyThreads) {
+        const int t = i / (KC / 4), c4 = i - t * (KC / 4);
+        *reinterpret_cast<float4 *>(&xs[t][4 * c4]) =
+            *reinterpret_cast<const float4 *>(src + (size_t)t * KC + 4 * c4);
+    }
+    // Lane (r, c): k = 64 b + 4 c .. 64 b + 4 c + 3 of expert 4 wave + r.
+    const int r = lane >> 4, c = lane & 15;
+    const int ej = min(4 * wave + r, E - 1);
+    float4 w4[WV4];
+    const float *wrow = ra.wrT + (size_t)ej * KC + 4 * c;
+#pragma unroll
+    for (int b = 0; b < WV4; ++b) w4[b] = *reinterpret_cast<const float4 *>(wrow + 64 * b);
+    const float bv = ra.bias ? ra.bias[ej] : 0.0f;
+    __syncthreads();
+    if (ra.rms_w) {
+        // (rms_row16 holds a whole row in registers first, so in place is safe)
+        for (int rr = tid >> 4; rr < T; rr += kTinyThreads / 16) {
+            float *xr = &xs[rr][0];
+            rms_row16([&](int i) { return xr[i]; }, ra.rms_w, KC / 16, ra.rms_eps, ra.rms_rcp,
+                      nullptr, false, xr, false);
+        }
+        __syncthreads();
+    }
+    if (4 * wave < E) {
+        float acc = 0.0f;
+        const float *xrow = &xs[min(c, T - 1)][0];
+        auto xread = [&](float (&xv)[16], int sl) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = *reinterpret_cast<const float4 *>(xrow + 16 * sl + 4 * q);
+                xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
+            }
+        };
+        float xa[16], xb[16];
+        xread(xa, 0);
+        tiny_static_for(std::make_integer_sequence<int, NS / 2>{}, [&](auto sc) {
+            constexpr int SL = 2 * decltype(sc)::value;
+            xread(xb, SL + 1);
+            chain16_dpp4<SL % 4>(acc, w4[SL / 4], xa);
+            if constexpr (SL + 2 < NS) xread(xa, SL + 2);
+            chain16_dpp4<(SL + 1) % 4>(acc, w4[(SL + 1) / 4], xb);
+        });
+        if (c < 8 && 4 * wave + r < E) lg[c * (E + 1) + 4 * wave + r] = ra.bias ? acc + bv : acc;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int ct = tid >> 3, l = tid & 7;
+        const float inv = finish_token8<2>(ra, lg + ct * (E + 1), l, isel + ct * k, psel + ct * k);
+        if (l == 0) invs[ct] = inv;
+    }
+    __syncthreads();
+    for (int ct = blockIdx.x; ct < T; ct += gridDim.x) {
+        if (tid < k) {
+            const int i = ct * k + tid;
+            if (ra.ids) ra.ids[i] = isel[i];
+            if (ra.gw) ra.gw[i] = ftz_f(psel[i] * invs[ct]);
+        }
+        if (ra.probs)
+            for (int ex = tid; ex < E; ex += kTinyThreads) ra.probs[ct * E + ex] = lg[ct * (E + 1) + ex];
+        if (ra.rms_w && ra.xn_out)
+            for (int c4 = tid; c4 < KC / 4; c4 += kTinyThreads)
+                *reinterpret_cast<float4 *>(ra.xn_out + (size_t)ct * KC + 4 * c4) =
+                    *reinterpret_cast<const float4 *>(&xs[ct][4 * c4]);
+    }
+}
+
 // Workgroup b: used expert b / (F / 16) (the ascending list of the experts
-// the ids name), feature group b % (F / 16).  KCH = d / 8.
-template <int KCH>
-__global__ __launch_bounds__(kTinyThreads) void decode_tiny_kernel(DecodeArgs a) {
+// the ids name), feature group b % (F / 16).  KCH = d / 8.  ROUTE: the ids
+// come from the routing above, the rows from LDS.
+template <int KCH, bool ROUTE>
+__global__ __launch_bounds__(kTinyThreads) void decode_tiny_kernel(DecodeArgs a, RouteArgs ra) {
     constexpr int KQ = KCH / 16;              // 16-wide k units per chunk
     constexpr int NCO = 8 * KCH / kTinyThreads;   // output columns per thread (d / 256)
+    constexpr int KC = 8 * KCH;
     __shared__ int uexp[kTinySlots], slot[kTinySlots];
     __shared__ int nu_s, ns_s;
     __shared__ float gu[kTinySlots][32];
     __shared__ float hh[kTinySlots][16];
+    __shared__ __align__(16) float xs[ROUTE ? kTinySlots : 1][KC + 4];
+    __shared__ float lg[ROUTE ? 8 * 17 : 1];
+    __shared__ int isel[ROUTE ? 8 * kTinySlots : 1];
+    __shared__ float psel[ROUTE ? 8 * kTinySlots : 1], invs[8];
     const int tid = threadIdx.x;
     const int n = a.nslots, d = a.d, F = a.F;
     const int nfg = F / 16;
     const int ub = blockIdx.x / nfg, fg = blockIdx.x - ub * nfg;
+    if constexpr (ROUTE) tiny_route<KC>(ra, xs, lg, isel, psel, invs);
     if (tid == 0) {
         // Distinct experts in ascending order, then the expert of this
         // workgroup's slots in slot order (n <= kTinySlots).
         int ids[kTinySlots], nu = 0;
-        for (int i = 0; i < n; ++i) ids[i] = a.ids[i];
+        for (int i = 0; i < n; ++i) ids[i] = ROUTE ? isel[i] : a.ids[i];
         int last = -1;
         for (;;) {
             int next = INT_MAX;
@@ -100,7 +202,8 @@ __global__ __launch_bounds__(kTinyThreads) void decode_tiny_kernel(DecodeArgs a)
     // Dots of the chunk for every slot of the expert (k ascending), then the
     // eight chunks added by a fixed xor tree.
     for (int s = 0; s < ns; ++s) {
-        const float *xr = a.x + (size_t)(slot[s] / a.topk) * d + c * KCH;
+        const int t = slot[s] / a.topk;
+        const float *xr = (ROUTE ? &xs[t][0] : a.x + (size_t)t * d) + c * KCH;
         float acc = 0.0f;
 #pragma unroll
         for (int q = 0; q < KQ; ++q)
@@ -147,14 +250,29 @@ bool decode_tiny_ok(int n, int d, int F, int E) {
            F % 32 == 0 && F / 16 <= kTinyMaxGroups;
 }
 
-hipError_t launch_decode_tiny(const DecodeArgs &a, hipStream_t s) {
+bool decode_tiny_routed_ok(int T, int d, int F, int E, int k) {
+    return T >= 1 && k >= 1 && k <= E && E <= 16 && (d == 256 || d == 512) &&
+           decode_tiny_ok(T * k, d, F, E);
+}
+
+hipError_t launch_decode_tiny(const DecodeArgs &a, const RouteArgs *ra, hipStream_t s) {
     if (!decode_tiny_ok(a.nslots, a.d, a.F, a.E) || !a.w2) return hipErrorInvalidValue;
+    if (ra && (!decode_tiny_routed_ok(ra->T, a.d, a.F, a.E, ra->k) || ra->d != a.d ||
+               ra->E != a.E || ra->k != a.topk || a.nslots != ra->T * ra->k || !ra->wrT ||
+               (ra->rms_w && !ra->x_raw)))
+        return hipErrorInvalidValue;
     const int groups = a.F / 16;
     const dim3 grid((unsigned)(std::min(a.E, a.nslots) * groups));
+    const RouteArgs none{};
+    if (ra) {
+        if (a.d == 256) hipLaunchKernelGGL((decode_tiny_kernel<32, true>), grid, dim3(kTinyThreads), 0, s, a, *ra);
+        else            hipLaunchKernelGGL((decode_tiny_kernel<64, true>), grid, dim3(kTinyThreads), 0, s, a, *ra);
+        return hipGetLastError();
+    }
     switch (a.d) {
-        case 256:  hipLaunchKernelGGL(decode_tiny_kernel<32>, grid, dim3(kTinyThreads), 0, s, a); break;
-        case 512:  hipLaunchKernelGGL(decode_tiny_kernel<64>, grid, dim3(kTinyThreads), 0, s, a); break;
-        default:   hipLaunchKernelGGL(decode_tiny_kernel<128>, grid, dim3(kTinyThreads), 0, s, a); break;
+        case 256:  hipLaunchKernelGGL((decode_tiny_kernel<32, false>), grid, dim3(kTinyThreads), 0, s, a, none); break;
+        case 512:  hipLaunchKernelGGL((decode_tiny_kernel<64, false>), grid, dim3(kTinyThreads), 0, s, a, none); break;
+        default:   hipLaunchKernelGGL((decode_tiny_kernel<128, false>), grid, dim3(kTinyThreads), 0, s, a, none); break;
     }
     return hipGetLastError();
 }

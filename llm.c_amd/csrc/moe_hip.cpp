@@ -1290,7 +1290,10 @@ int plan_forward(const MoeHipLayer *L, int T, FwdPlan *p, bool probs_given) {
     p->fused = p->use_decode && g_path != 3 && sizeof(float) * fused_floats <= moe::kFusedPartialBytes;
     // One to a few tokens: their few experts' 16-feature groups spread over
     // the CUs (the items of the fused kernels would leave most of them idle).
-    p->tiny = p->use_decode && g_path == 0 && moe::decode_tiny_ok((int)n, d, F, E);
+    const bool tiny_inside = g_rpath == 0 && L->wrT && !L->wr_nonfinite &&
+                             moe::decode_tiny_routed_ok(T, d, F, E, k);
+    p->tiny = p->use_decode && g_path == 0 && moe::decode_tiny_ok((int)n, d, F, E) &&
+              (tiny_inside || n <= (size_t)moe::kTinyLaunchSlots);
     if (p->tiny) {
         p->fused = false;
         p->ksplit = F / 16;
@@ -1402,7 +1405,13 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
     // routing bits as the row-block router, no routing launch).
     const bool routed = p.fused && g_rpath == 0 && L->wrT && !L->wr_nonfinite &&
                         moe::decode_routed_ok(T, d, F, E, k);
-    if (routed) {
+    // Steps of at most 4 assignments route inside the few-row kernel.
+    const bool tiny_routed = p.tiny && g_rpath == 0 && L->wrT && !L->wr_nonfinite &&
+                             moe::decode_tiny_routed_ok(T, d, F, E, k);
+    moe::DecodeArgs tn{};
+    tn.x = x; tn.ids = ids_d; tn.topk = k; tn.w = L->wgu; tn.w2 = L->wdT; tn.out = b.ys;
+    tn.d = d; tn.F = F; tn.E = E; tn.ksplit = p.ksplit; tn.nslots = (int)n;
+    if (routed || tiny_routed) {
         moe::RouteArgs ra{x, L->wr, L->bias, T, d, E, k, probs, ids_d, b.gw};
         ra.wrT = L->wrT;
         ra.no_dispatch = 1;
@@ -1417,7 +1426,8 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
         gu.d = d; gu.F = F; gu.E = E; gu.ksplit = 1; gu.nslots = (int)n;
         if (g_timing)
             for (int i = 0; i < 3; ++i) HIP_TRY(hipEventRecord(g_ev[i], s));
-        HIP_TRY(moe::launch_decode_routed(gu, ra, s));
+        if (tiny_routed) HIP_TRY(moe::launch_decode_tiny(tn, &ra, s));
+        else             HIP_TRY(moe::launch_decode_routed(gu, ra, s));
         if (g_route_mark) HIP_TRY(hipEventRecord(g_route_mark, s));
         if (g_timing) {
             HIP_TRY(hipEventRecord(g_ev[3], s));
@@ -1428,14 +1438,11 @@ static int run_forward(MoeHipLayer *L, const float *x, int T, float *out, float 
                        b.tile_expert, b.counters, s, !p.use_decode, nm, b.wide));
         if (g_route_mark) HIP_TRY(hipEventRecord(g_route_mark, s));
     }
-    g_last_path = routed ? 4 : !p.use_decode ? 1 : p.tiny ? 5 : p.fused ? 2 : 3;
-    if (routed) {
+    g_last_path = routed ? 4 : tiny_routed ? 6 : !p.use_decode ? 1 : p.tiny ? 5 : p.fused ? 2 : 3;
+    if (routed || tiny_routed) {
         // (the expert products ran with the routing)
     } else if (p.tiny) {
-        moe::DecodeArgs tn{};
-        tn.x = x; tn.ids = ids_d; tn.topk = k; tn.w = L->wgu; tn.w2 = L->wdT; tn.out = b.ys;
-        tn.d = d; tn.F = F; tn.E = E; tn.ksplit = p.ksplit; tn.nslots = (int)n;
-        HIP_TRY(moe::launch_decode_tiny(tn, s));
+        HIP_TRY(moe::launch_decode_tiny(tn, nullptr, s));
         if (g_timing) {
             HIP_TRY(hipEventRecord(g_ev[3], s));
             HIP_TRY(hipEventRecord(g_ev[4], s));

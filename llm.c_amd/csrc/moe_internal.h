@@ -182,9 +182,14 @@ hipError_t launch_decode_routed(const DecodeArgs &a, const RouteArgs &ra, hipStr
 // used experts' 16-feature groups, one workgroup each, writing split-K
 // partials Yp [F / 16][n][d] (out; w = wgu, w2 = wdT) that the combine adds
 // (ksplit F / 16, at most kTinyMaxGroups).  d of 256, 512 or 1024, F % 32 == 0.
-constexpr int kTinySlots = 4, kTinyMaxGroups = 128;
+// With ra: every workgroup routes the T tokens itself first (E <= 16, d of
+// 256 or 512; ra as for the routed kernel), writing ids, gate weights and
+// probabilities through ra.  Steps after a router launch take it up to
+// kTinyLaunchSlots assignments, with the routing inside up to kTinySlots.
+constexpr int kTinySlots = 8, kTinyLaunchSlots = 4, kTinyMaxGroups = 128;
 bool decode_tiny_ok(int n, int d, int F, int E);
-hipError_t launch_decode_tiny(const DecodeArgs &a, hipStream_t s);
+bool decode_tiny_routed_ok(int T, int d, int F, int E, int k);
+hipError_t launch_decode_tiny(const DecodeArgs &a, const RouteArgs *ra, hipStream_t s);
 // Waves per item of the fused decode kernel (8 when d and F allow, else 4);
 // its split-K partials number F / (16 * waves).
 int decode_fused_waves(int d, int F);

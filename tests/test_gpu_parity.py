@@ -400,8 +400,13 @@ def test_gateup_split_tail_layouts_covered():
 
 
 TINY = [
-    # name, T, d, F, E, k (steps of at most 4 assignments)
+    # name, T, d, F, E, k (steps of at most 8 assignments with the routing
+    # inside, at most 4 after a router launch)
     ("t1_c4", 1, 512, 2048, 16, 2),
+    ("t4_c4", 4, 512, 2048, 16, 2),
+    ("t8_k1", 8, 256, 512, 16, 1),
+    ("t1_k8", 1, 512, 256, 16, 8),
+    ("t2_k4_e5", 2, 256, 128, 5, 4),
     ("t1_k1", 1, 256, 256, 8, 1),
     ("t2_c4", 2, 512, 2048, 16, 2),
     ("t2_d1024", 2, 1024, 512, 8, 2),
@@ -414,10 +419,15 @@ TINY = [
 
 @pytest.mark.parametrize("name,T,d,F,E,k", TINY, ids=[c[0] for c in TINY])
 def test_decode_tiny(name, T, d, F, E, k):
-    """Decode steps of at most four assignments: the few-row kernel (path 5, the
-    used experts' 16-feature groups over the CUs) within the bars of the
-    oracle, routing bit-exact, and as x += MoE through moe_decode_batch."""
+    """Decode steps of at most four assignments: the few-row kernel (the used
+    experts' 16-feature groups over the CUs; path 6 routes inside it for up to
+    16 experts at d 256 or 512, path 5 after a router launch) within the bars
+    of the oracle, routing bit-exact, and as x += MoE through
+    moe_decode_batch.  Where the routing runs inside, the router launch
+    (router path 2) gives the same bits."""
     say(f"tiny decode {name}: T={T} d={d} F={F} E={E} k={k}")
+    inside = E <= 16 and d in (256, 512)
+    assert inside or T * k <= 4
     layer = mh.Layer(d, F, E, k)
     layer.fill_synthetic(31, 0.1, 0.02)
     hw = host_layer(d, F, E, k, 31, 0.1, 0.02)
@@ -429,11 +439,21 @@ def test_decode_tiny(name, T, d, F, E, k):
         dids = mh.DeviceArray((T, k), np.int32)
         layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
         mh.synchronize()
-        assert mh.last_forward_path() == 5
+        assert mh.last_forward_path() == (6 if inside else 5)
         o_ref, p_ref, i_ref = orc.moe_forward(x, hw, nthreads=8)
         assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
         assert np.array_equal(dids.to_host(), i_ref)
         assert_close(dout.to_host(), o_ref, f"tiny {name}")
+        if inside and T * k <= 4:
+            mh.set_router_path(2)
+            try:
+                dout2 = mh.DeviceArray((T, d))
+                layer.forward_dev(dx.ptr, T, dout2.ptr)
+                mh.synchronize()
+                assert mh.last_forward_path() == 5
+            finally:
+                mh.set_router_path(0)
+            assert np.array_equal(bits(dout2.to_host()), bits(dout.to_host()))
         base = orc.synth((T, d), 31, 5, 1.0)
         assert_close(mh.decode_batch(x, base, hw), base + o_ref, f"tiny {name} decode_batch")
     finally:
@@ -601,10 +621,13 @@ def test_rms_norm_device_bitexact(cols):
     assert nd == 0, f"{nd} of {ref.size} normalised values differ in bits"
 
 
-@pytest.mark.parametrize("name,T", [("c4", 64), ("c2", 512)])
+@pytest.mark.parametrize("name,T", [("c4", 64), ("c2", 512), ("c4", 1), ("c4", 2)],
+                         ids=["c4", "c2", "c4_t1", "c4_t2"])
 def test_ffn_sublayer_dev(name, T):
     """x += MoE(rms_norm(x)) in place on a device-resident residual stream:
-    x_norm bit-exact, routing bit-exact, x within the layer tolerance."""
+    x_norm bit-exact, routing bit-exact, x within the layer tolerance.  One
+    or two tokens take the few-row kernel with the norm and the routing
+    inside (path 6)."""
     c = CONFIGS[name]
     d, F, E, k = c["d"], c["F"], c["E"], c["k"]
     say(f"ffn sublayer {name}: T={T} d={d} F={F} E={E} k={k}")
@@ -619,6 +642,8 @@ def test_ffn_sublayer_dev(name, T):
     dids = mh.DeviceArray((T, k), np.int32)
     layer.ffn_sublayer_dev(dx.ptr, dw.ptr, 1e-5, T, dxn.ptr, dprobs.ptr, dids.ptr)
     mh.synchronize()
+    if T * k <= 4:
+        assert mh.last_forward_path() == 6
     xn_ref = orc.rms_norm(x, w, 1e-5)
     assert np.array_equal(bits(dxn.to_host()), bits(xn_ref))
     o_ref, p_ref, i_ref = orc.moe_forward(xn_ref, hw, nthreads=16)
@@ -649,13 +674,14 @@ def test_block_ffn_dropin_c1():
     assert np.array_equal(bits(x1), bits(x + fo))
 
 
-@pytest.mark.parametrize("path,rpath", [(2, 0), (2, 2), (3, 0), (1, 0)],
-                         ids=["gemv_routed", "gemv", "gemv2", "gemm"])
-def test_graph_replay(path, rpath):
+@pytest.mark.parametrize("path,rpath,T", [(2, 0, 64), (2, 2, 64), (3, 0, 64), (1, 0, 64),
+                                          (0, 0, 2), (0, 2, 2)],
+                         ids=["gemv_routed", "gemv", "gemv2", "gemm", "tiny_routed", "tiny"])
+def test_graph_replay(path, rpath, T):
     """A captured forward (two layers, accumulating) replays to the same bits
     as the eager calls, replay after replay, with eager work and
     synchronisations in between."""
-    T, d, F, E, k = 64, 512, 2048, 16, 2
+    d, F, E, k = 512, 2048, 16, 2
     mh.set_expert_path(path)
     mh.set_router_path(rpath)
     layers = [mh.Layer(d, F, E, k) for _ in range(2)]
@@ -674,6 +700,8 @@ def test_graph_replay(path, rpath):
 
         step()                       # eager; also sizes the workspace
         mh.synchronize()
+        if path == 0:
+            assert mh.last_forward_path() == (6 if rpath == 0 else 5)
         ref = out.to_host()
         ref_ids = [i.to_host() for i in ids]
         with mh.Graph() as g:

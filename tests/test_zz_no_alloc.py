@@ -55,12 +55,13 @@ def assert_same(a, b, what):
 
 
 # (config, first T, second smaller T): the decode layer (skinny fused
-# GEMVs), the small prefill layer (grouped GEMMs) and the batch-8x512 layer
-# (grouped GEMMs with a split down projection).
-CASES = [("c4", 64, 23), ("c1", 256, 97), ("c2", 4096, 1000)]
+# GEMVs), the small prefill layer (grouped GEMMs), the batch-8x512 layer
+# (grouped GEMMs with a split down projection) and the decode layer at
+# four and one sequences (the few-row kernel with the routing inside).
+CASES = [("c4", 64, 23), ("c1", 256, 97), ("c2", 4096, 1000), ("c4", 4, 1)]
 
 
-@pytest.mark.parametrize("cfg,t1,t2", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("cfg,t1,t2", CASES, ids=[f"{c[0]}_t{c[1]}" for c in CASES])
 def test_noalloc_matches_forward_dev(cfg, t1, t2):
     c = CONFIGS[cfg]
     d, F, E, k = c["d"], c["F"], c["E"], c["k"]
