@@ -490,8 +490,8 @@ def cpu_port_threads(mh, st, T=16384, d=2048, F=8192, E=64, k=4, pass_s=2.5, thr
 
 def cpu_decode_baseline(mh, T=64, d=512, F=2048, E=16, k=2, n_layers=8):
     """The reference's moe_forward (oracle/_ref; the oracle port where it
-    was not built) on the 64 decode rows of one layer, one thread as that
-    build runs it, warm-up then the median of 5; decode tokens/s = 64 / (8
+    was not built) on the T decode rows of one layer, one thread as that
+    build runs it, warm-up then the median of 5; decode tokens/s = T / (8
     layers x that time)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import orc
@@ -516,7 +516,8 @@ def cpu_decode_baseline(mh, T=64, d=512, F=2048, E=16, k=2, n_layers=8):
     what = (f"the reference's moe_forward built from its sources ({REF_BUILD})"
             if kind == "reference" else "the oracle port (oracle/Makefile)")
     return dict(value=T / (n_layers * layer_s), unit="tokens/s", cores=1, kind=kind,
-                sample=f"one MoE layer on the 64 decode rows, x{n_layers} layers, warm-up then "
+                sample=f"one MoE layer on the {T} decode row{'s' if T > 1 else ''}, x{n_layers} "
+                       f"layers, warm-up then "
                        f"median of 5 ({layer_s * 1e3:.1f} ms per layer), 1 thread; "
                        f"{cpu_model()}; {what}")
 
@@ -595,7 +596,7 @@ def main():
     log("c3_layer", json.dumps(c3))
     c3s = ffn_stack(mh, args.steps, args.warmup)
     log("c3_stack", json.dumps(c3s))
-    dec = dech = stp = None
+    dec = dech = stp = dec1 = stp1 = None
     if not args.no_decode:
         dec, dst = decode(mh, args.steps, args.warmup)
         log("decode", json.dumps(dec))
@@ -605,7 +606,15 @@ def main():
             L.close()
         stp = decode_step(mh, args.steps, args.warmup)
         log("decode_step", json.dumps(stp))
-    cpu = cpu_all = cpu_dec = None
+        # One sequence (the reference's inference_step shape): the same 8
+        # MoE layers at T=1, then the whole block stack at B=1.
+        dec1, dst1 = decode(mh, args.steps, args.warmup, T=1)
+        log("decode T=1", json.dumps(dec1))
+        for L in dst1["layers"]:
+            L.close()
+        stp1 = decode_step(mh, args.steps, args.warmup, B=1)
+        log("decode_step B=1", json.dumps(stp1))
+    cpu = cpu_all = cpu_dec = cpu_dec1 = None
     if not args.no_cpu:
         cpu = cpu_baseline(mh, st)
         log("cpu", json.dumps(cpu))
@@ -613,6 +622,9 @@ def main():
         log("cpu port, all threads", json.dumps(cpu_all))
         cpu_dec = cpu_decode_baseline(mh)
         log("cpu decode", json.dumps(cpu_dec))
+        if not args.no_decode:
+            cpu_dec1 = cpu_decode_baseline(mh, T=1)
+            log("cpu decode T=1", json.dumps(cpu_dec1))
 
     ms = pre["ms"]
     gu_tflops = pre["gateup_tflops"]
@@ -711,6 +723,25 @@ def main():
             "attn_ms_per_layer": stp["attn_ms_per_layer"], "attn_gbs": stp["attn_gbs"],
             "attn_hbm_frac": stp["attn_gbs"] / PEAK_HBM_GBS,
             "moe_ms_per_layer": stp["moe_ms_per_layer"],
+        }
+    if dec1:
+        line["decode_single_seq"] = {
+            "workload": "1 seq x 1 token, the same 8 MoE layers (d=512 d_ff=2048 E=16 top-2): "
+                        "the few-row expert kernel with the routing inside",
+            "tokens_per_s": dec1["tokens_per_s"], "ms_per_step": dec1["ms_per_step"],
+            "graph_ms_per_step": dec1["graph_ms_per_step"],
+            "device_ms_per_layer": dec1["device_ms_per_layer"],
+            "hbm_gbs": dec1["hbm_gbs_layer"], "hbm_frac": dec1["hbm_gbs_layer"] / PEAK_HBM_GBS,
+            "cpu_baseline": cpu_dec1,
+        }
+    if stp1:
+        line["decode_step_single_seq"] = {
+            "workload": "1 seq x 1 token at context 1024, the same 8 blocks (GQA 8/2 attention "
+                        "+ MoE), device-resident x",
+            "tokens_per_s": stp1["tokens_per_s"], "ms_per_step": stp1["ms_per_step"],
+            "graph_ms_per_step": stp1["graph_ms_per_step"],
+            "attn_ms_per_layer": stp1["attn_ms_per_layer"],
+            "moe_ms_per_layer": stp1["moe_ms_per_layer"],
         }
     print(json.dumps(line), flush=True)
 
