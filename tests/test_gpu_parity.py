@@ -456,6 +456,16 @@ def test_decode_tiny(name, T, d, F, E, k):
             assert np.array_equal(bits(dout2.to_host()), bits(dout.to_host()))
         base = orc.synth((T, d), 31, 5, 1.0)
         assert_close(mh.decode_batch(x, base, hw), base + o_ref, f"tiny {name} decode_batch")
+        # A router bias (mat_mul_add form) strong enough to move the choices.
+        bias = (0.3 * np.random.default_rng(E + T).standard_normal(E)).astype(np.float32)
+        layer.set_bias(bias)
+        layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+        mh.synchronize()
+        assert mh.last_forward_path() == (6 if inside else 5)
+        o_b, p_b, i_b = orc.moe_forward(x, hw, bias, nthreads=8)
+        assert np.array_equal(bits(dprobs.to_host()), bits(p_b))
+        assert np.array_equal(dids.to_host(), i_b)
+        assert_close(dout.to_host(), o_b, f"tiny {name} with bias")
     finally:
         layer.close()
 
