@@ -530,7 +530,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--only", choices=["prefill", "prefill_small", "backward", "decode",
-                                       "decode_step", "c3", "copy"], default=None,
+                                       "decode_step", "decode_single", "c3", "copy"],
+                    default=None,
                     help="run one section only (for profiling); prints its JSON to stderr")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -573,6 +574,10 @@ def main():
         return
     if args.only == "decode_step":
         log("decode_step", json.dumps(decode_step(mh, args.steps, args.warmup)))
+        return
+    if args.only == "decode_single":
+        log("decode T=1", json.dumps(decode(mh, args.steps, args.warmup, T=1)[0]))
+        log("decode_step B=1", json.dumps(decode_step(mh, args.steps, args.warmup, B=1)))
         return
     if args.only == "c3":
         log("c3_layer", json.dumps(layer_bench(mh, args.steps, args.warmup, **c3_shape)))
