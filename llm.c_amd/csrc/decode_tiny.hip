@@ -61,9 +61,9 @@ __device__ inline void tiny_static_for(std::integer_sequence<int, S...>, Fn &&f)
 }
 
 // The routing of the step's T <= kTinySlots tokens (E <= 16, d = KC): rows
-// to xs (normalised in place with ra.rms_w), then the chains, the finish of
-// eight token rows (rows past T repeat row T - 1; nothing reads them), and
-// token t's results written by workgroup t.  isel / psel: [8][k], invs [8].
+// to xs (normalised in place with ra.rms_w), then the chains and the finish
+// of eight token rows (rows past T repeat row T - 1; nothing reads them).
+// isel / psel: [8][k], invs [8].
 template <int KC>
 __device__ inline void tiny_route(const RouteArgs &ra, float (*xs)[KC + 4], float *lg, int *isel,
                                   float *psel, float *invs) {
@@ -122,6 +122,17 @@ __device__ inline void tiny_route(const RouteArgs &ra, float (*xs)[KC + 4], floa
         if (l == 0) invs[ct] = inv;
     }
     __syncthreads();
+}
+
+// Token t's routing results (ids, gate weights, probabilities, normalised
+// rows when the caller takes them), from workgroup t: after its products,
+// so that no barrier waits for these stores.
+template <int KC>
+__device__ inline void tiny_route_results(const RouteArgs &ra, float (*xs)[KC + 4],
+                                          const float *lg, const int *isel, const float *psel,
+                                          const float *invs) {
+    const int tid = threadIdx.x;
+    const int T = ra.T, E = ra.E, k = ra.k;
     for (int ct = blockIdx.x; ct < T; ct += gridDim.x) {
         if (tid < k) {
             const int i = ct * k + tid;
@@ -145,8 +156,8 @@ __global__ __launch_bounds__(kTinyThreads) void decode_tiny_kernel(DecodeArgs a,
     constexpr int KQ = KCH / 16;              // 16-wide k units per chunk
     constexpr int NCO = 8 * KCH / kTinyThreads;   // output columns per thread (d / 256)
     constexpr int KC = 8 * KCH;
-    __shared__ int uexp[kTinySlots], slot[kTinySlots];
-    __shared__ int nu_s, ns_s;
+    __shared__ int slot[kTinySlots];
+    __shared__ int e_s, ns_s;
     __shared__ float gu[kTinySlots][32];
     __shared__ float hh[kTinySlots][16];
     __shared__ __align__(16) float xs[ROUTE ? kTinySlots : 1][KC + 4];
@@ -158,30 +169,48 @@ __global__ __launch_bounds__(kTinyThreads) void decode_tiny_kernel(DecodeArgs a,
     const int nfg = F / 16;
     const int ub = blockIdx.x / nfg, fg = blockIdx.x - ub * nfg;
     if constexpr (ROUTE) tiny_route<KC>(ra, xs, lg, isel, psel, invs);
-    if (tid == 0) {
-        // Distinct experts in ascending order, then the expert of this
-        // workgroup's slots in slot order (n <= kTinySlots).
-        int ids[kTinySlots], nu = 0;
-        for (int i = 0; i < n; ++i) ids[i] = ROUTE ? isel[i] : a.ids[i];
-        int last = -1;
-        for (;;) {
-            int next = INT_MAX;
-            for (int i = 0; i < n; ++i)
-                if (ids[i] > last && ids[i] < next) next = ids[i];
-            if (next == INT_MAX) break;
-            uexp[nu++] = next;
-            last = next;
+    // Wave 0, lane i < n holding assignment i's expert: the distinct experts
+    // in ascending order (rank of each first occurrence among them), this
+    // workgroup's expert (rank ub) and its slots in slot order.
+    if (tid < 64) {
+        int id = INT_MAX;
+        if (tid < n) {
+            if constexpr (ROUTE) id = isel[tid];
+            else                 id = a.ids[tid];
         }
-        nu_s = nu;
-        int ns = 0;
-        if (ub < nu)
-            for (int i = 0; i < n; ++i)
-                if (ids[i] == uexp[ub]) slot[ns++] = i;
-        ns_s = ns;
+        // (every shuffle runs in all 64 lanes: a lane reading an inactive
+        // lane would get 0)
+        bool first = tid < n;
+#pragma unroll
+        for (int j = 0; j < kTinySlots; ++j) {
+            const int idj = __shfl(id, j);
+            if (j < tid && idj == id) first = false;
+        }
+        const unsigned long long fm = __ballot(first);
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < kTinySlots; ++j) {
+            const int idj = __shfl(id, j);
+            if (((fm >> j) & 1ull) && idj < id) ++rank;
+        }
+        const int nu = __popcll(fm);
+        const unsigned long long mine = __ballot(first && rank == ub);
+        const int src = __ffsll((long long)mine) - 1;
+        const int idm = __shfl(id, src < 0 ? 0 : src);
+        const int eb = ub < nu && src >= 0 && idm >= 0 && idm < a.E ? idm : -1;
+        const unsigned long long match = __ballot(tid < n && id == eb);
+        if ((match >> tid) & 1ull) slot[__popcll(match & ((1ull << tid) - 1))] = tid;
+        if (tid == 0) {
+            e_s = eb;
+            ns_s = __popcll(match);
+        }
     }
     __syncthreads();
-    if (ub >= nu_s) return;
-    const int e = uexp[ub], ns = ns_s;
+    if (e_s < 0) {
+        if constexpr (ROUTE) tiny_route_results<KC>(ra, xs, lg, isel, psel, invs);
+        return;
+    }
+    const int e = e_s, ns = ns_s;
     const int f0 = 16 * fg;
 
     // Gate/up: packed row of thread t (gate features f0 .. f0 + 15 at packed
@@ -249,6 +278,7 @@ __global__ __launch_bounds__(kTinyThreads) void decode_tiny_kernel(DecodeArgs a,
             yp[tid + kTinyThreads * i] = y;
         }
     }
+    if constexpr (ROUTE) tiny_route_results<KC>(ra, xs, lg, isel, psel, invs);
 }
 
 }  // namespace
