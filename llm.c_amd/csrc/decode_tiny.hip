@@ -33,7 +33,9 @@
 // row in VGPRs reaching the lanes by DPP, and eight lanes per token finish
 // (softmax, top-k, renormalisation) — the row-block router's chains and
 // finish (route_rows.h), so probabilities and experts are the same bits.
-// Workgroup t writes token t's ids, gate weights and probabilities.
+// Workgroup t writes token t's ids, gate weights and probabilities after
+// its products.  Wave 0 finds the used experts and the workgroup's slots
+// with ballots (lane i: assignment i's expert).
 #include <algorithm>
 #include <climits>
 #include <utility>
