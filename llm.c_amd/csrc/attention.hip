@@ -6,7 +6,8 @@
 // Three launches:
 //   QKV tiles     q, k, v = rms_norm(x) . [W_Q | W_K | W_V]: one 1024-thread
 //                 workgroup per 16 x 16 output tile with the whole reduction
-//                 (proj16_kernel).  rms_norm's row scale 1/rms (:48-60) is
+//                 (proj16_kernel; batches of at most 4 rows: one workgroup
+//                 per output column quad, projv_kernel).  rms_norm's row scale 1/rms (:48-60) is
 //                 taken out of the reduction: tiles multiply x * w_rms, sum
 //                 x^2 on the side, scale by 1/sqrt(ss/d + eps), apply RoPE at
 //                 the sequence's position from the caller's tables (:187-203)
@@ -230,6 +231,108 @@ __global__ __launch_bounds__(1024) void proj16_kernel(AttnArgs a) {
                              : (ocol < a.qd + a.kd ? a.kc : a.vc) +
                                    ((size_t)orow * a.max_seq + p) * a.kd;
     *reinterpret_cast<float4 *>(dst + col) = y;
+}
+
+// Projections of small batches (B <= kPVRows rows): one 256-thread
+// workgroup per output column quad c0 .. c0 + 3 (N / 4 workgroups, where the
+// 16 x 16 tiles would give N / 16 with 15 of 16 rows idle).  Thread t takes
+// k = t, t + 256, ... of the reduction for every row, all its loads issued
+// before the first product; the rows' sums (and QKV's sums of x^2) are added
+// over each wave by DPP and over the four waves through LDS in wave order.
+// Thread b < B then runs proj16's epilogue for row b.
+constexpr int kPVRows = 4;
+template <bool QKV>
+__global__ __launch_bounds__(256) void projv_kernel(AttnArgs a) {
+    constexpr int R = kPVRows, KU = 4;   // rows, k steps per thread per batch of loads
+    const int M = QKV ? a.d : a.qd, N = QKV ? a.qd + 2 * a.kd : a.d;
+    const float *X = QKV ? a.x : a.o;
+    const float *wp = QKV ? a.wqkv_p : a.wo_p;
+    const int c0 = 4 * blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int B = a.B;
+    __shared__ float4 red[4][R];
+    __shared__ float ssr[4][R];
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 acc[R];
+    float ss[R];
+#pragma unroll
+    for (int b = 0; b < R; ++b) { acc[b] = zero; ss[b] = 0.0f; }
+    for (int k0 = 0; k0 < M; k0 += 256 * KU) {
+        float4 wv[KU];
+        float xv[KU][R], wr[KU];
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+            const int k = k0 + tid + 256 * u;
+            const bool in = k < M;
+            const int kr = in ? k : 0;
+            const float *src;
+            if (wp)                      src = wp + ((size_t)(c0 >> 4) * M + kr) * 16 + (c0 & 15);
+            else if (!QKV)               src = a.wo + (size_t)kr * a.d + c0;
+            else if (c0 < a.qd)          src = a.wq + (size_t)kr * a.qd + c0;
+            else if (c0 < a.qd + a.kd)   src = a.wk + (size_t)kr * a.kd + (c0 - a.qd);
+            else                         src = a.wv + (size_t)kr * a.kd + (c0 - a.qd - a.kd);
+            wv[u] = masked4(in, *reinterpret_cast<const float4 *>(src));
+#pragma unroll
+            for (int b = 0; b < R; ++b) {
+                const bool inb = in && b < B;
+                const float v = X[inb ? (size_t)b * M + k : 0];
+                xv[u][b] = inb ? v : 0.0f;
+            }
+            wr[u] = QKV ? (in ? a.rms_w[kr] : 0.0f) : 1.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < KU; ++u)
+#pragma unroll
+            for (int b = 0; b < R; ++b) {
+                const float v = xv[u][b];
+                float xw = v;
+                if (QKV) {
+                    ss[b] = fmaf(v, v, ss[b]);
+                    xw = v * wr[u];
+                }
+                acc[b].x = fmaf(xw, wv[u].x, acc[b].x);
+                acc[b].y = fmaf(xw, wv[u].y, acc[b].y);
+                acc[b].z = fmaf(xw, wv[u].z, acc[b].z);
+                acc[b].w = fmaf(xw, wv[u].w, acc[b].w);
+            }
+    }
+#pragma unroll
+    for (int b = 0; b < R; ++b) {
+        if (b >= B) break;
+        const float4 t = make_float4(wave_sum(acc[b].x), wave_sum(acc[b].y), wave_sum(acc[b].z),
+                                     wave_sum(acc[b].w));
+        const float q = QKV ? wave_sum(ss[b]) : 0.0f;
+        if (lane == 0) {
+            red[wave][b] = t;
+            ssr[wave][b] = q;
+        }
+    }
+    __syncthreads();
+    if (tid >= B) return;
+    const int b = tid;
+    const int p = a.pos[b];
+    if (p < 0 || p >= a.max_seq) return;   // (out of range: left untouched)
+    float4 y = zero;
+    for (int w = 0; w < 4; ++w) y = add4(y, red[w][b]);
+    if (!QKV) {
+        float4 *xo = reinterpret_cast<float4 *>(a.x + (size_t)b * a.d + c0);
+        *xo = add4(*xo, y);
+        return;
+    }
+    const float sq = (ssr[0][b] + ssr[1][b]) + (ssr[2][b] + ssr[3][b]);
+    const float inv = 1.0f / sqrtf(sq / (float)M + a.eps);
+    y = make_float4(y.x * inv, y.y * inv, y.z * inv, y.w * inv);
+    const int col = c0 < a.qd ? c0 : c0 < a.qd + a.kd ? c0 - a.qd : c0 - a.qd - a.kd;
+    if (c0 < a.qd + a.kd) {
+        const int half = a.hd / 2, i0 = (col % a.hd) / 2;
+        const float *cr = a.cos_t + (size_t)p * half + i0, *sr = a.sin_t + (size_t)p * half + i0;
+        rope_pair(y.x, y.y, cr[0], sr[0]);
+        rope_pair(y.z, y.w, cr[1], sr[1]);
+    }
+    float *dst = c0 < a.qd ? a.q + (size_t)b * a.qd
+                           : (c0 < a.qd + a.kd ? a.kc : a.vc) + ((size_t)b * a.max_seq + p) * a.kd;
+    *reinterpret_cast<float4 *>(dst + col) = y;
+    (void)N;
 }
 
 // Merged output of one head at dimension dim from its chunk partials at
@@ -612,7 +715,9 @@ hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) {
     const int nc = a.B * a.nkv * nchunk;
     if (!a.cnt_merge) return hipErrorInvalidValue;
     auto t16 = [](int n) { return (unsigned)((n + kPT - 1) / kPT); };
-    hipLaunchKernelGGL(proj16_kernel<true>, dim3(t16(N), t16(a.B)), dim3(1024), 0, s, a);
+    const bool small = a.B <= kPVRows;
+    if (small) hipLaunchKernelGGL(projv_kernel<true>, dim3((unsigned)(N / 4)), dim3(256), 0, s, a);
+    else       hipLaunchKernelGGL(proj16_kernel<true>, dim3(t16(N), t16(a.B)), dim3(1024), 0, s, a);
     const bool fast = with_fast_shape(a.hd, gqa, [&](auto hd, auto g) {
         hipLaunchKernelGGL((attn_chunk_fast_kernel<decltype(hd)::value, decltype(g)::value>),
                            dim3((unsigned)nc), dim3(256), 0, s, a);
@@ -622,7 +727,8 @@ hipError_t launch_attn_decode(const AttnArgs &a, hipStream_t s) {
         hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((a.B * a.qd + 255) / 256)),
                            dim3(256), 0, s, a);
     }
-    hipLaunchKernelGGL(proj16_kernel<false>, dim3(t16(a.d), t16(a.B)), dim3(1024), 0, s, a);
+    if (small) hipLaunchKernelGGL(projv_kernel<false>, dim3((unsigned)(a.d / 4)), dim3(256), 0, s, a);
+    else       hipLaunchKernelGGL(proj16_kernel<false>, dim3(t16(a.d), t16(a.B)), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 
