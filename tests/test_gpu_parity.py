@@ -607,6 +607,7 @@ def test_decode_batch_c4():
     x_one = x0[:1].copy()
     mh.lib().moe_decode_step(hw.weights, hw.config(1), mh.fptr(np.ascontiguousarray(xn[:1])),
                              mh.fptr(x_one))
+    assert mh.last_forward_path() == 6   # the few-row kernel with the routing inside
     o1, _, _ = orc.moe_forward(xn[:1].copy(), hw)
     assert_close(x_one - x0[:1], o1, "c4 decode step")
 
