@@ -344,7 +344,8 @@ int moe_hip_set_expert_path(int mode);
  * 2 = 16-token row blocks with every expert in one workgroup, in their own
  * launch.  Automatic routes a decode step of up to 64 tokens (up to 16
  * experts, d_model 256 or 512, finite router weights) inside the fused
- * expert kernel, with the row blocks' arithmetic.  The tiles take up to 128
+ * expert kernel, or inside the few-row kernel when the step holds at most 8
+ * assignments, with the row blocks' arithmetic.  The tiles take up to 128
  * experts; with mode 1 a wider layer routes by row blocks.  Process-wide;
  * every choice gives the same bits. */
 int moe_hip_set_router_path(int mode);
