@@ -544,11 +544,12 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs a) {
 
 // The same for many split-K partials (the fused decode kernel writes one per
 // 64 features): G lanes share an output float4, each summing up to 8
-// consecutive partials of a slot in split order; lane 0 adds the G group
+// consecutive partials of a slot in split order (PL: 2 for steps of a few
+// tokens, so that more workgroups share the loads); lane 0 adds the G group
 // sums in a fixed tree order and applies the slot's gate weight.  KS > 0:
 // k = KS at compile time, and every load of the lane (partials, gate
 // weights, the accumulated output) is issued before the first sum.
-template <int G, int KS>
+template <int G, int KS, int PL = 8>
 __global__ __launch_bounds__(256) void combine_groups_kernel(CombineArgs a) {
     constexpr int KB = KS > 0 ? KS : 1;   // slots whose loads go out together
     const int d4 = a.d >> 2;
@@ -556,20 +557,20 @@ __global__ __launch_bounds__(256) void combine_groups_kernel(CombineArgs a) {
     const int g = threadIdx.x % G;
     const bool valid = gid < (size_t)a.T * d4;
     const int t = valid ? (int)(gid / d4) : 0, c4 = valid ? (int)(gid % d4) : 0;
-    const int s0 = 8 * g, s1 = min(s0 + 8, a.ksplit);
+    const int s0 = PL * g, s1 = min(s0 + PL, a.ksplit);
     const int k = KS > 0 ? KS : a.k;
     floatx4 *o = reinterpret_cast<floatx4 *>(a.out + (size_t)t * a.d + 4 * c4);
     floatx4 prev = {0.f, 0.f, 0.f, 0.f};
     if (KS > 0 && a.accumulate && g == 0) prev = *o;
     floatx4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < k; k0 += KB) {
-        floatx4 p[KB][8];
+        floatx4 p[KB][PL];
         float w[KB];
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             const float *yp = a.ys + ((size_t)t * a.k + k0 + kb) * a.d + 4 * c4;
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
+            for (int u = 0; u < PL; ++u)
                 p[kb][u] = *reinterpret_cast<const floatx4 *>(
                     yp + (size_t)min(s0 + u, a.ksplit - 1) * a.split_stride);
             w[kb] = a.gw[(size_t)t * a.k + k0 + kb];
@@ -579,7 +580,7 @@ __global__ __launch_bounds__(256) void combine_groups_kernel(CombineArgs a) {
             floatx4 y = {0.f, 0.f, 0.f, 0.f};
             if (s0 < s1) y = p[kb][0];
 #pragma unroll
-            for (int u = 1; u < 8; ++u)
+            for (int u = 1; u < PL; ++u)
                 if (s0 + u < s1)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) y[j] = y[j] + p[kb][u][j];
@@ -938,6 +939,26 @@ hipError_t launch_gemm_bwd(const GemmArgs &a, int mode, hipStream_t s) {
 hipError_t launch_combine(const CombineArgs &a, hipStream_t s) {
     if (a.pieces && (a.pieces_cols <= 0 || a.pieces_cols % 4 || a.d % a.pieces_cols))
         return hipErrorInvalidValue;
+    if (!a.pieces && a.T <= 8 && a.ksplit > 8 && a.ksplit <= 128) {
+        // A few tokens: two partials per lane, up to 64 lanes per output.
+        const int groups = (a.ksplit + 1) / 2;
+        const size_t n = (size_t)a.T * (a.d >> 2);
+        if (n == 0) return hipSuccess;
+        auto go = [&](auto kern, int G) {
+            hipLaunchKernelGGL(kern, dim3((unsigned)((n * G + 255) / 256)), dim3(256), 0, s, a);
+        };
+        auto by_k = [&](auto gc) {
+            constexpr int G = decltype(gc)::value;
+            if (a.k == 1)      go(combine_groups_kernel<G, 1, 2>, G);
+            else if (a.k == 2) go(combine_groups_kernel<G, 2, 2>, G);
+            else               go(combine_groups_kernel<G, 0, 2>, G);
+        };
+        if (groups <= 8)       by_k(std::integral_constant<int, 8>{});
+        else if (groups <= 16) by_k(std::integral_constant<int, 16>{});
+        else if (groups <= 32) by_k(std::integral_constant<int, 32>{});
+        else                   by_k(std::integral_constant<int, 64>{});
+        return hipGetLastError();
+    }
     if (!a.pieces && a.ksplit > 8 && a.ksplit <= 128) {
         const int groups = (a.ksplit + 7) / 8;
         const size_t n = (size_t)a.T * (a.d >> 2);
