@@ -168,8 +168,9 @@ def test_attn_decode_device(shape):
 @pytest.mark.gpu
 def test_attn_decode_repeatable_and_batch_sizes():
     """The same bits on a repeat (the merge counters are back at zero) and at
-    other batch sizes (ragged row tiles)."""
-    for B in (1, 33, 64, 70):
+    other batch sizes (ragged row tiles; up to 4 rows, the projections take
+    one workgroup per output column quad)."""
+    for B in (1, 2, 4, 5, 33, 64, 70):
         pos = np.arange(B, dtype=np.int32) * 7 % 200
         x, w, kc, vc, pos, c, s = make_case(B, 200, pos, 8)
         a1 = run_device(x, w, kc, vc, pos, c, s)
