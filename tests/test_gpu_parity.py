@@ -470,6 +470,43 @@ def test_decode_tiny(name, T, d, F, E, k):
         layer.close()
 
 
+@pytest.mark.parametrize("k", [1, 2])
+def test_decode_tiny_guess_differs(k):
+    """A step whose logits' top-k differs from the probabilities': logits 0
+    and 2^-30 round to the same probability, and the reference takes the
+    lower index (expert 0) where the larger logit is expert 1 (k = 1:
+    another expert; k = 2: the same experts in another order).  The few-row
+    kernel with the routing inside chooses on the rounded probabilities as
+    the reference does: routing bit-exact, outputs within the bars."""
+    T, d, F, E = 1, 256, 256, 4
+    wr = np.zeros((d, E), np.float32)
+    wr[0] = [0.0, 2.0 ** -30, -1.0, -1.0]     # only x[0] reaches the logits
+    rng = np.random.default_rng(3)
+    g = (0.05 * rng.standard_normal((E, d, F))).astype(np.float32)
+    u = (0.05 * rng.standard_normal((E, d, F))).astype(np.float32)
+    dn = (0.05 * rng.standard_normal((E, F, d))).astype(np.float32)
+    hw = HostMoE(wr, g, u, dn, k)
+    x = rng.standard_normal((T, d)).astype(np.float32)
+    x[0, 0] = 1.0
+    o_ref, p_ref, i_ref = orc.moe_forward(x, hw)
+    assert bits(p_ref)[0, 0] == bits(p_ref)[0, 1] and i_ref[0, 0] == 0   # the tie this case needs
+    layer = mh.Layer(d, F, E, k)
+    try:
+        layer.load(hw)
+        dx = mh.DeviceArray.from_host(x)
+        dout = mh.DeviceArray((T, d))
+        dprobs = mh.DeviceArray((T, E))
+        dids = mh.DeviceArray((T, k), np.int32)
+        layer.forward_dev(dx.ptr, T, dout.ptr, dprobs.ptr, dids.ptr)
+        mh.synchronize()
+        assert mh.last_forward_path() == 6
+        assert np.array_equal(bits(dprobs.to_host()), bits(p_ref))
+        assert np.array_equal(dids.to_host(), i_ref)
+        assert_close(dout.to_host(), o_ref, f"guess differs k={k}")
+    finally:
+        layer.close()
+
+
 def test_down_short_first():
     """A down projection of at least 4 rounds of 256-column tiles (d 2048,
     64 experts, a skewed router bias) runs the experts' short last m-tiles
