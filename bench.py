@@ -601,7 +601,7 @@ def main():
     log("c3_layer", json.dumps(c3))
     c3s = ffn_stack(mh, args.steps, args.warmup)
     log("c3_stack", json.dumps(c3s))
-    dec = dech = stp = dec1 = stp1 = None
+    dec = dech = stp = dec1 = dech1 = stp1 = None
     if not args.no_decode:
         dec, dst = decode(mh, args.steps, args.warmup)
         log("decode", json.dumps(dec))
@@ -615,6 +615,8 @@ def main():
         # MoE layers at T=1, then the whole block stack at B=1.
         dec1, dst1 = decode(mh, args.steps, args.warmup, T=1)
         log("decode T=1", json.dumps(dec1))
+        dech1 = decode_host_dropin(mh, dst1, T=1)
+        log("decode_host_dropin T=1", json.dumps(dech1))
         for L in dst1["layers"]:
             L.close()
         stp1 = decode_step(mh, args.steps, args.warmup, B=1)
@@ -738,6 +740,13 @@ def main():
             "device_ms_per_layer": dec1["device_ms_per_layer"],
             "hbm_gbs": dec1["hbm_gbs_layer"], "hbm_frac": dec1["hbm_gbs_layer"] / PEAK_HBM_GBS,
             "cpu_baseline": cpu_dec1,
+        }
+    if dech1:
+        line["decode_single_seq_host_dropin"] = {
+            "workload": "the same 8 layers through moe_decode_batch with one row (moe_decode_step, "
+                        "the inference_step slot), host x_norm and x, synchronous calls",
+            "tokens_per_s": dech1["tokens_per_s"], "ms_per_step": dech1["ms_per_step"],
+            "us_per_call": dech1["ms_per_step"] * 1e3 / dech1["layers"],
         }
     if stp1:
         line["decode_step_single_seq"] = {
